@@ -1,0 +1,186 @@
+/*
+ * vfk.h — C ABI of libvfk, the MI355X (gfx950) encoder-attention kernels.
+ *
+ * Every GPU entry point:
+ *   - takes raw device pointers plus element strides (never torch types),
+ *   - enqueues its kernels on the caller's `stream` (a hipStream_t; NULL = the
+ *     legacy default stream) and never synchronises it,
+ *   - allocates nothing: outputs are provided by the caller,
+ *   - returns VFK_OK (0) on success, a negative VFK_ERR_* code for a rejected
+ *     argument (message in vfk_last_error()), or a positive hipError_t value
+ *     when the HIP launch itself failed.
+ * The library keeps no mutable global state besides the thread-local error
+ * message, so concurrent calls from several host threads are safe.
+ *
+ * Strides are in elements. A stride of 0 broadcasts that dimension.
+ */
+#ifndef VFK_H
+#define VFK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+#define VFK_F32 0
+#define VFK_BF16 1
+#define VFK_F16 2
+
+/* status codes */
+#define VFK_OK 0
+#define VFK_ERR_INVALID (-1)     /* shape / pointer / stride rejected      */
+#define VFK_ERR_UNSUPPORTED (-2) /* valid request this build does not run  */
+
+/* activation codes for vfk_glu_fwd */
+#define VFK_ACT_GELU_ERF 0   /* 0.5 x (1 + erf(x / sqrt 2))                     */
+#define VFK_ACT_GELU_TANH 1  /* 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) */
+#define VFK_ACT_SILU 2       /* x * sigmoid(x)                                  */
+#define VFK_ACT_RELU 3       /* max(x, 0)                                       */
+
+/* A strided tensor of up to 4 dimensions. Unused trailing dims: size 1. */
+typedef struct vfk_tensor {
+  void* data;
+  int32_t dtype;       /* VFK_F32 / VFK_BF16 / VFK_F16 */
+  int32_t ndim;
+  int64_t size[4];
+  int64_t stride[4];   /* in elements */
+} vfk_tensor;
+
+/* ------------------------------------------------------------------------ */
+/* Library information and host-side helpers (no GPU needed)                  */
+/* ------------------------------------------------------------------------ */
+
+/* ABI version; bumped on any signature change. */
+int vfk_abi_version(void);
+
+/* Message of the last error raised on this host thread ("" if none). */
+const char* vfk_last_error(void);
+
+/* T5 relative-position bucket of each relative position rel[i] = key - query,
+ * evaluated with the fp32 formula of
+ * models/mt5/mt5_encoder.py:124-148 (T5RelativePositionBias._relative_position_bucket)
+ * and its Triton twin kernels/flash_attention_rpb.py:12-54. Host only. */
+int vfk_t5_bucket(const int64_t* rel, int32_t* out, int64_t n,
+                  int32_t bidirectional, int32_t num_buckets,
+                  int32_t max_distance);
+
+/* DeBERTa-v2 log bucket of each relative position rel[i] = query - key,
+ * following models/deberta_v2/deberta_v2_encoder.py:70-89
+ * (make_log_bucket_position). Host only. */
+int vfk_deberta_bucket(const int64_t* rel, int32_t* out, int64_t n,
+                       int32_t bucket_size, int32_t max_position);
+
+/* ------------------------------------------------------------------------ */
+/* Attention                                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* T5 relative-position-bias flash attention, forward.
+ * Replaces kernels/flash_attention_rpb.py:296-412 (flash_attention_rpb_final)
+ * and the Triton kernel at :61-230.
+ *   q [B,H,Lq,D], k/v [B,H,Lk,D], out [B,H,Lq,D]   (any strides, D == 64)
+ *   rpb_table [num_table_buckets, H] or data == NULL (no bias)
+ *   mask: additive mask broadcastable to [B,H,Lq,Lk] or data == NULL
+ *   is_decoder != 0: causal + unidirectional buckets.
+ * out = softmax(q k^T * softmax_scale + table[bucket(k - q), h] + mask) v */
+int vfk_flash_rpb_fwd(const vfk_tensor* q, const vfk_tensor* k,
+                      const vfk_tensor* v, const vfk_tensor* rpb_table,
+                      int32_t num_buckets, int32_t max_distance,
+                      int32_t is_decoder, const vfk_tensor* mask,
+                      float softmax_scale, vfk_tensor* out, void* stream);
+
+/* DeBERTa-v2/v3 disentangled flash attention, forward, gathering the bias
+ * from precomputed position projections (the reference's interface).
+ * Replaces kernels/flash_deberta_attention.py:455-499 (flash_deberta_attention)
+ * and the Triton kernel at :144-299.
+ *   q [B,H,M,D], k/v [B,H,N,D], out [B,H,M,D] (D == 64)
+ *   pos_key [B,H,M,2*att_span] or NULL, pos_query [B,H,N,2*att_span] or NULL
+ *   seq_lengths: device int32 [B] or NULL (= all N keys valid)
+ * Rows >= seq_lengths[b] of out are written as zeros. */
+int vfk_flash_deberta_fwd(const vfk_tensor* q, const vfk_tensor* k,
+                          const vfk_tensor* v, const int32_t* seq_lengths,
+                          const vfk_tensor* pos_key,
+                          const vfk_tensor* pos_query, int32_t causal,
+                          float sm_scale, int32_t position_buckets,
+                          int32_t max_relative_distance,
+                          int32_t use_log_bucket, vfk_tensor* out,
+                          void* stream);
+
+/* DeBERTa disentangled attention with the position projections computed in
+ * the kernel (no counterpart in the reference; it replaces the two
+ * [B,H,L,2S] matmuls at models/deberta_v2/deberta_v2_encoder.py:275-286
+ * followed by flash_deberta_attention).
+ *   key_rel   [H, 2*att_span, D]  = key_proj(rel_emb) per head   (c2p) or NULL
+ *   query_rel [H, 2*att_span, D]  = query_proj(rel_emb) per head (p2c) or NULL
+ * score(i,j) = (q_i.k_j + q_i.key_rel[c(i-j)] + k_j.query_rel[c(i-j)]) * sm_scale
+ * with c(d) = clamp(bucket(d) + att_span, 0, 2*att_span - 1). */
+int vfk_deberta_fused_fwd(const vfk_tensor* q, const vfk_tensor* k,
+                          const vfk_tensor* v, const int32_t* seq_lengths,
+                          const vfk_tensor* key_rel,
+                          const vfk_tensor* query_rel, float sm_scale,
+                          int32_t position_buckets,
+                          int32_t max_relative_distance,
+                          int32_t use_log_bucket, vfk_tensor* out,
+                          void* stream);
+
+/* Varlen (packed) bidirectional attention with optional in-kernel RoPE and
+ * sliding window, for ModernBERT (no counterpart kernel in the reference: it
+ * replaces F.scaled_dot_product_attention with the dense O(T^2) masks at
+ * models/modernbert/modernbert_encoder.py:236-255 and :491-550).
+ *   q/k/v [T,H,D] (any strides, D == 64), out [T,H,D]
+ *   cu_seqlens: device int32 [num_seqs + 1]; token t of sequence s has
+ *     position t - cu_seqlens[s]
+ *   max_seqlen: upper bound of the sequence lengths (sizes the grid)
+ *   window < 0: global; window >= 0: key j visible iff |i - j| <= window
+ *   rope_theta > 0: rotate q and k (non-interleaved halves) in the kernel
+ *   key_valid: device uint8 [T] (0 = key masked) or NULL */
+int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
+                        const vfk_tensor* v, const int32_t* cu_seqlens,
+                        int32_t num_seqs, int32_t max_seqlen, int32_t window,
+                        float rope_theta, const uint8_t* key_valid,
+                        float softmax_scale, vfk_tensor* out, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Memory-bound epilogues                                                    */
+/* ------------------------------------------------------------------------ */
+
+/* RoPE with a cos/sin table. Replaces kernels/fused_rope_global.py:18-142
+ * (_fused_rope_kernel / fused_rope_apply).
+ *   x, out [B,S,H,D]; cos, sin [B,S,D] (stride 0 broadcasts)
+ * out[..d] = x[d] cos[d] - x[d+D/2] sin[d]        (d <  D/2)
+ *          = x[d] cos[d] + x[d-D/2] sin[d]        (d >= D/2)            */
+int vfk_rope_fwd(const vfk_tensor* x, const vfk_tensor* cos,
+                 const vfk_tensor* sin, vfk_tensor* out, void* stream);
+
+/* LayerNorm over the last dim. Replaces kernels/fused_layernorm.py:19-274.
+ *   x, out [rows, n] (row stride, unit column stride); weight/bias [n] or
+ *   NULL; optional residual [rows, n]: x := x + residual first, and the sum
+ *   is written to residual_out when that is not NULL. */
+int vfk_layernorm_fwd(const vfk_tensor* x, const vfk_tensor* residual,
+                      const vfk_tensor* weight, const vfk_tensor* bias,
+                      float eps, vfk_tensor* out, vfk_tensor* residual_out,
+                      void* stream);
+
+/* RMSNorm (T5 / vLLM RMSNorm used at models/mt5/mt5_encoder.py:41,461,471,519):
+ * out = x * rsqrt(mean(x^2) + eps) * weight, statistics in fp32. Same
+ * residual convention as vfk_layernorm_fwd. */
+int vfk_rmsnorm_fwd(const vfk_tensor* x, const vfk_tensor* residual,
+                    const vfk_tensor* weight, float eps, vfk_tensor* out,
+                    vfk_tensor* residual_out, void* stream);
+
+/* Gated activation out = act(a) * b over [rows, n] (row strides).
+ * Replaces kernels/fused_glu_mlp.py:23-104 (act on the first operand) and
+ * kernels/ff_fused.py:24-125 (act on `gate`). */
+int vfk_glu_fwd(int32_t act, const vfk_tensor* a, const vfk_tensor* b,
+                vfk_tensor* out, void* stream);
+
+/* out = a + b, elementwise over [rows, n] (row strides).
+ * Replaces kernels/fused_dropout_residual.py:10-104 in inference mode. */
+int vfk_residual_add(const vfk_tensor* a, const vfk_tensor* b,
+                     vfk_tensor* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VFK_H */

@@ -1,0 +1,143 @@
+"""GPU parity of the memory-bound epilogues against the oracle (fp32, CPU)."""
+import pytest
+import torch
+
+from _tol import assert_elem_close
+from oracle import epilogues as oe
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+
+def _rand(shape, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(4096, 768), (333, 1024), (17, 1000), (5, 8192), (64, 24)])
+@pytest.mark.parametrize("affine", ["none", "w", "wb"])
+def test_layernorm(dev, dtype, shape, affine):
+    from kernels.fused_layernorm import FusedLayerNorm, fused_layernorm
+    x = _rand(shape, dtype, 1)
+    n = shape[-1]
+    w = _rand((n,), dtype, 2) if affine != "none" else None
+    b = _rand((n,), dtype, 3) if affine == "wb" else None
+    want = oe.layernorm(x, w, b, 1e-5)
+    got = fused_layernorm(x.to(dev), n, None if w is None else w.to(dev),
+                          None if b is None else b.to(dev), 1e-5)
+    assert_elem_close(got, want, dtype, f"layernorm {shape} {affine}")
+    if affine == "wb":
+        mod = FusedLayerNorm(n, eps=1e-5, dtype=dtype, device=dev)
+        with torch.no_grad():
+            mod.weight.copy_(w)
+            mod.bias.copy_(b)
+        assert_elem_close(mod(x.to(dev)), want, dtype, "FusedLayerNorm module")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_layernorm_residual_fused(dev, dtype):
+    from kernels.fused_layernorm import fused_add_layernorm
+    x = _rand((1000, 768), dtype, 4)
+    r = _rand((1000, 768), dtype, 5)
+    w = _rand((768,), dtype, 6)
+    y, s = fused_add_layernorm(x.to(dev), r.to(dev), w.to(dev), None, 1e-5)
+    ssum = (x.float() + r.float())
+    assert_elem_close(s, ssum, dtype, "residual sum")
+    # the norm sees the sum as computed (rounded to dtype when stored)
+    assert_elem_close(y, oe.layernorm(ssum, w, None, 1e-5), dtype, "add+LN")
+
+
+def test_layernorm_state_dict_compat(dev):
+    from kernels.fused_layernorm import FusedLayerNorm
+    ref = torch.nn.LayerNorm(768, eps=1e-5, bias=False)
+    mod = FusedLayerNorm(768, eps=1e-5, bias=False)
+    mod.load_state_dict(ref.state_dict())
+    assert set(mod.state_dict()) == {"weight"}
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(2048, 1024), (7, 1000)])
+def test_rmsnorm(dev, dtype, shape):
+    from kernels.rms_norm import RMSNorm
+    x = _rand(shape, dtype, 7)
+    mod = RMSNorm(shape[-1], eps=1e-6, dtype=dtype, device=dev)
+    w = _rand((shape[-1],), dtype, 8)
+    with torch.no_grad():
+        mod.weight.copy_(w)
+    assert_elem_close(mod(x.to(dev)), oe.rmsnorm(x, w, 1e-6), dtype, "rmsnorm")
+    r = _rand(shape, dtype, 9)
+    y, s = mod(x.to(dev), r.to(dev))
+    assert_elem_close(y, oe.rmsnorm(x.float() + r.float(), w, 1e-6), dtype, "add+rms")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("act", ["gelu", "gelu_pytorch_tanh", "silu"])
+def test_glu_chunked(dev, dtype, act):
+    """ModernBERT MLP: act(input) * gate on the two chunk() halves of Wi's output."""
+    from kernels.fused_glu_mlp import fused_gelu_mul_dropout
+    x = _rand((1500, 2 * 1152), dtype, 10, 2.0).to(dev)
+    a, b = x.chunk(2, dim=-1)
+    got = fused_gelu_mul_dropout(a, b, act_fn=act)
+    name = {"gelu": "gelu_erf", "gelu_pytorch_tanh": "gelu_tanh", "silu": "silu"}[act]
+    want = oe.glu(a.cpu(), b.cpu(), name)
+    assert_elem_close(got, want, dtype, f"glu {act}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("act", ["gelu", "gelu_new", "gelu_accurate", "relu", "silu"])
+def test_ff_fused(dev, dtype, act):
+    from kernels.ff_fused import fused_gelu_mul_dropout
+    gate = _rand((3, 77, 2816), dtype, 11, 2.0)
+    up = _rand((3, 77, 2816), dtype, 12)
+    got = fused_gelu_mul_dropout(gate.to(dev), up.to(dev), act_fn=act)
+    assert got.shape == gate.shape
+    name = {"gelu": "gelu_tanh", "gelu_new": "gelu_tanh", "gelu_accurate": "gelu_erf",
+            "relu": "relu", "silu": "silu"}[act]
+    assert_elem_close(got, oe.glu(gate, up, name), dtype, f"ff_fused {act}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_residual(dev, dtype):
+    from kernels.fused_dropout_residual import fused_dropout_residual
+    x = _rand((1, 4001, 768), dtype, 13)
+    r = _rand((1, 4001, 768), dtype, 14)
+    got = fused_dropout_residual(x.to(dev), r.to(dev), 0.1, training=False)
+    assert_elem_close(got, oe.residual_add(x, r), dtype, "residual")
+    # odd sizes take the scalar path
+    x2, r2 = _rand((3, 5), dtype, 15), _rand((3, 5), dtype, 16)
+    assert_elem_close(fused_dropout_residual(x2.to(dev), r2.to(dev)), oe.residual_add(x2, r2),
+                      dtype, "residual odd")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("cos_rank", [3, 4])
+def test_rope_table(dev, dtype, cos_rank):
+    from kernels.fused_rope_global import fused_rope_global_apply
+    from kernels.fused_rope_local import fused_rope_local_apply
+    from oracle.attention import rope_cos_sin
+    B, S, H, D = 2, 300, 12, 64
+    q = _rand((B, S, H, D), dtype, 17)
+    k = _rand((B, S, H, D), dtype, 18)
+    cos, sin = rope_cos_sin(torch.arange(S), 160000.0, D)
+    cos = cos.to(dtype)[None].expand(B, S, D)
+    sin = sin.to(dtype)[None].expand(B, S, D)
+    if cos_rank == 4:
+        cos, sin = cos[:, None], sin[:, None]
+    for fn in (fused_rope_global_apply, fused_rope_local_apply):
+        gq, gk = fn(q.to(dev), k.to(dev), cos.to(dev), sin.to(dev))
+        assert_elem_close(gq, oe.rope_table(q, cos, sin), dtype, "rope q")
+        assert_elem_close(gk, oe.rope_table(k, cos, sin), dtype, "rope k")
+
+
+def test_rope_strided_qkv_view(dev):
+    """q/k as strided views of a fused [B,S,3,H,D] projection (no copies)."""
+    from kernels.fused_rope_global import fused_rope_apply
+    from oracle.attention import rope_cos_sin
+    qkv = _rand((1, 500, 3, 12, 64), torch.bfloat16, 19)
+    q = qkv[:, :, 0]
+    cos, sin = rope_cos_sin(torch.arange(500), 10000.0, 64)
+    cos, sin = cos.bfloat16()[None], sin.bfloat16()[None]
+    got = fused_rope_apply(qkv.to(dev)[:, :, 0], cos.to(dev), sin.to(dev))
+    assert_elem_close(got, oe.rope_table(q, cos, sin), torch.bfloat16, "rope view")

@@ -1,0 +1,148 @@
+"""GPU parity of T5 relative-position-bias attention (flash_attention_rpb_final)
+against the oracle restatement of the reference's eager path."""
+import pytest
+import torch
+
+import workloads
+from _tol import assert_attn_close
+from oracle import attention as oa
+from oracle import buckets as ob
+
+pytestmark = pytest.mark.gpu
+
+
+def _rpb():
+    from kernels.flash_attention_rpb import flash_attention_rpb_final
+    return flash_attention_rpb_final
+
+
+def test_config1_fp32(dev):
+    """Config 1 (the CPU plumbing check) on the GPU in fp32."""
+    c = workloads.config1()
+    want = oa.rpb_attention(c.q, c.k, c.v, c.table, 32, 128, False, c.mask, 1.0)
+    got = _rpb()(c.q.to(dev), c.k.to(dev), c.v.to(dev), c.table.to(dev), 32, 128, False,
+                 padding_mask=c.mask.to(dev), softmax_scale=1.0)
+    assert got.dtype == torch.float32 and got.shape == c.q.shape
+    assert_attn_close(got, want, "cfg1 fp32", max_abs=1e-4, cos=0.999999)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_config1_16bit(dev, dtype):
+    c = workloads.config1()
+    q, k, v = (t.to(dtype) for t in (c.q, c.k, c.v))
+    mask = c.mask.clamp(min=torch.finfo(dtype).min).to(dtype)
+    want = oa.rpb_attention(q, k, v, c.table, 32, 128, False, mask, 1.0)
+    got = _rpb()(q.to(dev), k.to(dev), v.to(dev), c.table.to(dev), 32, 128, False,
+                 padding_mask=mask.to(dev))
+    assert got.dtype == dtype
+    assert_attn_close(got, want, f"cfg1 {dtype}")
+
+
+def test_config4_attention_subset(dev):
+    """mT5-large shapes: 4 of the 32 sequences at L=768 against the oracle."""
+    g = torch.Generator().manual_seed(4)
+    B, H, L = 4, 16, 768
+    lengths = torch.tensor([768, 512, 700, 601])
+    q, k, v = (torch.randn(B, H, L, 64, generator=g) * 0.64 for _ in range(3))
+    q, k, v = (t.bfloat16() for t in (q, k, v))
+    table = (torch.randn(32, H, generator=g) * 0.1).bfloat16()
+    keep = (torch.arange(L)[None] < lengths[:, None]).bfloat16()
+    mask = ((1.0 - keep) * torch.finfo(torch.bfloat16).min)[:, None, None, :]
+    want = oa.rpb_attention(q, k, v, table, 32, 128, False, mask, 1.0)
+    got = _rpb()(q.to(dev), k.to(dev), v.to(dev), table.to(dev), 32, 128, False,
+                 padding_mask=mask.to(dev))
+    for b in range(B):
+        n = int(lengths[b])
+        assert_attn_close(got[b, :, :n], want[b, :, :n], f"cfg4 batch {b}")
+
+
+def test_config4_full_size_properties(dev):
+    """All 32 x 768 rows at full size: V = 1 gives 1 on every row, and a
+    batch permutation permutes the output (size-independent checks)."""
+    c = workloads.config4(device=dev)
+    B, L = c.hidden.shape[:2]
+    g = torch.Generator().manual_seed(44)
+    q = (torch.randn(B, 16, L, 64, generator=g) * 0.64).bfloat16().to(dev)
+    k = (torch.randn(B, 16, L, 64, generator=g) * 0.64).bfloat16().to(dev)
+    ones = torch.ones(B, 16, L, 64, dtype=torch.bfloat16, device=dev)
+    out = _rpb()(q, k, ones, c.table, 32, 128, False, padding_mask=c.mask)
+    assert torch.allclose(out.float(), torch.ones_like(out, dtype=torch.float32), atol=1e-2)
+    v = torch.randn(B, 16, L, 64, generator=g).bfloat16().to(dev)
+    o1 = _rpb()(q, k, v, c.table, 32, 128, False, padding_mask=c.mask)
+    perm = torch.randperm(B, generator=g).to(dev)
+    o2 = _rpb()(q[perm], k[perm], v[perm], c.table, 32, 128, False, padding_mask=c.mask[perm])
+    assert torch.equal(o1[perm], o2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_causal_decoder(dev, dtype):
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(2, 4, 200, 64, generator=g).to(dtype) for _ in range(3))
+    table = torch.randn(32, 4, generator=g) * 0.1
+    want = oa.rpb_attention(q, k, v, table, 32, 128, True, None, 0.125)
+    got = _rpb()(q.to(dev), k.to(dev), v.to(dev), table.to(dev), 32, 128, True,
+                 softmax_scale=0.125)
+    assert_attn_close(got, want, f"causal {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_no_table_full_mask_cross_lengths(dev, dtype):
+    """rpb_table=None, a per-query 4-D mask, Lq != Lk."""
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(2, 3, 130, 64, generator=g).to(dtype)
+    k = torch.randn(2, 3, 70, 64, generator=g).to(dtype)
+    v = torch.randn(2, 3, 70, 64, generator=g).to(dtype)
+    mask = torch.randn(2, 1, 130, 70, generator=g).to(dtype)
+    want = oa.rpb_attention(q, k, v, None, 32, 128, False, mask, 0.125)
+    got = _rpb()(q.to(dev), k.to(dev), v.to(dev), None, 32, 128, False,
+                 padding_mask=mask.to(dev), softmax_scale=0.125)
+    assert_attn_close(got, want, f"no-table {dtype}")
+
+
+def test_strided_inputs(dev):
+    """[B, L, H, D] projections viewed as [B, H, L, D] (transpose, no copy)."""
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(2, 300, 3, 8, 64, generator=g).bfloat16()
+    q, k, v = (x[:, :, i].transpose(1, 2) for i in range(3))
+    table = torch.randn(32, 8, generator=g) * 0.1
+    want = oa.rpb_attention(q, k, v, table, 32, 128, False, None, 0.3)
+    xd = x.to(dev)
+    qd, kd, vd = (xd[:, :, i].transpose(1, 2) for i in range(3))
+    got = _rpb()(qd, kd, vd, table.to(dev), 32, 128, False, softmax_scale=0.3)
+    assert_attn_close(got, want, "strided")
+
+
+def test_all_keys_masked_row_is_uniform(dev):
+    """A batch row whose keys are all masked averages V uniformly, as the
+    reference's finite additive mask does."""
+    g = torch.Generator().manual_seed(8)
+    q, k, v = (torch.randn(2, 2, 96, 64, generator=g).bfloat16() for _ in range(3))
+    mask = torch.zeros(2, 1, 1, 96)
+    mask[1] = torch.finfo(torch.float32).min
+    want = oa.rpb_attention(q, k, v, None, 32, 128, False, mask, 1.0)
+    got = _rpb()(q.to(dev), k.to(dev), v.to(dev), None, 32, 128, False,
+                 padding_mask=mask.to(dev))
+    assert_attn_close(got, want, "all-masked")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("bidirectional", [True, False])
+def test_device_buckets_exact(dev, dtype, bidirectional):
+    """Recovers the device's bucket of every (query, key) pair: q = k = 0, V
+    one-hot per key and a table with a single hot bucket give
+    out[q, j] > 0 exactly when bucket(j - q) is the hot bucket."""
+    Lq, Lk, H = 256, 64, 1
+    want = ob.t5_bucket_matrix(Lq, Lk, bidirectional, 32, 128)
+    z = torch.zeros(1, H, Lq, 64, dtype=dtype, device=dev)
+    zk = torch.zeros(1, H, Lk, 64, dtype=dtype, device=dev)
+    v = torch.eye(64, dtype=dtype, device=dev)[None, None]
+    for hot in range(32):
+        table = torch.zeros(32, H, device=dev)
+        table[hot] = 80.0
+        out = _rpb()(z, zk, v, table, 32, 128, not bidirectional)
+        member = (want == hot)
+        if not bidirectional:
+            member &= torch.arange(Lk)[None, :] <= torch.arange(Lq)[:, None]
+        rows = member.any(dim=1)
+        got = out[0, 0].float().cpu() > 1e-3
+        assert torch.equal(got[rows], member[rows]), f"bucket {hot}"

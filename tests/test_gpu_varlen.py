@@ -1,0 +1,86 @@
+"""GPU parity of the ModernBERT packed local/global RoPE attention against the
+oracle's per-sequence restatement of the reference's SDPA + dense masks."""
+import pytest
+import torch
+
+import workloads
+from _tol import assert_attn_close
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+
+LENGTHS = [1, 5, 63, 64, 65, 127, 128, 129, 200, 300, 700]
+
+
+def _vl():
+    from kernels.varlen_attention import varlen_rope_attention
+    return varlen_rope_attention
+
+
+def _pack(lengths, dtype, seed, H=12):
+    g = torch.Generator().manual_seed(seed)
+    T = sum(lengths)
+    qkv = (torch.randn(T, 3, H, 64, generator=g) * 0.8).to(dtype)
+    cu = workloads.cu_from_lengths(torch.tensor(lengths))
+    return qkv, cu
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("window,theta", [(-1, 160000.0), (64, 10000.0), (-1, 0.0), (5, 10000.0)])
+def test_varlen_small_packs(dev, dtype, window, theta):
+    qkv, cu = _pack(LENGTHS, dtype, 1)
+    q, k, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
+    want = oa.varlen_attention(q, k, v, cu, window, theta, None, 0.125)
+    qd = qkv.to(dev)
+    got = _vl()(qd[:, 0], qd[:, 1], qd[:, 2], cu.to(dev), max(LENGTHS), window, theta, 0.125)
+    assert_attn_close(got, want, f"varlen {dtype} w={window} theta={theta}")
+
+
+@pytest.mark.parametrize("window", [-1, 64])
+def test_varlen_key_valid_mask(dev, window):
+    qkv, cu = _pack(LENGTHS, torch.bfloat16, 2)
+    T = qkv.shape[0]
+    g = torch.Generator().manual_seed(3)
+    key_valid = torch.rand(T, generator=g) > 0.1
+    q, k, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
+    want = oa.varlen_attention(q, k, v, cu, window, 160000.0, key_valid, 0.125)
+    qd = qkv.to(dev)
+    got = _vl()(qd[:, 0], qd[:, 1], qd[:, 2], cu.to(dev), max(LENGTHS), window, 160000.0, 0.125,
+                key_valid=key_valid.to(dev))
+    assert_attn_close(got, want, f"key_valid w={window}")
+
+
+@pytest.mark.parametrize("window,theta", [(-1, 160000.0), (64, 10000.0)])
+def test_config2_subset(dev, window, theta):
+    """Config 2 (64 sequences, 512..768 tokens): 6 sequences checked exactly."""
+    c = workloads.config2(device=dev)
+    qkv = c.qkv
+    got = _vl()(qkv[:, 0], qkv[:, 1], qkv[:, 2], c.cu_seqlens, c.max_seqlen, window, theta, 0.125)
+    cu = c.cu_seqlens.cpu()
+    for s in (0, 1, 17, 31, 50, 63):
+        a, b = int(cu[s]), int(cu[s + 1])
+        sub = qkv[a:b].cpu()
+        want = oa.varlen_attention(sub[:, 0], sub[:, 1], sub[:, 2],
+                                   torch.tensor([0, b - a], dtype=torch.int32), window, theta, None, 0.125)
+        assert_attn_close(got[a:b], want, f"cfg2 seq {s} w={window}")
+
+
+def test_config2_full_properties(dev):
+    """Whole config 2: V = 1 -> 1; permuting the packing order permutes rows."""
+    c = workloads.config2(device=dev)
+    q, k = c.qkv[:, 0], c.qkv[:, 1]
+    ones = torch.ones_like(c.qkv[:, 2])
+    for window in (-1, 64):
+        o = _vl()(q, k, ones, c.cu_seqlens, c.max_seqlen, window, 160000.0, 0.125)
+        assert torch.allclose(o.float(), torch.ones_like(o, dtype=torch.float32), atol=1e-2)
+    # reverse the sequence order of the pack
+    cu = c.cu_seqlens.cpu().tolist()
+    n = len(cu) - 1
+    order = list(range(n))[::-1]
+    idx = torch.cat([torch.arange(cu[s], cu[s + 1]) for s in order]).to(dev)
+    lens = torch.tensor([cu[s + 1] - cu[s] for s in order])
+    cu2 = workloads.cu_from_lengths(lens).to(dev)
+    v = c.qkv[:, 2]
+    o1 = _vl()(q, k, v, c.cu_seqlens, c.max_seqlen, 64, 10000.0, 0.125)
+    o2 = _vl()(q[idx], k[idx], v[idx], cu2, c.max_seqlen, 64, 10000.0, 0.125)
+    assert torch.equal(o1[idx], o2)

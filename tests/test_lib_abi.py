@@ -1,0 +1,93 @@
+"""The C ABI library loads on a CPU-only host, exports every symbol that
+include/vfk.h declares, and its host-side bucket helpers are bit-exact with
+the oracle. No GPU compute is issued here."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import buckets as ob
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    src = open(os.path.join(ROOT, "include", "vfk.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(vfk_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_symbols_exported():
+    from kernels import _lib
+    lib = _lib.load()
+    syms = _declared_symbols()
+    assert len(syms) >= 13
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert set(syms) <= set(_lib._SIGNATURES) | {"vfk_last_error"}
+
+
+def test_abi_version():
+    from kernels import _lib
+    assert _lib.load().vfk_abi_version() == 1
+
+
+def _host_t5(rel, bidirectional, nb, md):
+    from kernels import _lib
+    rel = np.ascontiguousarray(rel, dtype=np.int64)
+    out = np.zeros(rel.shape, dtype=np.int32)
+    _lib.call("vfk_t5_bucket", rel.ctypes.data, out.ctypes.data, rel.size,
+              int(bidirectional), nb, md)
+    return out
+
+
+def _host_deb(rel, bs, mp):
+    from kernels import _lib
+    rel = np.ascontiguousarray(rel, dtype=np.int64)
+    out = np.zeros(rel.shape, dtype=np.int32)
+    _lib.call("vfk_deberta_bucket", rel.ctypes.data, out.ctypes.data, rel.size, bs, mp)
+    return out
+
+
+@pytest.mark.parametrize("bidirectional", [True, False])
+@pytest.mark.parametrize("nb,md", [(32, 128), (32, 64), (64, 256), (16, 100), (128, 1024)])
+def test_t5_host_bucket_matches_oracle(bidirectional, nb, md):
+    # full [L, L] matrix like the reference evaluates it
+    L = 1200
+    want = ob.t5_bucket_matrix(L, L, bidirectional, nb, md).numpy()
+    rel = (np.arange(L)[None, :] - np.arange(L)[:, None]).astype(np.int64)
+    got = _host_t5(rel, bidirectional, nb, md)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("bs,mp", [(256, 512), (256, 1024), (128, 512), (64, 256)])
+def test_deberta_host_bucket_matches_oracle(bs, mp):
+    L = 1100
+    want = ob.build_relative_position_v2(L, L, bs, mp)[0].numpy()
+    rel = (np.arange(L)[:, None] - np.arange(L)[None, :]).astype(np.int64)
+    got = _host_deb(rel, bs, mp)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_invalid_arguments_raise():
+    from kernels import _lib
+    # num_buckets too small for the T5 formula: rejected, nothing launched
+    rel = np.zeros(4, dtype=np.int64)
+    out = np.zeros(4, dtype=np.int32)
+    with pytest.raises(NotImplementedError):
+        _lib.call("vfk_t5_bucket", rel.ctypes.data, out.ctypes.data, 4, 1, 2, 128)
+    with pytest.raises(ValueError):
+        _lib.call("vfk_t5_bucket", None, None, 4, 1, 32, 128)
+
+
+def test_product_rejects_cpu_tensors():
+    from kernels.flash_attention_rpb import flash_attention_rpb_final
+    from kernels.fused_layernorm import fused_layernorm
+    q = torch.randn(1, 1, 8, 64)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        flash_attention_rpb_final(q, q, q, None, 32, 128, False)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        fused_layernorm(torch.randn(4, 8), 8)

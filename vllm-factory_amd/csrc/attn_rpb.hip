@@ -1,0 +1,369 @@
+// T5 relative-position-bias flash attention (forward), kernels for gfx950.
+//
+// Reference behaviour: kernels/flash_attention_rpb.py:61-230 (Triton kernel)
+// and its eager twin models/mt5/mt5_encoder.py:150-164, :285-320.
+//   out = softmax(q k^T * scale + table[bucket(k - q), h] + mask) v
+// The bucket of every relative position the workgroup can meet is evaluated
+// once into an LDS table of bias values (already multiplied by log2 e), so the
+// inner loop does one LDS read per score instead of a log and a gather.
+#include <math.h>
+
+#include "attn_core.h"
+#include "launch_util.h"
+
+namespace vfk {
+
+enum { MASK_NONE = 0, MASK_KEY = 1, MASK_FULL = 2 };
+
+struct RpbArgs {
+  const void* q; const void* k; const void* v; void* o;
+  int64_t qs[4], ks[4], vs[4], os[4];  // [B,H,L,D] strides, D stride is 1
+  const void* table; int table_dt; int64_t tb0, tb1; int total_buckets;
+  const void* mask; int mask_dt; int64_t ms[4];
+  int B, H, Lq, Lk;
+  float c2;     // softmax_scale * log2(e)
+  float inv_scale;  // 1 / softmax_scale: bias and mask in raw score units
+  int bidir, causal, offset_pos;  // offset added for rel > 0 (bidirectional)
+  int lut_len;  // ntiles * kBN + kBM (LDS bias table entries)
+  StepFn step;
+};
+
+__device__ inline float ld_f(const void* p, int dt, int64_t i) {
+  if (dt == VFK_F32) return reinterpret_cast<const float*>(p)[i];
+  if (dt == VFK_BF16) return BF16::to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  return F16::to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+// Additive mask value in raw score units (mask / softmax_scale). Clamped at
+// -1e30: still absorbs any score exactly (so a row whose keys are all masked
+// averages uniformly, like the reference's finite mask), while the softmax's
+// later multiply by scale*log2(e) cannot overflow.
+__device__ inline float mask_raw(float m, float inv_scale) {
+  return fmaxf(m * inv_scale, -1.0e30f);
+}
+// fp32 kernel works in log2 units.
+__device__ inline float mask_l2(float m) {
+  return fmaxf(m * VFK_LOG2E, -3.0e38f);
+}
+
+__device__ inline int rpb_bucket(const RpbArgs& a, int rel) {
+  int b;
+  if (a.bidir) {
+    const int mag = rel < 0 ? -rel : rel;
+    b = step_eval(a.step, mag) + (rel > 0 ? a.offset_pos : 0);
+  } else {
+    b = step_eval(a.step, rel < 0 ? -rel : 0);
+  }
+  return min(max(b, 0), a.total_buckets - 1);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 / fp16 MFMA kernel
+// ---------------------------------------------------------------------------
+template <typename E, int MASK>
+__global__ __launch_bounds__(256, 2) void rpb_fwd_kernel(RpbArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);
+  uint16_t* Vt = Ks + kKsElems;
+  float* maskt = reinterpret_cast<float*>(Vt + kVtElems);  // [kBN]
+  int* tflag = reinterpret_cast<int*>(maskt + kBN);        // [ntiles]
+  const int ntiles_all = (a.Lk + kBN - 1) / kBN;
+  float* lut = reinterpret_cast<float*>(tflag + ((ntiles_all + 3) & ~3));
+
+  const int nqt = (a.Lq + kBM - 1) / kBM;
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = work % nqt;
+  const int bh = work / nqt;
+  const int h = bh % a.H, b = bh / a.H;
+  const int q0 = qt * kBM;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, hl = lane >> 5;
+
+  const uint16_t* Qp = reinterpret_cast<const uint16_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const uint16_t* Kp = reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
+  const uint16_t* Vp = reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
+
+  // ---- bias table over rel = key - query, rel in [-(q0+127), Lk-1-q0] ----
+  const bool has_table = a.table != nullptr;
+  if (has_table) {
+    for (int e = t; e < a.lut_len; e += 256) {
+      const int rel = e - q0 - (kBM - 1);
+      const int bk = rpb_bucket(a, rel);
+      lut[e] = ld_f(a.table, a.table_dt, bk * a.tb0 + h * a.tb1) * a.inv_scale;
+    }
+  }
+  // ---- key-mask tile classification: bit0 = some nonzero, bit1 = some live
+  int kt_end = ntiles_all;
+  if (a.causal) kt_end = min(kt_end, (min(q0 + kBM, a.Lq) - 1) / kBN + 1);
+  bool any_live = true;
+  if (MASK == MASK_KEY) {
+    for (int i = t; i < ntiles_all; i += 256) tflag[i] = 0;
+    __syncthreads();
+    const char* mb = reinterpret_cast<const char*>(a.mask);
+    for (int j = t; j < a.Lk; j += 256) {
+      const float mv = ld_f(mb, a.mask_dt, b * a.ms[0] + h * a.ms[1] + j * a.ms[3]);
+      // live: not clamped, i.e. contributes unless a row has no live key
+      const int f = (mv != 0.f ? 1 : 0) | (mask_raw(mv, a.inv_scale) > -1.0e30f ? 2 : 0);
+      if (f) atomicOr(&tflag[j / kBN], f);
+    }
+    __syncthreads();
+    int live = 0;
+    for (int i = 0; i < kt_end; ++i) live |= tflag[i] & 2;
+    any_live = live != 0;
+  }
+  __syncthreads();
+
+  // ---- this lane's query row ----
+  const int qrow = q0 + w * 32 + (lane & 31);
+  const bool qvalid = qrow < a.Lq;
+  u32x4_t qf[4];
+  load_q(qf, Qp + (int64_t)qrow * a.qs[2], qvalid);
+
+  float m = -INFINITY, l = 0.f;
+  f32x16_t o0 = {}, o1 = {};
+  // lut index of element i in tile kt: kt*64 + x_key(i) + lut_base
+  const int lut_base = 4 * hl - w * 32 - (lane & 31) + (kBM - 1);
+
+  auto skip_tile = [&](int kt) -> bool {
+    if (MASK != MASK_KEY) return false;
+    return any_live && !(tflag[kt] & 2);
+  };
+
+  KVStage st;
+  int kt = 0;
+  while (kt < kt_end && skip_tile(kt)) ++kt;
+  if (kt < kt_end) kv_load(st, Kp, a.ks[2], Vp, a.vs[2], kt * kBN, a.Lk);
+  while (kt < kt_end) {
+    const int key0 = kt * kBN;
+    kv_store(st, Ks, Vt);
+    if (MASK == MASK_KEY) {
+      if (t < kBN) {
+        const int j = key0 + t;
+        maskt[t] = j < a.Lk ? mask_raw(ld_f(a.mask, a.mask_dt, b * a.ms[0] + h * a.ms[1] + j * a.ms[3]), a.inv_scale) : 0.f;
+      }
+    }
+    __syncthreads();
+    int nk = kt + 1;
+    while (nk < kt_end && skip_tile(nk)) ++nk;
+    if (nk < kt_end) kv_load(st, Kp, a.ks[2], Vp, a.vs[2], nk * kBN, a.Lk);
+
+    f32x16_t s0, s1;
+    qk_tile<E>(Ks, qf, s0, s1);
+    float x[32];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { x[i] = s0[i]; x[16 + i] = s1[i]; }
+    if (has_table) {
+      const float* lp = lut + key0 + lut_base;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) x[i] += lp[x_key(i, 0)];
+    }
+    if (MASK == MASK_KEY) {
+      if (tflag[kt] & 1) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] += maskt[x_key(i, hl)];
+      }
+    } else if (MASK == MASK_FULL) {
+      if (qvalid) {
+        const int64_t mo = b * a.ms[0] + h * a.ms[1] + (int64_t)qrow * a.ms[2];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const int j = key0 + x_key(i, hl);
+          if (j < a.Lk) x[i] += mask_raw(ld_f(a.mask, a.mask_dt, mo + (int64_t)j * a.ms[3]), a.inv_scale);
+        }
+      }
+    }
+    if (key0 + kBN > a.Lk || a.causal) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int j = key0 + x_key(i, hl);
+        if (j >= a.Lk || (a.causal && j > qrow)) x[i] = -INFINITY;
+      }
+    }
+    u32x4_t p[4];
+    softmax_tile<E>(x, a.c2, m, l, o0, o1, p);
+    pv_tile<E>(Vt, p, o0, o1);
+    __syncthreads();
+    kt = nk;
+  }
+  const float l_tot = half_swap_sum(l);
+  if (qvalid) {
+    uint16_t* orow = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1] + (int64_t)qrow * a.os[2];
+    store_out<E>(orow, o0, o1, l_tot);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 kernel: one thread per query row, exact fp32 arithmetic throughout.
+// ---------------------------------------------------------------------------
+template <int MASK>
+__global__ __launch_bounds__(64) void rpb_fwd_f32_kernel(RpbArgs a) {
+  __shared__ float Kt[64][kHD + 1];
+  __shared__ float Vt32[64][kHD + 1];
+  const int nqt = (a.Lq + 63) / 64;
+  const int qt = blockIdx.x % nqt;
+  const int bh = blockIdx.x / nqt;
+  const int h = bh % a.H, b = bh / a.H;
+  const int qrow = qt * 64 + threadIdx.x;
+  const bool qvalid = qrow < a.Lq;
+  const float* Qp = reinterpret_cast<const float*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const float* Kp = reinterpret_cast<const float*>(a.k) + b * a.ks[0] + h * a.ks[1];
+  const float* Vp = reinterpret_cast<const float*>(a.v) + b * a.vs[0] + h * a.vs[1];
+  float qv[kHD], acc[kHD];
+#pragma unroll
+  for (int d = 0; d < kHD; ++d) {
+    qv[d] = qvalid ? Qp[(int64_t)qrow * a.qs[2] + d] : 0.f;
+    acc[d] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  int kend = a.Lk;
+  if (a.causal) kend = min(kend, min(qt * 64 + 64, a.Lq));
+  for (int key0 = 0; key0 < kend; key0 += 64) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < 64 * kHD; e += 64) {
+      const int r = e / kHD, d = e % kHD;
+      const int j = key0 + r;
+      Kt[r][d] = j < a.Lk ? Kp[(int64_t)j * a.ks[2] + d] : 0.f;
+      Vt32[r][d] = j < a.Lk ? Vp[(int64_t)j * a.vs[2] + d] : 0.f;
+    }
+    __syncthreads();
+    const int nk = min(64, kend - key0);
+    for (int r = 0; r < nk; ++r) {
+      const int j = key0 + r;
+      if (a.causal && j > qrow) break;
+      float s = 0.f;
+#pragma unroll
+      for (int d = 0; d < kHD; ++d) s += qv[d] * Kt[r][d];
+      s = s * a.c2;
+      if (a.table) s += ld_f(a.table, a.table_dt, rpb_bucket(a, j - qrow) * a.tb0 + h * a.tb1) * VFK_LOG2E;
+      if (MASK != MASK_NONE)
+        s += mask_l2(ld_f(a.mask, a.mask_dt, b * a.ms[0] + h * a.ms[1] + (int64_t)qrow * a.ms[2] + (int64_t)j * a.ms[3]));
+      const float mn = fmaxf(m, s);
+      const float alpha = exp2f(m - mn);
+      const float p = exp2f(s - mn);
+      l = l * alpha + p;
+#pragma unroll
+      for (int d = 0; d < kHD; ++d) acc[d] = acc[d] * alpha + p * Vt32[r][d];
+      m = mn;
+    }
+  }
+  if (!qvalid) return;
+  float* op = reinterpret_cast<float*>(a.o) + b * a.os[0] + h * a.os[1] + (int64_t)qrow * a.os[2];
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+  for (int d = 0; d < kHD; ++d) op[d] = acc[d] * inv;
+}
+
+}  // namespace vfk
+
+using namespace vfk;
+
+static int check_bhld(const vfk_tensor* t, const char* name, int dtype) {
+  int rc = check_tensor(t, name, 4);
+  if (rc) return rc;
+  if (t->dtype != dtype)
+    return set_error(VFK_ERR_INVALID, "%s: dtype %d differs from q", name, t->dtype);
+  if (t->size[3] != kHD)
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: head_dim %lld (only 64 is built)",
+                     name, (long long)t->size[3]);
+  if (t->stride[3] != 1)
+    return set_error(VFK_ERR_INVALID, "%s: head_dim must be contiguous", name);
+  if (dtype != VFK_F32) {
+    if (!aligned16(t->data) || t->stride[0] % 8 || t->stride[1] % 8 || t->stride[2] % 8)
+      return set_error(VFK_ERR_INVALID, "%s: rows must be 16-byte aligned", name);
+  }
+  return VFK_OK;
+}
+
+extern "C" int vfk_flash_rpb_fwd(const vfk_tensor* q, const vfk_tensor* k,
+                                 const vfk_tensor* v, const vfk_tensor* rpb_table,
+                                 int32_t num_buckets, int32_t max_distance,
+                                 int32_t is_decoder, const vfk_tensor* mask,
+                                 float softmax_scale, vfk_tensor* out,
+                                 void* stream) {
+  int rc = check_tensor(q, "q", 4);
+  if (rc) return rc;
+  const int dt = q->dtype;
+  if ((rc = check_bhld(q, "q", dt)) || (rc = check_bhld(k, "k", dt)) ||
+      (rc = check_bhld(v, "v", dt)) || (rc = check_bhld(out, "out", dt)))
+    return rc;
+  const int64_t B = q->size[0], H = q->size[1], Lq = q->size[2], Lk = k->size[2];
+  if (k->size[0] != B || k->size[1] != H || v->size[0] != B || v->size[1] != H ||
+      v->size[2] != Lk)
+    return set_error(VFK_ERR_INVALID, "vfk_flash_rpb_fwd: q/k/v shapes disagree");
+  for (int i = 0; i < 4; ++i)
+    if (out->size[i] != q->size[i])
+      return set_error(VFK_ERR_INVALID, "vfk_flash_rpb_fwd: out shape must equal q");
+  if (Lq > (1 << 20) || Lk > (1 << 20) || B * H > (1 << 24))
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_rpb_fwd: sizes too large");
+  RpbArgs a = {};
+  a.q = q->data; a.k = k->data; a.v = v->data; a.o = out->data;
+  for (int i = 0; i < 4; ++i) {
+    a.qs[i] = q->stride[i]; a.ks[i] = k->stride[i];
+    a.vs[i] = v->stride[i]; a.os[i] = out->stride[i];
+  }
+  a.B = (int)B; a.H = (int)H; a.Lq = (int)Lq; a.Lk = (int)Lk;
+  if (!(softmax_scale > 0.f) || !isfinite(softmax_scale))
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_rpb_fwd: softmax_scale must be > 0");
+  a.c2 = softmax_scale * VFK_LOG2E;
+  a.inv_scale = 1.0f / softmax_scale;
+  a.bidir = is_decoder ? 0 : 1;
+  a.causal = is_decoder ? 1 : 0;
+  if (present(rpb_table)) {
+    if ((rc = check_tensor(rpb_table, "rpb_table", 2))) return rc;
+    if (rpb_table->size[1] != H)
+      return set_error(VFK_ERR_INVALID, "rpb_table: expected [buckets, %lld]", (long long)H);
+    if (rpb_table->size[0] < 1)
+      return set_error(VFK_ERR_INVALID, "rpb_table: no buckets");
+    a.table = rpb_table->data; a.table_dt = rpb_table->dtype;
+    a.tb0 = rpb_table->stride[0]; a.tb1 = rpb_table->stride[1];
+    a.total_buckets = (int)rpb_table->size[0];
+    if ((rc = build_t5_step(a.bidir, num_buckets, max_distance, &a.step))) return rc;
+    a.offset_pos = num_buckets / 2;
+  }
+  int mode = MASK_NONE;
+  if (present(mask)) {
+    if ((rc = check_tensor(mask, "padding_mask", 4))) return rc;
+    const int64_t want[4] = {B, H, Lq, Lk};
+    for (int i = 0; i < 4; ++i) {
+      if (mask->size[i] != want[i] && mask->size[i] != 1)
+        return set_error(VFK_ERR_INVALID, "padding_mask: dim %d not broadcastable", i);
+      a.ms[i] = mask->size[i] == 1 ? 0 : mask->stride[i];
+    }
+    a.mask = mask->data; a.mask_dt = mask->dtype;
+    mode = (a.ms[2] == 0) ? MASK_KEY : MASK_FULL;
+  }
+  if (B == 0 || H == 0 || Lq == 0) return VFK_OK;
+  if (Lk == 0)
+    return set_error(VFK_ERR_INVALID, "vfk_flash_rpb_fwd: no keys");
+  hipStream_t st = (hipStream_t)stream;
+  if (dt == VFK_F32) {
+    const int nqt = ceil_div(Lq, 64);
+    dim3 grid((unsigned)(nqt * B * H));
+    if (mode == MASK_NONE)
+      hipLaunchKernelGGL(rpb_fwd_f32_kernel<MASK_NONE>, grid, dim3(64), 0, st, a);
+    else
+      hipLaunchKernelGGL(rpb_fwd_f32_kernel<MASK_FULL>, grid, dim3(64), 0, st, a);
+    return launch_status("vfk_flash_rpb_fwd");
+  }
+  const int ntiles = ceil_div(Lk, kBN);
+  a.lut_len = a.table ? ntiles * kBN + kBM : 0;
+  const size_t lds = (size_t)(kKsElems + kVtElems) * 2 + kBN * 4 +
+                     ((ntiles + 3) & ~3) * 4 + (size_t)a.lut_len * 4;
+  if (lds > 160 * 1024)
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_rpb_fwd: Lk=%lld needs %zu B of LDS",
+                     (long long)Lk, lds);
+  const int nqt = ceil_div(Lq, kBM);
+  dim3 grid((unsigned)(nqt * B * H));
+#define VFK_RPB_LAUNCH(E)                                                              \
+  switch (mode) {                                                                      \
+    case MASK_NONE: hipLaunchKernelGGL((rpb_fwd_kernel<E, MASK_NONE>), grid, dim3(256), lds, st, a); break; \
+    case MASK_KEY: hipLaunchKernelGGL((rpb_fwd_kernel<E, MASK_KEY>), grid, dim3(256), lds, st, a); break;   \
+    default: hipLaunchKernelGGL((rpb_fwd_kernel<E, MASK_FULL>), grid, dim3(256), lds, st, a); break;        \
+  }
+  if (dt == VFK_BF16) {
+    VFK_RPB_LAUNCH(BF16)
+  } else {
+    VFK_RPB_LAUNCH(F16)
+  }
+#undef VFK_RPB_LAUNCH
+  return launch_status("vfk_flash_rpb_fwd");
+}

@@ -1,0 +1,324 @@
+// Varlen (packed-sequence) bidirectional attention for ModernBERT, gfx950.
+//
+// Replaces F.scaled_dot_product_attention over the whole packed stream with
+// dense [T, T] block-diagonal / sliding-window masks
+// (models/modernbert/modernbert_encoder.py:236-255, :491-550): work is cut per
+// sequence by cu_seqlens, so cross-sequence pairs are never computed, and a
+// sliding-window layer only visits the key tiles its rows can see.
+// RoPE (non-interleaved halves, HF ModernBertRotaryEmbedding tables) is
+// applied in the kernel: Q once per row in registers, K as each tile is staged.
+#include <math.h>
+
+#include "attn_core.h"
+#include "launch_util.h"
+
+namespace vfk {
+
+struct VarlenArgs {
+  const void* q; const void* k; const void* v; void* o;
+  int64_t qs[2], ks[2], vs[2], os[2];  // [T,H,D] strides of T and H (D stride 1)
+  const int32_t* cu; int nseq; int nqt; int H; int window;
+  float c2;                 // softmax scale * log2(e)
+  int rope;
+  float inv_freq_rev[32];   // inv_freq[f] / (2 pi)
+  float inv_freq[32];       // HF fp32 inv_freq (fp32 kernel)
+  const uint8_t* key_valid; // optional, [T]
+};
+
+template <typename E, bool ROPE, bool LOCAL, bool KVALID>
+__global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenArgs a) {
+  __shared__ __align__(16) uint16_t Ks[kKsElems];
+  __shared__ __align__(16) uint16_t Vt[kVtElems];
+  __shared__ float kmask[kBN];
+  __shared__ int kflag[2];
+
+  const int total = gridDim.x;
+  const int work = xcd_remap(blockIdx.x, total);
+  const int qt = work % a.nqt;
+  const int h = (work / a.nqt) % a.H;
+  const int s = work / (a.nqt * a.H);
+  const int tok0 = a.cu[s];
+  const int n = a.cu[s + 1] - tok0;
+  const int q0 = qt * kBM;
+  if (q0 >= n) return;  // whole workgroup: uniform exit
+
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, hl = lane >> 5;
+  const uint16_t* Qp = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)tok0 * a.qs[0] + h * a.qs[1];
+  const uint16_t* Kp = reinterpret_cast<const uint16_t*>(a.k) + (int64_t)tok0 * a.ks[0] + h * a.ks[1];
+  const uint16_t* Vp = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)tok0 * a.vs[0] + h * a.vs[1];
+
+  float invf[8];
+  if (ROPE) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) invf[i] = a.inv_freq_rev[8 * (t & 3) + i];
+  }
+
+  // key range of the workgroup (sequence-relative)
+  int klo = 0, khi = n;
+  if (LOCAL) {
+    klo = max(0, q0 - a.window);
+    khi = min(n, q0 + kBM + a.window);
+  }
+  const int kt_begin = klo / kBN;
+  const int kt_end = (khi + kBN - 1) / kBN;
+
+  // this wave's rows and the keys they can see
+  const int wq_lo = q0 + w * 32;
+  const int wq_hi = min(wq_lo + 31, n - 1);
+  const int qrow = wq_lo + (lane & 31);
+  const bool qvalid = qrow < n;
+
+  u32x4_t qf[4];
+  load_q(qf, Qp + (int64_t)qrow * a.qs[0], qvalid);
+  if (ROPE) rope_q<E>(qf, qrow, a.inv_freq_rev);
+
+  float m = -INFINITY, l = 0.f;
+  f32x16_t o0 = {}, o1 = {};
+
+  KVStage st;
+  int kt = kt_begin;
+  kv_load(st, Kp, a.ks[0], Vp, a.vs[0], kt * kBN, n);
+  while (kt < kt_end) {
+    const int key0 = kt * kBN;
+    if (ROPE) rope_k<E>(st, key0 + (t >> 2), invf);
+    kv_store(st, Ks, Vt);
+    if (KVALID) {
+      if (t == 0) kflag[kt & 1] = 0;
+    }
+    __syncthreads();
+    if (KVALID) {
+      if (t < kBN) {
+        const int j = key0 + t;
+        const bool ok = j >= n || a.key_valid[tok0 + j] != 0;
+        kmask[t] = ok ? 0.f : -INFINITY;
+        if (!ok) atomicOr(&kflag[kt & 1], 1);
+      }
+    }
+    if (kt + 1 < kt_end) kv_load(st, Kp, a.ks[0], Vp, a.vs[0], (kt + 1) * kBN, n);
+    if (KVALID) __syncthreads();
+
+    // does this wave see any key of the tile?
+    bool active = wq_lo < n;
+    if (LOCAL) active = active && key0 <= wq_hi + a.window && key0 + kBN - 1 >= wq_lo - a.window;
+    if (active) {
+      f32x16_t s0, s1;
+      qk_tile<E>(Ks, qf, s0, s1);
+      float x[32];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) { x[i] = s0[i]; x[16 + i] = s1[i]; }
+      if (KVALID) {
+        if (kflag[kt & 1]) {
+#pragma unroll
+          for (int i = 0; i < 32; ++i) x[i] += kmask[x_key(i, hl)];
+        }
+      }
+      bool partial = key0 + kBN > n;
+      if (LOCAL)
+        partial = partial || (wq_hi - key0 > a.window) || (key0 + kBN - 1 - wq_lo > a.window);
+      if (partial) {
+        const int rb = qrow - key0 - 4 * hl;  // qrow - key for x_key(i, 0) = 0
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const int kk = x_key(i, 0);
+          const int rel = rb - kk;
+          bool dead = key0 + kk + 4 * hl >= n;
+          if (LOCAL) dead = dead || rel > a.window || rel < -a.window;
+          if (dead) x[i] = -INFINITY;
+        }
+      }
+      u32x4_t p[4];
+      softmax_tile<E>(x, a.c2, m, l, o0, o1, p);
+      pv_tile<E>(Vt, p, o0, o1);
+    }
+    __syncthreads();
+    ++kt;
+  }
+  const float l_tot = half_swap_sum(l);
+  if (qvalid) {
+    uint16_t* orow = reinterpret_cast<uint16_t*>(a.o) + (int64_t)(tok0 + qrow) * a.os[0] + h * a.os[1];
+    store_out<E>(orow, o0, o1, l_tot);
+  }
+}
+
+// fp32: one thread per query row, exact fp32 arithmetic, accurate sin/cos.
+__global__ __launch_bounds__(64) void varlen_fwd_f32_kernel(VarlenArgs a, const float* inv_freq_unused) {
+  __shared__ float Kt[64][kHD + 1];
+  __shared__ float Vt32[64][kHD + 1];
+  const int nqt64 = a.nqt * 2;
+  const int qt = blockIdx.x % nqt64;
+  const int h = (blockIdx.x / nqt64) % a.H;
+  const int s = blockIdx.x / (nqt64 * a.H);
+  const int tok0 = a.cu[s];
+  const int n = a.cu[s + 1] - tok0;
+  const int q0 = qt * 64;
+  if (q0 >= n) return;
+  const int qrow = q0 + threadIdx.x;
+  const bool qvalid = qrow < n;
+  const float* Qp = reinterpret_cast<const float*>(a.q) + (int64_t)tok0 * a.qs[0] + h * a.qs[1];
+  const float* Kp = reinterpret_cast<const float*>(a.k) + (int64_t)tok0 * a.ks[0] + h * a.ks[1];
+  const float* Vp = reinterpret_cast<const float*>(a.v) + (int64_t)tok0 * a.vs[0] + h * a.vs[1];
+  float qv[kHD], acc[kHD];
+#pragma unroll
+  for (int d = 0; d < kHD; ++d) {
+    qv[d] = qvalid ? Qp[(int64_t)qrow * a.qs[0] + d] : 0.f;
+    acc[d] = 0.f;
+  }
+  if (a.rope) {
+#pragma unroll
+    for (int f = 0; f < 32; ++f) {
+      float sn, cs;
+      sincosf((float)qrow * a.inv_freq[f], &sn, &cs);
+      const float x1 = qv[f], x2 = qv[f + 32];
+      qv[f] = x1 * cs - x2 * sn;
+      qv[f + 32] = x2 * cs + x1 * sn;
+    }
+  }
+  float m = -INFINITY, l = 0.f;
+  int klo = 0, khi = n;
+  if (a.window >= 0) {
+    klo = max(0, q0 - a.window);
+    khi = min(n, q0 + 64 + a.window);
+  }
+  for (int key0 = klo; key0 < khi; key0 += 64) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < 64 * 32; e += 64) {
+      const int r = e / 32, f = e % 32;
+      const int j = key0 + r;
+      float k1 = 0.f, k2 = 0.f, v1 = 0.f, v2 = 0.f;
+      if (j < khi) {
+        k1 = Kp[(int64_t)j * a.ks[0] + f];
+        k2 = Kp[(int64_t)j * a.ks[0] + f + 32];
+        v1 = Vp[(int64_t)j * a.vs[0] + f];
+        v2 = Vp[(int64_t)j * a.vs[0] + f + 32];
+        if (a.rope) {
+          float sn, cs;
+          sincosf((float)j * a.inv_freq[f], &sn, &cs);
+          const float x1 = k1, x2 = k2;
+          k1 = x1 * cs - x2 * sn;
+          k2 = x2 * cs + x1 * sn;
+        }
+      }
+      Kt[r][f] = k1; Kt[r][f + 32] = k2;
+      Vt32[r][f] = v1; Vt32[r][f + 32] = v2;
+    }
+    __syncthreads();
+    const int nk = min(64, khi - key0);
+    for (int r = 0; r < nk; ++r) {
+      const int j = key0 + r;
+      if (a.window >= 0 && (j - qrow > a.window || qrow - j > a.window)) continue;
+      if (a.key_valid && !a.key_valid[tok0 + j]) continue;
+      float sc = 0.f;
+#pragma unroll
+      for (int d = 0; d < kHD; ++d) sc += qv[d] * Kt[r][d];
+      sc *= a.c2;
+      const float mn = fmaxf(m, sc);
+      const float alpha = exp2f(m - mn);
+      const float p = exp2f(sc - mn);
+      l = l * alpha + p;
+#pragma unroll
+      for (int d = 0; d < kHD; ++d) acc[d] = acc[d] * alpha + p * Vt32[r][d];
+      m = mn;
+    }
+  }
+  if (!qvalid) return;
+  float* op = reinterpret_cast<float*>(a.o) + (int64_t)(tok0 + qrow) * a.os[0] + h * a.os[1];
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+  for (int d = 0; d < kHD; ++d) op[d] = acc[d] * inv;
+}
+
+}  // namespace vfk
+
+using namespace vfk;
+
+static int check_thd(const vfk_tensor* t, const char* name, int dtype, int64_t T, int64_t H) {
+  int rc = check_tensor(t, name, 3);
+  if (rc) return rc;
+  if (t->dtype != dtype)
+    return set_error(VFK_ERR_INVALID, "%s: dtype differs from q", name);
+  if (t->size[0] != T || t->size[1] != H)
+    return set_error(VFK_ERR_INVALID, "%s: expected [%lld, %lld, 64]", name, (long long)T, (long long)H);
+  if (t->size[2] != kHD)
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: head_dim %lld (only 64 is built)", name,
+                     (long long)t->size[2]);
+  if (t->stride[2] != 1)
+    return set_error(VFK_ERR_INVALID, "%s: head_dim must be contiguous", name);
+  if (dtype != VFK_F32 && (!aligned16(t->data) || t->stride[0] % 8 || t->stride[1] % 8))
+    return set_error(VFK_ERR_INVALID, "%s: rows must be 16-byte aligned", name);
+  return VFK_OK;
+}
+
+extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
+                                   const vfk_tensor* v, const int32_t* cu_seqlens,
+                                   int32_t num_seqs, int32_t max_seqlen,
+                                   int32_t window, float rope_theta,
+                                   const uint8_t* key_valid, float softmax_scale,
+                                   vfk_tensor* out, void* stream) {
+  int rc = check_tensor(q, "q", 3);
+  if (rc) return rc;
+  const int dt = q->dtype;
+  const int64_t T = q->size[0], H = q->size[1];
+  if ((rc = check_thd(q, "q", dt, T, H)) || (rc = check_thd(k, "k", dt, T, H)) ||
+      (rc = check_thd(v, "v", dt, T, H)) || (rc = check_thd(out, "out", dt, T, H)))
+    return rc;
+  if (!cu_seqlens) return set_error(VFK_ERR_INVALID, "cu_seqlens is NULL");
+  if (num_seqs < 0 || max_seqlen < 0)
+    return set_error(VFK_ERR_INVALID, "num_seqs/max_seqlen must be >= 0");
+  if (T >= (1ll << 31) || H > 4096 || max_seqlen > (1 << 24))
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: sizes too large");
+  if (num_seqs == 0 || max_seqlen == 0 || H == 0) return VFK_OK;
+  VarlenArgs a = {};
+  a.q = q->data; a.k = k->data; a.v = v->data; a.o = out->data;
+  for (int i = 0; i < 2; ++i) {
+    a.qs[i] = q->stride[i]; a.ks[i] = k->stride[i];
+    a.vs[i] = v->stride[i]; a.os[i] = out->stride[i];
+  }
+  a.cu = cu_seqlens; a.nseq = num_seqs; a.H = (int)H;
+  a.window = window < 0 ? -1 : window;
+  if (!(softmax_scale > 0.f) || !isfinite(softmax_scale))
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: softmax_scale must be > 0");
+  a.c2 = softmax_scale * VFK_LOG2E;
+  a.key_valid = key_valid;
+  a.rope = rope_theta > 0.f;
+  if (a.rope) {
+    // inv_freq exactly as the HF rotary module computes it in fp32:
+    // 1 / theta ** (arange(0, 64, 2).float() / 64)
+    for (int f = 0; f < 32; ++f) {
+      const float e = (float)(2 * f) / 64.0f;
+      const float inv = 1.0f / powf(rope_theta, e);
+      a.inv_freq[f] = inv;
+      a.inv_freq_rev[f] = inv / 6.283185307179586f;
+    }
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (dt == VFK_F32) {
+    a.nqt = ceil_div(max_seqlen, 128);
+    const int64_t blocks = (int64_t)a.nqt * 2 * H * num_seqs;
+    hipLaunchKernelGGL(varlen_fwd_f32_kernel, dim3((unsigned)blocks), dim3(64), 0, st, a,
+                       (const float*)nullptr);
+    return launch_status("vfk_varlen_attn_fwd");
+  }
+  a.nqt = ceil_div(max_seqlen, kBM);
+  const int64_t blocks = (int64_t)a.nqt * H * num_seqs;
+  if (blocks >= (1ll << 31))
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: grid too large");
+  const bool local = a.window >= 0, kv = key_valid != nullptr, rope = a.rope != 0;
+#define VFK_VL(E, R, L, K) \
+  hipLaunchKernelGGL((varlen_fwd_kernel<E, R, L, K>), dim3((unsigned)blocks), dim3(256), 0, st, a)
+#define VFK_VL_E(E)                                                   \
+  if (rope) {                                                         \
+    if (local) { if (kv) VFK_VL(E, true, true, true); else VFK_VL(E, true, true, false); } \
+    else { if (kv) VFK_VL(E, true, false, true); else VFK_VL(E, true, false, false); }    \
+  } else {                                                            \
+    if (local) { if (kv) VFK_VL(E, false, true, true); else VFK_VL(E, false, true, false); } \
+    else { if (kv) VFK_VL(E, false, false, true); else VFK_VL(E, false, false, false); }    \
+  }
+  if (dt == VFK_BF16) {
+    VFK_VL_E(BF16)
+  } else {
+    VFK_VL_E(F16)
+  }
+#undef VFK_VL_E
+#undef VFK_VL
+  return launch_status("vfk_varlen_attn_fwd");
+}

@@ -1,0 +1,601 @@
+// Memory-bound epilogues: RoPE (table form), LayerNorm, RMSNorm, gated
+// activations and residual add. All arithmetic is fp32 in registers; every
+// HBM access on the fast path is a 128-bit load or store.
+#include <math.h>
+
+#include "launch_util.h"
+#include "vfk_common.h"
+
+namespace vfk {
+
+// ---------------------------------------------------------------------------
+// Element access: VEC elements = 16 bytes.
+// ---------------------------------------------------------------------------
+template <int DT>
+struct Elt;
+
+template <>
+struct Elt<VFK_F32> {
+  static constexpr int VEC = 4;
+  __device__ static inline void load(const void* base, int64_t i, float* f) {
+    f32x4_t v = *reinterpret_cast<const f32x4_t*>(
+        reinterpret_cast<const float*>(base) + i);
+    f[0] = v[0]; f[1] = v[1]; f[2] = v[2]; f[3] = v[3];
+  }
+  __device__ static inline void store(void* base, int64_t i, const float* f) {
+    f32x4_t v = {f[0], f[1], f[2], f[3]};
+    *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(base) + i) = v;
+  }
+  __device__ static inline float ld1(const void* base, int64_t i) {
+    return reinterpret_cast<const float*>(base)[i];
+  }
+  __device__ static inline void st1(void* base, int64_t i, float v) {
+    reinterpret_cast<float*>(base)[i] = v;
+  }
+};
+
+template <typename E>
+struct Elt16 {
+  static constexpr int VEC = 8;
+  __device__ static inline void load(const void* base, int64_t i, float* f) {
+    u32x4_t v = *reinterpret_cast<const u32x4_t*>(
+        reinterpret_cast<const uint16_t*>(base) + i);
+    unpack8<E>(v, f);
+  }
+  __device__ static inline void store(void* base, int64_t i, const float* f) {
+    *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(base) + i) =
+        pack8<E>(f);
+  }
+  __device__ static inline float ld1(const void* base, int64_t i) {
+    return E::to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
+  }
+  __device__ static inline void st1(void* base, int64_t i, float v) {
+    reinterpret_cast<uint16_t*>(base)[i] = E::from_f32(v);
+  }
+};
+template <>
+struct Elt<VFK_BF16> : Elt16<BF16> {};
+template <>
+struct Elt<VFK_F16> : Elt16<F16> {};
+
+// Generic scalar access for mixed-dtype parameters (weights may differ).
+__device__ inline float ld_any(const void* base, int dt, int64_t i) {
+  if (dt == VFK_F32) return reinterpret_cast<const float*>(base)[i];
+  if (dt == VFK_BF16) return BF16::to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
+  return F16::to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
+}
+
+template <int LANES>
+__device__ inline float group_sum(float v) {
+#pragma unroll
+  for (int o = LANES / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm / RMSNorm (one group of LANES lanes per row)
+// ---------------------------------------------------------------------------
+struct NormArgs {
+  const void* x; int64_t x_rs;
+  const void* res; int64_t res_rs;        // optional residual added first
+  void* res_out; int64_t res_out_rs;      // optional: writes x + res
+  const void* w; int w_dt;                // optional weight
+  const void* b; int b_dt;                // optional bias (LayerNorm only)
+  void* y; int64_t y_rs;
+  int64_t rows; int n; float eps;
+};
+
+template <int DT, int LANES, int CH, bool RMS>
+__global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
+  using L = Elt<DT>;
+  constexpr int VEC = L::VEC;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane / LANES;
+  const int l = lane % LANES;
+  constexpr int RPW = 64 / LANES;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + wave) * RPW + sub;
+  const bool active = row < a.rows;
+  const int nch = a.n / VEC;
+  float x[CH][VEC];
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = c * LANES + l;
+    if (active && ch < nch) {
+      L::load(a.x, row * a.x_rs + (int64_t)ch * VEC, x[c]);
+      if (a.res) {
+        float r[VEC];
+        L::load(a.res, row * a.res_rs + (int64_t)ch * VEC, r);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) x[c][i] += r[i];
+        if (a.res_out) L::store(a.res_out, row * a.res_out_rs + (int64_t)ch * VEC, x[c]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) x[c][i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) s += RMS ? x[c][i] * x[c][i] : x[c][i];
+  }
+  s = group_sum<LANES>(s);
+  const float inv_n = 1.0f / (float)a.n;
+  float mean = 0.f, rstd;
+  if (RMS) {
+    rstd = 1.0f / sqrtf(s * inv_n + a.eps);
+  } else {
+    mean = s * inv_n;
+    float v = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int ch = c * LANES + l;
+      if (ch < nch) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          float d = x[c][i] - mean;
+          v += d * d;
+        }
+      }
+    }
+    v = group_sum<LANES>(v);
+    rstd = 1.0f / sqrtf(v * inv_n + a.eps);
+  }
+  if (!active) return;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = c * LANES + l;
+    if (ch < nch) {
+      float y[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const int col = ch * VEC + i;
+        float t = (x[c][i] - mean) * rstd;
+        if (a.w) t *= ld_any(a.w, a.w_dt, col);
+        if (!RMS && a.b) t += ld_any(a.b, a.b_dt, col);
+        y[i] = t;
+      }
+      L::store(a.y, row * a.y_rs + (int64_t)ch * VEC, y);
+    }
+  }
+}
+
+// Any width / alignment: one 256-thread block per row, LDS reduction.
+template <int DT, bool RMS>
+__global__ __launch_bounds__(256) void norm_scalar_kernel(NormArgs a) {
+  using L = Elt<DT>;
+  const int64_t row = blockIdx.x;
+  __shared__ float red[8];
+  float s = 0.f;
+  for (int c = threadIdx.x; c < a.n; c += 256) {
+    float v = L::ld1(a.x, row * a.x_rs + c);
+    if (a.res) v += L::ld1(a.res, row * a.res_rs + c);
+    s += RMS ? v * v : v;
+  }
+  s = group_sum<64>(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  s = red[0] + red[1] + red[2] + red[3];
+  __syncthreads();
+  const float inv_n = 1.0f / (float)a.n;
+  float mean = 0.f, rstd;
+  if (RMS) {
+    rstd = 1.0f / sqrtf(s * inv_n + a.eps);
+  } else {
+    mean = s * inv_n;
+    float v2 = 0.f;
+    for (int c = threadIdx.x; c < a.n; c += 256) {
+      float v = L::ld1(a.x, row * a.x_rs + c);
+      if (a.res) v += L::ld1(a.res, row * a.res_rs + c);
+      v2 += (v - mean) * (v - mean);
+    }
+    v2 = group_sum<64>(v2);
+    if ((threadIdx.x & 63) == 0) red[4 + (threadIdx.x >> 6)] = v2;
+    __syncthreads();
+    v2 = red[4] + red[5] + red[6] + red[7];
+    rstd = 1.0f / sqrtf(v2 * inv_n + a.eps);
+  }
+  for (int c = threadIdx.x; c < a.n; c += 256) {
+    float v = L::ld1(a.x, row * a.x_rs + c);
+    if (a.res) {
+      v += L::ld1(a.res, row * a.res_rs + c);
+      if (a.res_out) L::st1(a.res_out, row * a.res_out_rs + c, v);
+    }
+    float t = (v - mean) * rstd;
+    if (a.w) t *= ld_any(a.w, a.w_dt, c);
+    if (!RMS && a.b) t += ld_any(a.b, a.b_dt, c);
+    L::st1(a.y, row * a.y_rs + c, t);
+  }
+}
+
+template <int DT, int LANES, bool RMS>
+static void launch_norm_vec(const NormArgs& a, int ch, hipStream_t st) {
+  const int rows_per_block = 4 * (64 / LANES);
+  dim3 grid(ceil_div(a.rows, rows_per_block));
+#define VFK_NORM_CASE(C)                                                   \
+  case C:                                                                  \
+    hipLaunchKernelGGL((norm_vec_kernel<DT, LANES, C, RMS>), grid, dim3(256), \
+                       0, st, a);                                          \
+    break;
+  switch (ch) {
+    VFK_NORM_CASE(1)
+    VFK_NORM_CASE(2)
+    VFK_NORM_CASE(3)
+    VFK_NORM_CASE(4)
+    VFK_NORM_CASE(6)
+    VFK_NORM_CASE(8)
+    VFK_NORM_CASE(12)
+    VFK_NORM_CASE(16)
+  }
+#undef VFK_NORM_CASE
+}
+
+static int pick_ch(int need) {
+  static const int opts[] = {1, 2, 3, 4, 6, 8, 12, 16};
+  for (int o : opts)
+    if (o >= need) return o;
+  return 0;
+}
+
+template <int DT, bool RMS>
+static void dispatch_norm(const NormArgs& a, bool vec_ok, hipStream_t st) {
+  constexpr int VEC = Elt<DT>::VEC;
+  const int nch = a.n / VEC;
+  if (vec_ok) {
+    const int lanes = (nch % 64 == 0 || nch > 96) ? 64 : 32;
+    const int ch = pick_ch((nch + lanes - 1) / lanes);
+    if (ch) {
+      if (lanes == 64)
+        launch_norm_vec<DT, 64, RMS>(a, ch, st);
+      else
+        launch_norm_vec<DT, 32, RMS>(a, ch, st);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((norm_scalar_kernel<DT, RMS>), dim3((unsigned)a.rows),
+                     dim3(256), 0, st, a);
+}
+
+static int norm_entry(const vfk_tensor* x, const vfk_tensor* residual,
+                      const vfk_tensor* weight, const vfk_tensor* bias,
+                      float eps, vfk_tensor* out, vfk_tensor* residual_out,
+                      void* stream, bool rms, const char* name) {
+  int rc;
+  if ((rc = check_tensor(x, "x", 2)) || (rc = check_tensor(out, "out", 2)))
+    return rc;
+  const int64_t rows = x->size[0], n = x->size[1];
+  if (n <= 0 || rows < 0 || n > (1 << 30))
+    return set_error(VFK_ERR_INVALID, "%s: bad shape [%lld, %lld]", name,
+                     (long long)rows, (long long)n);
+  if (out->size[0] != rows || out->size[1] != n || out->dtype != x->dtype)
+    return set_error(VFK_ERR_INVALID, "%s: out must match x", name);
+  if (x->stride[1] != 1 || out->stride[1] != 1)
+    return set_error(VFK_ERR_INVALID, "%s: last dim must be contiguous", name);
+  NormArgs a = {};
+  a.x = x->data; a.x_rs = x->stride[0];
+  a.y = out->data; a.y_rs = out->stride[0];
+  a.rows = rows; a.n = (int)n; a.eps = eps;
+  bool vec_ok = aligned16(x->data) && aligned16(out->data);
+  const int es = elem_size(x->dtype);
+  const int VEC = 16 / es;
+  if (n % VEC || a.x_rs % VEC || a.y_rs % VEC) vec_ok = false;
+  if (present(residual)) {
+    if ((rc = check_tensor(residual, "residual", 2))) return rc;
+    if (residual->size[0] != rows || residual->size[1] != n ||
+        residual->dtype != x->dtype || residual->stride[1] != 1)
+      return set_error(VFK_ERR_INVALID, "%s: residual must match x", name);
+    a.res = residual->data; a.res_rs = residual->stride[0];
+    if (!aligned16(a.res) || a.res_rs % VEC) vec_ok = false;
+    if (present(residual_out)) {
+      if ((rc = check_tensor(residual_out, "residual_out", 2))) return rc;
+      if (residual_out->size[0] != rows || residual_out->size[1] != n ||
+          residual_out->dtype != x->dtype || residual_out->stride[1] != 1)
+        return set_error(VFK_ERR_INVALID, "%s: residual_out must match x", name);
+      a.res_out = residual_out->data; a.res_out_rs = residual_out->stride[0];
+      if (!aligned16(a.res_out) || a.res_out_rs % VEC) vec_ok = false;
+    }
+  } else if (present(residual_out)) {
+    return set_error(VFK_ERR_INVALID, "%s: residual_out needs residual", name);
+  }
+  if (present(weight)) {
+    if ((rc = check_tensor(weight, "weight", 1))) return rc;
+    if (weight->size[0] != n || weight->stride[0] != 1)
+      return set_error(VFK_ERR_INVALID, "%s: weight must be contiguous [n]", name);
+    a.w = weight->data; a.w_dt = weight->dtype;
+  }
+  if (present(bias)) {
+    if ((rc = check_tensor(bias, "bias", 1))) return rc;
+    if (bias->size[0] != n || bias->stride[0] != 1)
+      return set_error(VFK_ERR_INVALID, "%s: bias must be contiguous [n]", name);
+    a.b = bias->data; a.b_dt = bias->dtype;
+  }
+  if (rows == 0) return VFK_OK;
+  hipStream_t st = (hipStream_t)stream;
+  switch (x->dtype) {
+    case VFK_F32:
+      rms ? dispatch_norm<VFK_F32, true>(a, vec_ok, st)
+          : dispatch_norm<VFK_F32, false>(a, vec_ok, st);
+      break;
+    case VFK_BF16:
+      rms ? dispatch_norm<VFK_BF16, true>(a, vec_ok, st)
+          : dispatch_norm<VFK_BF16, false>(a, vec_ok, st);
+      break;
+    case VFK_F16:
+      rms ? dispatch_norm<VFK_F16, true>(a, vec_ok, st)
+          : dispatch_norm<VFK_F16, false>(a, vec_ok, st);
+      break;
+  }
+  return launch_status(name);
+}
+
+// ---------------------------------------------------------------------------
+// Gated activations and residual add over [rows, n] with row strides.
+// ---------------------------------------------------------------------------
+struct BinArgs {
+  const void* a; int64_t a_rs;
+  const void* b; int64_t b_rs;
+  void* y; int64_t y_rs;
+  int64_t rows; int64_t n;
+};
+
+#define VFK_OP_ADD 100
+
+template <int OP>
+__device__ inline float apply_op(float a, float b) {
+  if (OP == VFK_ACT_GELU_ERF) return 0.5f * a * (1.0f + erff(a * 0.70710678118654752f)) * b;
+  if (OP == VFK_ACT_GELU_TANH) {
+    const float inner = 0.7978845608028654f * (a + 0.044715f * a * a * a);
+    return 0.5f * a * (1.0f + tanhf(inner)) * b;
+  }
+  if (OP == VFK_ACT_SILU) return a / (1.0f + expf(-a)) * b;
+  if (OP == VFK_ACT_RELU) return fmaxf(a, 0.f) * b;
+  return a + b;  // VFK_OP_ADD
+}
+
+template <int DT, int OP>
+__global__ __launch_bounds__(256) void binary_vec_kernel(BinArgs p) {
+  using L = Elt<DT>;
+  constexpr int VEC = L::VEC;
+  const int64_t cpr = p.n / VEC;
+  const int64_t total = p.rows * cpr;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total;
+       c += (int64_t)gridDim.x * 256) {
+    const int64_t r = c / cpr;
+    const int64_t col = (c - r * cpr) * VEC;
+    float x[VEC], y[VEC];
+    L::load(p.a, r * p.a_rs + col, x);
+    L::load(p.b, r * p.b_rs + col, y);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) x[i] = apply_op<OP>(x[i], y[i]);
+    L::store(p.y, r * p.y_rs + col, x);
+  }
+}
+
+template <int DT, int OP>
+__global__ __launch_bounds__(256) void binary_scalar_kernel(BinArgs p) {
+  using L = Elt<DT>;
+  const int64_t total = p.rows * p.n;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total;
+       c += (int64_t)gridDim.x * 256) {
+    const int64_t r = c / p.n;
+    const int64_t col = c - r * p.n;
+    L::st1(p.y, r * p.y_rs + col,
+           apply_op<OP>(L::ld1(p.a, r * p.a_rs + col), L::ld1(p.b, r * p.b_rs + col)));
+  }
+}
+
+template <int DT, int OP>
+static void launch_binary(const BinArgs& p, bool vec_ok, hipStream_t st) {
+  constexpr int VEC = Elt<DT>::VEC;
+  const int64_t work = vec_ok ? p.rows * (p.n / VEC) : p.rows * p.n;
+  // enough blocks to fill 256 CUs several times; the loop covers the rest
+  int64_t blocks = (work + 255) / 256;
+  if (blocks > 256 * 16) blocks = 256 * 16;
+  if (blocks < 1) blocks = 1;
+  if (vec_ok)
+    hipLaunchKernelGGL((binary_vec_kernel<DT, OP>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((binary_scalar_kernel<DT, OP>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+}
+
+template <int OP>
+static void dispatch_binary(int dt, const BinArgs& p, bool vec_ok, hipStream_t st) {
+  switch (dt) {
+    case VFK_F32: launch_binary<VFK_F32, OP>(p, vec_ok, st); break;
+    case VFK_BF16: launch_binary<VFK_BF16, OP>(p, vec_ok, st); break;
+    case VFK_F16: launch_binary<VFK_F16, OP>(p, vec_ok, st); break;
+  }
+}
+
+static int binary_entry(int op, const vfk_tensor* a, const vfk_tensor* b,
+                        vfk_tensor* out, void* stream, const char* name) {
+  int rc;
+  if ((rc = check_tensor(a, "a", 2)) || (rc = check_tensor(b, "b", 2)) ||
+      (rc = check_tensor(out, "out", 2)))
+    return rc;
+  const int64_t rows = a->size[0], n = a->size[1];
+  if (b->size[0] != rows || b->size[1] != n || out->size[0] != rows ||
+      out->size[1] != n)
+    return set_error(VFK_ERR_INVALID, "%s: shape mismatch", name);
+  if (b->dtype != a->dtype || out->dtype != a->dtype)
+    return set_error(VFK_ERR_INVALID, "%s: dtype mismatch", name);
+  if (a->stride[1] != 1 || b->stride[1] != 1 || out->stride[1] != 1)
+    return set_error(VFK_ERR_INVALID, "%s: last dim must be contiguous", name);
+  if (rows == 0 || n == 0) return VFK_OK;
+  BinArgs p = {a->data, a->stride[0], b->data, b->stride[0],
+               out->data, out->stride[0], rows, n};
+  const int VEC = 16 / elem_size(a->dtype);
+  const bool vec_ok = aligned16(a->data) && aligned16(b->data) &&
+                      aligned16(out->data) && n % VEC == 0 &&
+                      p.a_rs % VEC == 0 && p.b_rs % VEC == 0 &&
+                      p.y_rs % VEC == 0;
+  hipStream_t st = (hipStream_t)stream;
+  switch (op) {
+    case VFK_ACT_GELU_ERF: dispatch_binary<VFK_ACT_GELU_ERF>(a->dtype, p, vec_ok, st); break;
+    case VFK_ACT_GELU_TANH: dispatch_binary<VFK_ACT_GELU_TANH>(a->dtype, p, vec_ok, st); break;
+    case VFK_ACT_SILU: dispatch_binary<VFK_ACT_SILU>(a->dtype, p, vec_ok, st); break;
+    case VFK_ACT_RELU: dispatch_binary<VFK_ACT_RELU>(a->dtype, p, vec_ok, st); break;
+    case VFK_OP_ADD: dispatch_binary<VFK_OP_ADD>(a->dtype, p, vec_ok, st); break;
+    default: return set_error(VFK_ERR_INVALID, "%s: unknown activation %d", name, op);
+  }
+  return launch_status(name);
+}
+
+// ---------------------------------------------------------------------------
+// RoPE with explicit cos/sin tables, x [B,S,H,D], cos/sin [B,S,D].
+// ---------------------------------------------------------------------------
+struct RopeArgs {
+  const void* x; int64_t xs[4];
+  const void* c; int64_t cs[3];
+  const void* s; int64_t ss[3];
+  void* y; int64_t ys[4];
+  int64_t B, S, H; int D;
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs p) {
+  using L = Elt<DT>;
+  constexpr int VEC = L::VEC;
+  const int half = p.D / 2;
+  const int cpr = half / VEC;  // chunk pairs per row
+  const int64_t total = p.B * p.S * p.H * cpr;
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * 256) {
+    int64_t r = t / cpr;
+    const int d0 = (int)(t - r * cpr) * VEC;
+    const int64_t h = r % p.H; r /= p.H;
+    const int64_t s = r % p.S;
+    const int64_t b = r / p.S;
+    const int64_t xo = b * p.xs[0] + s * p.xs[1] + h * p.xs[2];
+    const int64_t yo = b * p.ys[0] + s * p.ys[1] + h * p.ys[2];
+    const int64_t co = b * p.cs[0] + s * p.cs[1];
+    const int64_t so = b * p.ss[0] + s * p.ss[1];
+    float x1[VEC], x2[VEC], c1[VEC], c2[VEC], s1[VEC], s2[VEC];
+    L::load(p.x, xo + d0, x1);
+    L::load(p.x, xo + d0 + half, x2);
+    L::load(p.c, co + d0, c1);
+    L::load(p.c, co + d0 + half, c2);
+    L::load(p.s, so + d0, s1);
+    L::load(p.s, so + d0 + half, s2);
+    float y1[VEC], y2[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      y1[i] = x1[i] * c1[i] - x2[i] * s1[i];
+      y2[i] = x2[i] * c2[i] + x1[i] * s2[i];
+    }
+    L::store(p.y, yo + d0, y1);
+    L::store(p.y, yo + d0 + half, y2);
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void rope_scalar_kernel(RopeArgs p) {
+  using L = Elt<DT>;
+  const int half = p.D / 2;
+  const int64_t total = p.B * p.S * p.H * p.D;
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * 256) {
+    int64_t r = t / p.D;
+    const int d = (int)(t - r * p.D);
+    const int64_t h = r % p.H; r /= p.H;
+    const int64_t s = r % p.S;
+    const int64_t b = r / p.S;
+    const int64_t xo = b * p.xs[0] + s * p.xs[1] + h * p.xs[2];
+    const float x = L::ld1(p.x, xo + d * p.xs[3]);
+    const int pd = d < half ? d + half : d - half;
+    const float xp = L::ld1(p.x, xo + pd * p.xs[3]);
+    const float c = L::ld1(p.c, b * p.cs[0] + s * p.cs[1] + d * p.cs[2]);
+    const float sn = L::ld1(p.s, b * p.ss[0] + s * p.ss[1] + d * p.ss[2]);
+    const float y = d < half ? x * c - xp * sn : x * c + xp * sn;
+    L::st1(p.y, b * p.ys[0] + s * p.ys[1] + h * p.ys[2] + d * p.ys[3], y);
+  }
+}
+
+}  // namespace vfk
+
+using namespace vfk;
+
+extern "C" int vfk_layernorm_fwd(const vfk_tensor* x, const vfk_tensor* residual,
+                                 const vfk_tensor* weight, const vfk_tensor* bias,
+                                 float eps, vfk_tensor* out,
+                                 vfk_tensor* residual_out, void* stream) {
+  return norm_entry(x, residual, weight, bias, eps, out, residual_out, stream,
+                    false, "vfk_layernorm_fwd");
+}
+
+extern "C" int vfk_rmsnorm_fwd(const vfk_tensor* x, const vfk_tensor* residual,
+                               const vfk_tensor* weight, float eps,
+                               vfk_tensor* out, vfk_tensor* residual_out,
+                               void* stream) {
+  return norm_entry(x, residual, weight, nullptr, eps, out, residual_out,
+                    stream, true, "vfk_rmsnorm_fwd");
+}
+
+extern "C" int vfk_glu_fwd(int32_t act, const vfk_tensor* a,
+                           const vfk_tensor* b, vfk_tensor* out, void* stream) {
+  if (act < VFK_ACT_GELU_ERF || act > VFK_ACT_RELU)
+    return set_error(VFK_ERR_INVALID, "vfk_glu_fwd: unknown activation %d", act);
+  return binary_entry(act, a, b, out, stream, "vfk_glu_fwd");
+}
+
+extern "C" int vfk_residual_add(const vfk_tensor* a, const vfk_tensor* b,
+                                vfk_tensor* out, void* stream) {
+  return binary_entry(VFK_OP_ADD, a, b, out, stream, "vfk_residual_add");
+}
+
+extern "C" int vfk_rope_fwd(const vfk_tensor* x, const vfk_tensor* cos,
+                            const vfk_tensor* sin, vfk_tensor* out,
+                            void* stream) {
+  int rc;
+  if ((rc = check_tensor(x, "x", 4)) || (rc = check_tensor(out, "out", 4)) ||
+      (rc = check_tensor(cos, "cos", 3)) || (rc = check_tensor(sin, "sin", 3)))
+    return rc;
+  const int64_t B = x->size[0], S = x->size[1], H = x->size[2], D = x->size[3];
+  for (int i = 0; i < 4; ++i)
+    if (out->size[i] != x->size[i])
+      return set_error(VFK_ERR_INVALID, "vfk_rope_fwd: out shape mismatch");
+  if (D % 2 || D <= 0)
+    return set_error(VFK_ERR_INVALID, "vfk_rope_fwd: head_dim must be even");
+  const vfk_tensor* cs[2] = {cos, sin};
+  for (const vfk_tensor* t : cs) {
+    if ((t->size[0] != B && t->size[0] != 1) || t->size[1] != S || t->size[2] != D)
+      return set_error(VFK_ERR_INVALID, "vfk_rope_fwd: cos/sin must be [B|1,S,D]");
+    if (t->dtype != x->dtype)
+      return set_error(VFK_ERR_INVALID, "vfk_rope_fwd: cos/sin dtype must match x");
+  }
+  if (out->dtype != x->dtype)
+    return set_error(VFK_ERR_INVALID, "vfk_rope_fwd: out dtype must match x");
+  RopeArgs p = {};
+  p.x = x->data; p.c = cos->data; p.s = sin->data; p.y = out->data;
+  for (int i = 0; i < 4; ++i) { p.xs[i] = x->stride[i]; p.ys[i] = out->stride[i]; }
+  for (int i = 0; i < 3; ++i) { p.cs[i] = cos->stride[i]; p.ss[i] = sin->stride[i]; }
+  if (cos->size[0] == 1) p.cs[0] = 0;
+  if (sin->size[0] == 1) p.ss[0] = 0;
+  p.B = B; p.S = S; p.H = H; p.D = (int)D;
+  const int64_t rows = B * S * H;
+  if (rows == 0) return VFK_OK;
+  const int VEC = 16 / elem_size(x->dtype);
+  bool vec_ok = (D / 2) % VEC == 0 && x->stride[3] == 1 && out->stride[3] == 1 &&
+                cos->stride[2] == 1 && sin->stride[2] == 1 &&
+                aligned16(x->data) && aligned16(out->data) &&
+                aligned16(cos->data) && aligned16(sin->data);
+  for (int i = 0; i < 3; ++i)
+    vec_ok = vec_ok && p.xs[i] % VEC == 0 && p.ys[i] % VEC == 0;
+  for (int i = 0; i < 2; ++i)
+    vec_ok = vec_ok && p.cs[i] % VEC == 0 && p.ss[i] % VEC == 0;
+  const int64_t work = vec_ok ? rows * (D / 2 / VEC) : rows * D;
+  int64_t blocks = (work + 255) / 256;
+  if (blocks > 256 * 16) blocks = 256 * 16;
+  hipStream_t st = (hipStream_t)stream;
+#define VFK_ROPE(DT)                                                               \
+  if (vec_ok)                                                                      \
+    hipLaunchKernelGGL((rope_vec_kernel<DT>), dim3((unsigned)blocks), dim3(256), 0, st, p); \
+  else                                                                             \
+    hipLaunchKernelGGL((rope_scalar_kernel<DT>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  switch (x->dtype) {
+    case VFK_F32: VFK_ROPE(VFK_F32); break;
+    case VFK_BF16: VFK_ROPE(VFK_BF16); break;
+    case VFK_F16: VFK_ROPE(VFK_F16); break;
+  }
+#undef VFK_ROPE
+  return launch_status("vfk_rope_fwd");
+}

@@ -1,0 +1,121 @@
+// Shared definitions for the libvfk HIP kernels (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/vfk.h"
+#include "vfk_host.h"
+
+// ---------------------------------------------------------------------------
+// Vector types used as MFMA operands and for 128-bit memory traffic.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+#define VFK_LOG2E 1.4426950408889634f
+#define VFK_NUM_XCD 8
+
+namespace vfk {
+
+// Element type tags. Storage of 16-bit types is raw uint16_t bits.
+struct BF16 {
+  static constexpr int code = VFK_BF16;
+  typedef bf16x8_t vec8;
+  __device__ static inline float to_f32(uint16_t b) {
+    return __uint_as_float(((uint32_t)b) << 16);
+  }
+  __device__ static inline uint16_t from_f32(float f) {
+    __bf16 h = (__bf16)f;
+    return __builtin_bit_cast(uint16_t, h);
+  }
+  // two floats -> packed pair (lo = a)
+  __device__ static inline uint32_t pack2(float a, float b) {
+    f32x2_t v = {a, b};
+    bf16x2_t h = __builtin_convertvector(v, bf16x2_t);
+    return __builtin_bit_cast(uint32_t, h);
+  }
+  __device__ static inline f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+        0, 0, 0);
+  }
+};
+
+struct F16 {
+  static constexpr int code = VFK_F16;
+  typedef f16x8_t vec8;
+  __device__ static inline float to_f32(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+  }
+  __device__ static inline uint16_t from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+  __device__ static inline uint32_t pack2(float a, float b) {
+    f32x2_t v = {a, b};
+    f16x2_t h = __builtin_convertvector(v, f16x2_t);
+    return __builtin_bit_cast(uint32_t, h);
+  }
+  __device__ static inline f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        __builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
+        0, 0);
+  }
+};
+
+// Unpack eight 16-bit values held in a u32x4 into floats.
+template <typename E>
+__device__ inline void unpack8(u32x4_t v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = E::to_f32((uint16_t)(v[i] & 0xffffu));
+    f[2 * i + 1] = E::to_f32((uint16_t)(v[i] >> 16));
+  }
+}
+
+template <typename E>
+__device__ inline u32x4_t pack8(const float* f) {
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = E::pack2(f[2 * i], f[2 * i + 1]);
+  return r;
+}
+
+// Max of a value with the lane 32 positions away (the two half-waves hold
+// the same attention row in the S^T layout used by the attention kernels).
+__device__ inline float half_swap_max(float x) {
+  int xi = __float_as_int(x);
+  auto r = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+__device__ inline float half_swap_sum(float x) {
+  int xi = __float_as_int(x);
+  auto r = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+// L2. Remap the hardware block id so that consecutive work items (which
+// share K/V rows) run on the same XCD.
+__device__ inline int xcd_remap(int bid, int n) {
+  int xcd = bid % VFK_NUM_XCD;
+  int slot = bid / VFK_NUM_XCD;
+  int per = n / VFK_NUM_XCD;
+  int rem = n % VFK_NUM_XCD;
+  if (xcd < rem) return xcd * (per + 1) + slot;
+  return rem * (per + 1) + (xcd - rem) * per + slot;
+}
+
+}  // namespace vfk
+
