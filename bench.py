@@ -1,0 +1,266 @@
+#!/usr/bin/env python3
+"""Benchmark of the encoder-attention hot path on one MI355X.
+
+Headline (one JSON line): ModernBERT-base attention on a varlen pack of 64
+sequences with lengths U{512..768} (bf16, 12 heads, d 64). One step = one
+global layer (RoPE theta 160000, full attention within each sequence) plus one
+local layer (RoPE theta 10000, window +-64), both with RoPE applied in the
+kernel. `value` = algorithmic attention TFLOP/s over valid pairs only:
+sum_s 4*d*H*len_s^2 (global) + 4*d*H*#{|i-j| <= 64} (local).
+
+Extra figures in the same line: per-kernel roofline of the dominant kernel,
+the T5 RPB attention at mT5-large shapes, the DeBERTa disentangled attention,
+the memory-bound epilogues in GB/s, and the CPU oracle timed on the host.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--only headline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "vllm-factory_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+class KernelTimer:
+    """Per-launch HIP-event timing on the current stream (the one the kernels use)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.ms = {}
+
+    def run(self, name, fn):
+        s, e = _events(self.torch)
+        s.record()
+        out = fn()
+        e.record()
+        self.ms.setdefault(name, []).append((s, e))
+        return out
+
+    def avg_ms(self, name):
+        ev = self.ms[name]
+        return sum(s.elapsed_time(e) for s, e in ev) / len(ev)
+
+    def reset(self):
+        self.ms = {}
+
+
+def headline(torch, args):
+    import workloads
+    from kernels.varlen_attention import varlen_rope_attention
+
+    dev = torch.device("cuda:0")
+    c = workloads.config2(device=dev)
+    q, k, v = c.qkv[:, 0], c.qkv[:, 1], c.qkv[:, 2]
+    lens = c.lengths.tolist()
+    H, d = 12, 64
+    fl_global = sum(4 * d * H * n * n for n in lens)
+    fl_local = sum(4 * d * H * workloads.window_pairs(n, 64) for n in lens)
+    out_g = torch.empty_like(q)
+    out_l = torch.empty_like(q)
+    timer = KernelTimer(torch)
+
+    def step():
+        timer.run("global", lambda: varlen_rope_attention(q, k, v, c.cu_seqlens, c.max_seqlen, -1,
+                                                           160000.0, 0.125, out=out_g))
+        timer.run("local", lambda: varlen_rope_attention(q, k, v, c.cu_seqlens, c.max_seqlen, 64,
+                                                          10000.0, 0.125, out=out_l))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    g_ms, l_ms = timer.avg_ms("global"), timer.avg_ms("local")
+    value = (fl_global + fl_local) / (ms_step * 1e-3) / 1e12
+    g_tf = fl_global / (g_ms * 1e-3) / 1e12
+    l_tf = fl_local / (l_ms * 1e-3) / 1e12
+    return dict(
+        value=value, ms_per_step=ms_step, tokens=int(sum(lens)),
+        roofline=dict(bound="mfma", kernel="varlen_fwd_kernel (global, RoPE theta 160000)",
+                      achieved=g_tf, peak=PEAK_BF16_TFLOPS, unit="TFLOP/s", frac=g_tf / PEAK_BF16_TFLOPS,
+                      traffic=None, flops_per_launch=fl_global, avg_launch_ms=g_ms),
+        kernels=dict(
+            global_attn=dict(ms=g_ms, tflops=g_tf, gflop=fl_global / 1e9, frac=g_tf / PEAK_BF16_TFLOPS),
+            local_attn=dict(ms=l_ms, tflops=l_tf, gflop=fl_local / 1e9, frac=l_tf / PEAK_BF16_TFLOPS),
+        ),
+    ), c
+
+
+def rpb_config4(torch, args):
+    """mT5-large RPB attention at config 4 shapes (B=32, L=768, lens U{512..768})."""
+    import workloads
+    from kernels.flash_attention_rpb import flash_attention_rpb_final
+
+    dev = torch.device("cuda:0")
+    c = workloads.config4(device=dev)
+    B, L = c.hidden.shape[:2]
+    g = torch.Generator().manual_seed(1004)
+    q, k, v = ((torch.randn(B, 16, L, 64, generator=g) * 0.64).bfloat16().to(dev) for _ in range(3))
+    lens = c.lengths.tolist()
+    flops = sum(4 * 64 * 16 * n * n for n in lens)
+    timer = KernelTimer(torch)
+    fn = lambda: flash_attention_rpb_final(q, k, v, c.table, 32, 128, False, padding_mask=c.mask)
+    for _ in range(args.warmup):
+        fn()
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        timer.run("rpb", fn)
+    torch.cuda.synchronize()
+    ms = timer.avg_ms("rpb")
+    tf = flops / (ms * 1e-3) / 1e12
+    return dict(ms=ms, tflops=tf, gflop=flops / 1e9, frac=tf / PEAK_BF16_TFLOPS,
+                note="queries and keys of padded rows excluded from the FLOP count")
+
+
+def epilogue_bench(torch, args, c2):
+    import workloads
+    from kernels.fused_layernorm import fused_layernorm
+    from kernels.fused_rope_global import fused_rope_global_apply
+    from kernels.rms_norm import rms_norm
+    from kernels.ff_fused import fused_gelu_mul_dropout as ffg
+
+    dev = torch.device("cuda:0")
+    T = c2.qkv.shape[0]
+    res = {}
+    timer = KernelTimer(torch)
+
+    def bench(name, fn, nbytes):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            timer.run(name, fn)
+        torch.cuda.synchronize()
+        ms = timer.avg_ms(name)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = dict(ms=ms, gbs=gbs, mb=nbytes / 1e6, frac=gbs / PEAK_HBM_GBS)
+
+    # RoPE (table form, the drop-in kernel): q, k [1, T, 12, 64] bf16, cos/sin [1, T, 64]
+    q = c2.qkv[:, 0].contiguous().view(1, T, 12, 64)
+    k = c2.qkv[:, 1].contiguous().view(1, T, 12, 64)
+    pos = torch.cat([torch.arange(int(n)) for n in c2.lengths]).to(dev)
+    inv = 1.0 / (160000.0 ** (torch.arange(0, 64, 2, device=dev).float() / 64))
+    fr = pos.float()[:, None] * inv[None]
+    emb = torch.cat([fr, fr], -1)
+    cos, sin = emb.cos().bfloat16()[None], emb.sin().bfloat16()[None]
+    bench("rope_qk", lambda: fused_rope_global_apply(q, k, cos, sin), 4 * T * 768 * 2 + 2 * T * 64 * 2)
+    # LayerNorm [T, 768] bf16, no bias (ModernBERT)
+    g = torch.Generator().manual_seed(1002)
+    x = torch.randn(T, 768, generator=g).bfloat16().to(dev)
+    w = torch.ones(768, dtype=torch.bfloat16, device=dev)
+    bench("layernorm", lambda: fused_layernorm(x, 768, w, None, 1e-5), 2 * T * 768 * 2)
+    # mT5 RMSNorm and gated-GELU at config 4 shapes (valid tokens only counted)
+    c4 = workloads.config4(device=dev)
+    tv = int(c4.lengths.sum())
+    h = c4.hidden.reshape(-1, 1024)
+    bench("rmsnorm", lambda: rms_norm(h, c4.ln1, 1e-6), 2 * h.shape[0] * 1024 * 2)
+    res["rmsnorm"]["valid_token_mb"] = 2 * tv * 1024 * 2 / 1e6
+    gate = torch.randn(32 * 768, 2816, generator=g).bfloat16().to(dev)
+    up = torch.randn(32 * 768, 2816, generator=g).bfloat16().to(dev)
+    bench("gated_gelu", lambda: ffg(gate, up, "gelu_new"), 3 * gate.numel() * 2)
+    del c4
+    return res
+
+
+def cpu_baseline(torch, c2, max_seconds=20.0):
+    """The oracle (CPU restatement of the reference's eager path, fp32) on the
+    host cores: global + local attention for as many config-2 sequences as
+    fit in ~max_seconds, reported as TFLOP/s of the same algorithmic count."""
+    sys.path.insert(0, ROOT)
+    import workloads
+    from oracle import attention as oa
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    qkv = c2.qkv.float().cpu()
+    cu = c2.cu_seqlens.cpu().tolist()
+    lens = c2.lengths.tolist()
+    flops = 0
+    done = 0
+    t0 = time.perf_counter()
+    for s in range(len(lens)):
+        a, b = cu[s], cu[s + 1]
+        sub = qkv[a:b]
+        cus = torch.tensor([0, b - a], dtype=torch.int32)
+        oa.varlen_attention(sub[:, 0], sub[:, 1], sub[:, 2], cus, -1, 160000.0, None, 0.125)
+        oa.varlen_attention(sub[:, 0], sub[:, 1], sub[:, 2], cus, 64, 10000.0, None, 0.125)
+        n = b - a
+        flops += 4 * 64 * 12 * (n * n + workloads.window_pairs(n, 64))
+        done += 1
+        if time.perf_counter() - t0 > max_seconds:
+            break
+    dt = time.perf_counter() - t0
+    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                sample=f"{done} of {len(lens)} config-2 sequences, global + local layer, fp32 oracle "
+                       f"(per-sequence dense softmax), {dt:.1f} s")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="'headline' to skip the extra figures")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path is "
+              "data-parallel with no exchange step: N GPUs each run the same kernels on their "
+              "share of sequences)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    head, c2 = headline(torch, args)
+    extra = {}
+    if args.only != "headline":
+        extra["rpb_mt5_large_config4"] = rpb_config4(torch, args)
+        extra["epilogues"] = epilogue_bench(torch, args, c2)
+    line = {
+        "metric": "encoder attn TFLOP/s + % bf16 MFMA peak at L=512-768; end-to-end tokens/s",
+        "value": head["value"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded, random-init Wqkv ~ N(0,0.02))",
+        "config": {"workload": "ModernBERT-base attention, 64 varlen-packed sequences U{512..768} "
+                               "(T=%d), 12 heads x 64, global (RoPE 160000) + local +-64 (RoPE 10000)"
+                               % head["tokens"],
+                   "global_batch": 64, "seq_len": "512-768", "parallelism": "none (1 GPU)"},
+        "roofline": head["roofline"],
+        "kernels": head["kernels"],
+        "extra": extra,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(torch, c2)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

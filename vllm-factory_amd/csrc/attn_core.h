@@ -126,10 +126,13 @@ __device__ inline int x_key(int i, int h) {
 // masked); c = softmax scale * log2(e), so p = exp2(c * (x - m)) is one FMA
 // and one exp2 per score. m: running reference max in raw units; l: this
 // lane's partial row sum.
+// exact: evaluate (x - m) * c instead of fma(x, c, -m*c). Needed when x may
+// carry a huge finite additive mask (|x| ~ 1e30): the rounding of m*c alone
+// would then exceed the whole exponent range, while x - m stays exact.
 template <typename E>
 __device__ inline void softmax_tile(float (&x)[32], float c, float& m, float& l,
                                     f32x16_t& o0, f32x16_t& o1,
-                                    u32x4_t (&p)[4]) {
+                                    u32x4_t (&p)[4], bool exact = false) {
   float mx = x[0];
 #pragma unroll
   for (int i = 1; i < 32; ++i) mx = fmaxf(mx, x[i]);
@@ -147,12 +150,21 @@ __device__ inline void softmax_tile(float (&x)[32], float c, float& m, float& l,
       m = m_new;
     }
   }
-  const float nmc = (m == -INFINITY) ? 0.f : -m * c;
   float sum = 0.f;
+  if (exact) {
+    const float ms = (m == -INFINITY) ? 0.f : m;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    x[i] = fast_exp2(__builtin_fmaf(x[i], c, nmc));
-    sum += x[i];
+    for (int i = 0; i < 32; ++i) {
+      x[i] = fast_exp2((x[i] - ms) * c);
+      sum += x[i];
+    }
+  } else {
+    const float nmc = (m == -INFINITY) ? 0.f : -m * c;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      x[i] = fast_exp2(__builtin_fmaf(x[i], c, nmc));
+      sum += x[i];
+    }
   }
   l += sum;
 #pragma unroll

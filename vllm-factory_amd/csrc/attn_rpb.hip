@@ -178,8 +178,12 @@ __global__ __launch_bounds__(256, 2) void rpb_fwd_kernel(RpbArgs a) {
         if (j >= a.Lk || (a.causal && j > qrow)) x[i] = -INFINITY;
       }
     }
+    // tiles carrying additive mask values take the exact exponent form
+    bool exact = false;
+    if (MASK == MASK_KEY) exact = (tflag[kt] & 1) != 0;
+    if (MASK == MASK_FULL) exact = true;
     u32x4_t p[4];
-    softmax_tile<E>(x, a.c2, m, l, o0, o1, p);
+    softmax_tile<E>(x, a.c2, m, l, o0, o1, p, exact);
     pv_tile<E>(Vt, p, o0, o1);
     __syncthreads();
     kt = nk;
