@@ -130,6 +130,41 @@ def rpb_config4(torch, args):
                 note="queries and keys of padded rows excluded from the FLOP count")
 
 
+def deberta_config3(torch, args):
+    """DeBERTa-v3-large disentangled attention, config 3 (B=32, L=512, lens U{256..512}).
+    Primary FLOP count includes the c2p/p2c projections over valid rows:
+    sum_b H * (4 d len_b^2 + 4 d len_b 2S); the core-only count is also given."""
+    import workloads
+    from kernels.flash_deberta_attention import flash_deberta_attention, flash_deberta_attention_fused
+
+    dev = torch.device("cuda:0")
+    c = workloads.config3(device=dev)
+    lens = c.lengths.tolist()
+    H, d, S = 16, 64, 256
+    core = sum(4 * d * H * n * n for n in lens)
+    proj = sum(4 * d * H * n * 2 * S for n in lens)
+    timer = KernelTimer(torch)
+    fused = lambda: flash_deberta_attention_fused(c.q, c.k, c.v, c.lengths, c.key_rel, c.query_rel,
+                                                  c.sm_scale, 256, 512, True)
+    pk = torch.matmul(c.q, c.key_rel.unsqueeze(0).transpose(-1, -2).contiguous())
+    pq = torch.matmul(c.k, c.query_rel.unsqueeze(0).transpose(-1, -2).contiguous())
+    gather = lambda: flash_deberta_attention(c.q, c.k, c.v, c.lengths, pk, pq, False, c.sm_scale,
+                                             256, 512, True)
+    for name, fn in (("fused", fused), ("gather", gather)):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            timer.run(name, fn)
+        torch.cuda.synchronize()
+    fm, gm = timer.avg_ms("fused"), timer.avg_ms("gather")
+    tf = (core + proj) / (fm * 1e-3) / 1e12
+    return dict(fused_ms=fm, tflops=tf, frac=tf / PEAK_BF16_TFLOPS, gflop=(core + proj) / 1e9,
+                core_gflop=core / 1e9, core_only_tflops=core / (fm * 1e-3) / 1e12,
+                gather_ms=gm, gather_note="reference interface: pos_key/pos_query [B,H,L,512] "
+                                          "precomputed outside the timed region")
+
+
 def epilogue_bench(torch, args, c2):
     import workloads
     from kernels.fused_layernorm import fused_layernorm
@@ -235,6 +270,7 @@ def main():
     extra = {}
     if args.only != "headline":
         extra["rpb_mt5_large_config4"] = rpb_config4(torch, args)
+        extra["deberta_v3_large_config3"] = deberta_config3(torch, args)
         extra["epilogues"] = epilogue_bench(torch, args, c2)
     line = {
         "metric": "encoder attn TFLOP/s + % bf16 MFMA peak at L=512-768; end-to-end tokens/s",

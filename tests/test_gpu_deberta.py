@@ -1,0 +1,108 @@
+"""GPU parity of DeBERTa disentangled attention (gather form = the reference
+interface, fused form = in-kernel c2p/p2c) against the oracle."""
+import math
+
+import pytest
+import torch
+
+import workloads
+from _tol import assert_attn_close
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+SM = 1.0 / math.sqrt(192)
+
+
+def _k():
+    from kernels import flash_deberta_attention as m
+    return m
+
+
+def _case(B, H, L, S, dtype, seed, lens=None, scale=0.8):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = ((torch.randn(B, H, L, 64, generator=g) * scale).to(dtype) for _ in range(3))
+    kr = (torch.randn(H, 2 * S, 64, generator=g) * scale).to(dtype)
+    qr = (torch.randn(H, 2 * S, 64, generator=g) * scale).to(dtype)
+    if lens is None:
+        lens = torch.randint(1, L + 1, (B,), generator=g)
+    return q, k, v, kr, qr, torch.as_tensor(lens, dtype=torch.int32)
+
+
+def _valid_rows(out, lens):
+    return [out[b, :, :int(n)] for b, n in enumerate(lens)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("log_bucket", [True, False])
+def test_gather_small(dev, dtype, log_bucket):
+    q, k, v, kr, qr, lens = _case(2, 3, 200, 64, dtype, 1, lens=[200, 77])
+    pk, pq = oa.deberta_position_projections(q, k, kr, qr)
+    pk, pq = pk.to(dtype), pq.to(dtype)
+    want = oa.deberta_flash_attention(q, k, v, lens, pk, pq, SM, 64, 128, log_bucket)
+    got = _k().flash_deberta_attention(q.to(dev), k.to(dev), v.to(dev), lens.to(dev), pk.to(dev),
+                                       pq.to(dev), False, SM, 64, 128, log_bucket)
+    assert_attn_close(got, want, f"gather {dtype} log={log_bucket}")
+    assert torch.all(got[1, :, 77:] == 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gather_causal_and_partial_projections(dev, dtype):
+    q, k, v, kr, qr, lens = _case(2, 2, 150, 32, dtype, 2, lens=[150, 150])
+    pk, pq = oa.deberta_position_projections(q, k, kr, qr)
+    pk = pk.to(dtype)
+    want = oa.deberta_flash_attention(q, k, v, None, pk, None, SM, 32, 64, True, causal=True)
+    got = _k().flash_deberta_attention(q.to(dev), k.to(dev), v.to(dev), None, pk.to(dev), None,
+                                       True, SM, 32, 64, True)
+    assert_attn_close(got, want, f"causal c2p-only {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_fused_small(dev, dtype):
+    for lens in ([200, 77, 1, 64], [129, 128, 65, 190]):
+        q, k, v, kr, qr, ln = _case(4, 2, 200, 256, dtype, 3, lens=lens)
+        pk, pq = oa.deberta_position_projections(q, k, kr, qr)
+        want = oa.deberta_flash_attention(q, k, v, ln, pk, pq, SM, 256, 512, True)
+        got = _k().flash_deberta_attention_fused(q.to(dev), k.to(dev), v.to(dev), ln.to(dev),
+                                                 kr.to(dev), qr.to(dev), SM, 256, 512, True)
+        for b, n in enumerate(lens):
+            assert_attn_close(got[b, :, :n], want[b, :, :n], f"fused {dtype} lens={lens} b={b}")
+        assert torch.all(got[2, :, lens[2]:] == 0)
+
+
+def test_fused_config3_subset(dev):
+    """DeBERTa-v3-large shapes (L = 512, 256 buckets, max_relative_positions 512):
+    4 of the 32 sequences of config 3 against the oracle."""
+    c = workloads.config3(batch=4, device=dev)
+    got = _k().flash_deberta_attention_fused(c.q, c.k, c.v, c.lengths, c.key_rel, c.query_rel,
+                                             c.sm_scale, 256, 512, True)
+    q, k, v, kr, qr = (t.cpu() for t in (c.q, c.k, c.v, c.key_rel, c.query_rel))
+    pk, pq = oa.deberta_position_projections(q, k, kr, qr)
+    lens = c.lengths.cpu()
+    want = oa.deberta_flash_attention(q, k, v, lens, pk, pq, c.sm_scale, 256, 512, True)
+    for b in range(4):
+        n = int(lens[b])
+        assert_attn_close(got[b, :, :n], want[b, :, :n], f"cfg3 b={b}")
+
+
+def test_fused_equals_gather_full_config3(dev):
+    """All of config 3: the fused kernel and the gather kernel fed with the
+    device-computed projections agree (size-independent consistency)."""
+    c = workloads.config3(device=dev)
+    pk = torch.matmul(c.q, c.key_rel.unsqueeze(0).transpose(-1, -2).contiguous())
+    pq = torch.matmul(c.k, c.query_rel.unsqueeze(0).transpose(-1, -2).contiguous())
+    a = _k().flash_deberta_attention(c.q, c.k, c.v, c.lengths, pk, pq, False, c.sm_scale, 256, 512, True)
+    b = _k().flash_deberta_attention_fused(c.q, c.k, c.v, c.lengths, c.key_rel, c.query_rel,
+                                           c.sm_scale, 256, 512, True)
+    for i, n in enumerate(c.lengths.tolist()):
+        assert_attn_close(b[i, :, :n], a[i, :, :n], f"fused vs gather b={i}")
+        assert torch.all(b[i, :, n:] == 0) and torch.all(a[i, :, n:] == 0)
+
+
+def test_zero_length_rows(dev):
+    q, k, v, kr, qr, lens = _case(2, 2, 70, 64, torch.bfloat16, 5, lens=[0, 70])
+    got = _k().flash_deberta_attention_fused(q.to(dev), k.to(dev), v.to(dev), lens.to(dev),
+                                             kr.to(dev), qr.to(dev), SM, 64, 128, True)
+    assert torch.all(got[0] == 0)
+    pk, pq = oa.deberta_position_projections(q, k, kr, qr)
+    want = oa.deberta_flash_attention(q, k, v, lens, pk, pq, SM, 64, 128, True)
+    assert_attn_close(got[1], want[1], "zero-length batch row")

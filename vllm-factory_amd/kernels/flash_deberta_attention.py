@@ -1,0 +1,120 @@
+"""DeBERTa-v2/v3 disentangled flash attention on gfx950.
+
+Drop-in for kernels/flash_deberta_attention.py:455-507: `flash_deberta_attention`
+with the same signature, defaults and output convention (a new [B, H, M, D]
+tensor whose rows >= seq_lengths[b] are zero), plus `clear_config_cache` and
+`HAS_TRITON` for import compatibility. Scores follow
+    s(i, j) = (q_i.k_j + pos_key[i, c(i-j)] + pos_query[j, c(i-j)]) * sm_scale,
+    c(d) = clamp(bucket(d) + att_span, 0, 2 att_span - 1),
+with the log bucket of models/deberta_v2/deberta_v2_encoder.py:70-89 evaluated
+bit-exactly.
+
+`flash_deberta_attention_fused` (no reference counterpart) takes the per-head
+relative-position projections key_rel = key_proj(rel_emb), query_rel =
+query_proj(rel_emb) ([H, 2S, D]) instead of the [B, H, L, 2S] pos_key /
+pos_query tensors the reference materialises with two batched matmuls
+(deberta_v2_encoder.py:275-286).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+# The reference exports whether its Triton path is usable; this package has no
+# Triton path (the HIP kernels are the only implementation).
+HAS_TRITON = False
+
+
+def clear_config_cache() -> None:
+    """Kept for API compatibility: tile shapes are fixed at build time."""
+    return None
+
+
+def _seq_lengths(seq_lengths: Optional[torch.Tensor], B: int, dev) -> Optional[torch.Tensor]:
+    if seq_lengths is None:
+        return None
+    sl = seq_lengths.to(device=dev, dtype=torch.int32).contiguous()
+    if sl.numel() != B:
+        raise ValueError(f"seq_lengths must have {B} entries")
+    return sl
+
+
+def flash_deberta_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    seq_lengths: Optional[torch.Tensor] = None,
+    pos_key: Optional[torch.Tensor] = None,
+    pos_query: Optional[torch.Tensor] = None,
+    causal: bool = False,
+    sm_scale: Optional[float] = None,
+    position_buckets: int = 0,
+    max_relative_distance: int = 0,
+    use_log_bucket: bool = False,
+) -> torch.Tensor:
+    """Flash attention with DeBERTa disentangled relative position bias.
+
+    q (B, H, M, D), k/v (B, H, N, D); pos_key (B, H, M, 2*ATT_SPAN),
+    pos_query (B, H, N, 2*ATT_SPAN); seq_lengths (B,) int32 or None.
+    """
+    dev = _lib.require_gpu(q, k, v, pos_key, pos_query)
+    B, H, M, D = q.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    qq, kk, vv = (_lib.rows_aligned(t) for t in (q, k, v))
+    pk = pos_key.to(q.dtype) if pos_key is not None else None
+    pq = pos_query.to(q.dtype) if pos_query is not None else None
+    sl = _seq_lengths(seq_lengths, B, dev)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    _lib.on_device(
+        "vfk_flash_deberta_fwd", dev,
+        _lib.ref(_lib.desc(qq)), _lib.ref(_lib.desc(kk)), _lib.ref(_lib.desc(vv)),
+        sl.data_ptr() if sl is not None else None,
+        _lib.ref(_lib.desc(pk)), _lib.ref(_lib.desc(pq)),
+        int(bool(causal)), float(sm_scale), int(position_buckets), int(max_relative_distance),
+        int(bool(use_log_bucket)), _lib.ref(_lib.desc(out)),
+    )
+    return out
+
+
+def flash_deberta_attention_fused(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    seq_lengths: Optional[torch.Tensor],
+    key_rel: Optional[torch.Tensor],
+    query_rel: Optional[torch.Tensor],
+    sm_scale: float,
+    position_buckets: int = 256,
+    max_relative_distance: int = 512,
+    use_log_bucket: bool = True,
+) -> torch.Tensor:
+    """Disentangled attention with c2p / p2c computed inside the kernel.
+
+    key_rel, query_rel: [H, 2*ATT_SPAN, D] per-head projections of the
+    relative-position embeddings. Equivalent to flash_deberta_attention with
+    pos_key = q @ key_rel^T and pos_query = k @ query_rel^T.
+    """
+    dev = _lib.require_gpu(q, k, v, key_rel, query_rel)
+    B = q.shape[0]
+    qq, kk, vv = (_lib.rows_aligned(t) for t in (q, k, v))
+    kr = _lib.rows_aligned(key_rel.to(q.dtype)) if key_rel is not None else None
+    qr = _lib.rows_aligned(query_rel.to(q.dtype)) if query_rel is not None else None
+    sl = _seq_lengths(seq_lengths, B, dev)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    _lib.on_device(
+        "vfk_deberta_fused_fwd", dev,
+        _lib.ref(_lib.desc(qq)), _lib.ref(_lib.desc(kk)), _lib.ref(_lib.desc(vv)),
+        sl.data_ptr() if sl is not None else None,
+        _lib.ref(_lib.desc(kr)), _lib.ref(_lib.desc(qr)), float(sm_scale),
+        int(position_buckets), int(max_relative_distance), int(bool(use_log_bucket)),
+        _lib.ref(_lib.desc(out)),
+    )
+    return out
+
+
+__all__ = ["flash_deberta_attention", "flash_deberta_attention_fused", "clear_config_cache", "HAS_TRITON"]
