@@ -133,13 +133,24 @@ int vfk_deberta_fused_fwd(const vfk_tensor* q, const vfk_tensor* k,
  *     position t - cu_seqlens[s]
  *   max_seqlen: upper bound of the sequence lengths (sizes the grid)
  *   window < 0: global; window >= 0: key j visible iff |i - j| <= window
- *   rope_theta > 0: rotate q and k (non-interleaved halves) in the kernel
- *   key_valid: device uint8 [T] (0 = key masked) or NULL */
+ *   rope_cos_sin: NULL (no rotation) or the fp32 table written by
+ *     vfk_rope_table with rope_positions >= max_seqlen rows; q and k are then
+ *     rotated (non-interleaved halves) inside the kernel
+ *   key_valid: device uint8 [T] (0 = key masked) or NULL
+ * Rows that see no key are written as zeros. */
 int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
                         const vfk_tensor* v, const int32_t* cu_seqlens,
                         int32_t num_seqs, int32_t max_seqlen, int32_t window,
-                        float rope_theta, const uint8_t* key_valid,
-                        float softmax_scale, vfk_tensor* out, void* stream);
+                        const float* rope_cos_sin, int32_t rope_positions,
+                        const uint8_t* key_valid, float softmax_scale,
+                        vfk_tensor* out, void* stream);
+
+/* RoPE cos/sin table of transformers' ModernBertRotaryEmbedding (default rope,
+ * head_dim 64; the module the reference calls at
+ * models/modernbert/modernbert_encoder.py:236-242): out[p][f] = (cos, sin) of
+ * the fp32 product p * inv_freq[f], inv_freq[f] = 1 / theta^(2f/64), for
+ * p < max_positions, f < 32. out: device fp32 [max_positions * 64]. */
+int vfk_rope_table(float theta, int32_t max_positions, float* out, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Memory-bound epilogues                                                    */

@@ -84,3 +84,13 @@ def test_config2_full_properties(dev):
     o1 = _vl()(q, k, v, c.cu_seqlens, c.max_seqlen, 64, 10000.0, 0.125)
     o2 = _vl()(q[idx], k[idx], v[idx], cu2, c.max_seqlen, 64, 10000.0, 0.125)
     assert torch.equal(o1[idx], o2)
+
+
+def test_rope_table_matches_hf(dev):
+    """vfk_rope_table == the HF rotary tables (fp32), up to one ulp of sin/cos."""
+    from kernels.varlen_attention import rope_table
+    for theta in (160000.0, 10000.0):
+        t = rope_table(theta, 800, dev).cpu()
+        c, s = oa.rope_cos_sin(torch.arange(t.shape[0]), theta)   # cat(f, f): [n, 64]
+        torch.testing.assert_close(t[..., 0], c[:, :32], atol=2e-7, rtol=0)
+        torch.testing.assert_close(t[..., 1], s[:, :32], atol=2e-7, rtol=0)

@@ -106,23 +106,19 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_kernel(DebArgs a) {
 
     f32x16_t s0, s1;
     qk_tile<E>(Ks, qf, s0, s1);
-    float x[32];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { x[i] = s0[i]; x[16 + i] = s1[i]; }
     const int16_t* lp = lut + (lut_lane - key0);
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const int xk = x_key(i, 0);           // key - key0 - 4*hl
+    map_scores(s0, s1, [&](int e, float v) {
+      const int xk = x_key(e, 0);           // key - key0 - 4*hl
       const int key = key0 + xk + 4 * hl;
       const int c = lp[-xk];
       float bias = 0.f;
       if (PKrow && qvalid) bias += E::to_f32(PKrow[(int64_t)c * a.pks[3]]);
       if (PQp && key < kend) bias += E::to_f32(PQp[(int64_t)key * a.pqs[2] + (int64_t)c * a.pqs[3]]);
-      x[i] += bias;
-      if (key >= kend || (a.causal && key > qrow + (a.N - a.M))) x[i] = -INFINITY;
-    }
+      v += bias;
+      return (key >= kend || (a.causal && key > qrow + (a.N - a.M))) ? -INFINITY : v;
+    });
     u32x4_t p[4];
-    softmax_tile<E>(x, a.c2, m, l, o0, o1, p);
+    softmax_tile<E>(s0, s1, a.c2, m, l, o0, o1, p);
     pv_tile<E>(Vt, p, o0, o1);
     __syncthreads();
   }
@@ -339,22 +335,18 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
 
     f32x16_t s0, s1;
     qk_tile<E>(Ks, qf, s0, s1);
-    float x[32];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { x[i] = s0[i]; x[16 + i] = s1[i]; }
     const int16_t* lp = lut + (lut_lane - key0);
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const int xk = x_key(i, 0);
+    map_scores(s0, s1, [&](int e, float v) {
+      const int xk = x_key(e, 0);
       const int c = lp[-xk];
       float bias = 0.f;
       if (Kr) bias += E::to_f32(Cw[(c - cw) * kCs + cl]);
       if (Qr) bias += E::to_f32(PT[(xk + 4 * hl) * kPTs + (c - wbase)]);
-      x[i] += bias;
-      if (key0 + xk + 4 * hl >= kend) x[i] = -INFINITY;
-    }
+      v += bias;
+      return (key0 + xk + 4 * hl >= kend) ? -INFINITY : v;
+    });
     u32x4_t p[4];
-    softmax_tile<E>(x, a.c2, m, l, o0, o1, p);
+    softmax_tile<E>(s0, s1, a.c2, m, l, o0, o1, p);
     pv_tile<E>(Vt, p, o0, o1);
     __syncthreads();
   }

@@ -148,42 +148,30 @@ __global__ __launch_bounds__(256, 2) void rpb_fwd_kernel(RpbArgs a) {
 
     f32x16_t s0, s1;
     qk_tile<E>(Ks, qf, s0, s1);
-    float x[32];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { x[i] = s0[i]; x[16 + i] = s1[i]; }
-    if (has_table) {
-      const float* lp = lut + key0 + lut_base;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) x[i] += lp[x_key(i, 0)];
-    }
+    if (has_table) add_by_key(s0, s1, lut + key0 + lut_base);
     if (MASK == MASK_KEY) {
-      if (tflag[kt] & 1) {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) x[i] += maskt[x_key(i, hl)];
-      }
+      if (tflag[kt] & 1) add_by_key(s0, s1, maskt + 4 * hl);
     } else if (MASK == MASK_FULL) {
       if (qvalid) {
         const int64_t mo = b * a.ms[0] + h * a.ms[1] + (int64_t)qrow * a.ms[2];
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const int j = key0 + x_key(i, hl);
-          if (j < a.Lk) x[i] += mask_raw(ld_f(a.mask, a.mask_dt, mo + (int64_t)j * a.ms[3]), a.inv_scale);
-        }
+        map_scores(s0, s1, [&](int e, float v) {
+          const int j = key0 + x_key(e, hl);
+          return j < a.Lk ? v + mask_raw(ld_f(a.mask, a.mask_dt, mo + (int64_t)j * a.ms[3]), a.inv_scale) : v;
+        });
       }
     }
     if (key0 + kBN > a.Lk || a.causal) {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        const int j = key0 + x_key(i, hl);
-        if (j >= a.Lk || (a.causal && j > qrow)) x[i] = -INFINITY;
-      }
+      map_scores(s0, s1, [&](int e, float v) {
+        const int j = key0 + x_key(e, hl);
+        return (j >= a.Lk || (a.causal && j > qrow)) ? -INFINITY : v;
+      });
     }
     // tiles carrying additive mask values take the exact exponent form
     bool exact = false;
     if (MASK == MASK_KEY) exact = (tflag[kt] & 1) != 0;
     if (MASK == MASK_FULL) exact = true;
     u32x4_t p[4];
-    softmax_tile<E>(x, a.c2, m, l, o0, o1, p, exact);
+    softmax_tile<E>(s0, s1, a.c2, m, l, o0, o1, p, exact);
     pv_tile<E>(Vt, p, o0, o1);
     __syncthreads();
     kt = nk;

@@ -5,8 +5,9 @@
 // (models/modernbert/modernbert_encoder.py:236-255, :491-550): work is cut per
 // sequence by cu_seqlens, so cross-sequence pairs are never computed, and a
 // sliding-window layer only visits the key tiles its rows can see.
-// RoPE (non-interleaved halves, HF ModernBertRotaryEmbedding tables) is
-// applied in the kernel: Q once per row in registers, K as each tile is staged.
+// RoPE (non-interleaved halves) is applied in the kernel from an fp32 cos/sin
+// table (vfk_rope_table, the HF ModernBertRotaryEmbedding values): Q once per
+// row in registers, K as each tile is staged.
 #include <math.h>
 
 #include "attn_core.h"
@@ -19,21 +20,96 @@ struct VarlenArgs {
   int64_t qs[2], ks[2], vs[2], os[2];  // [T,H,D] strides of T and H (D stride 1)
   const int32_t* cu; int nseq; int nqt; int H; int window;
   float c2;                 // softmax scale * log2(e)
-  int rope;
-  float inv_freq_rev[32];   // inv_freq[f] / (2 pi)
-  float inv_freq[32];       // HF fp32 inv_freq (fp32 kernel)
+  const float* rope;        // optional [positions][32][2] (cos, sin) table
   const uint8_t* key_valid; // optional, [T]
+};
+
+// cos/sin table of HF rotary embeddings: row p, f < 32:
+// (cos(p * inv_freq[f]), sin(p * inv_freq[f])) with fp32 p * inv_freq[f].
+struct RopeTableArgs {
+  float* out;
+  int npos;
+  float inv_freq[32];
+};
+
+__global__ __launch_bounds__(256) void rope_table_kernel(RopeTableArgs a) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= a.npos * 32) return;
+  const int p = e >> 5, f = e & 31;
+  const float ang = (float)p * a.inv_freq[f];
+  float sn, cs;
+  sincosf(ang, &sn, &cs);
+  f32x2_t v = {cs, sn};
+  reinterpret_cast<f32x2_t*>(a.out)[e] = v;
+}
+
+// Half-width of the relative-position penalty table used on tiles that cut
+// through the sliding window: entry kPenOff + (key - row) is 0 inside the
+// window and -inf outside, for |key - row| < kPenOff.
+constexpr int kPenOff = 192;
+constexpr int kPenLen = 2 * kPenOff;
+
+template <typename E, bool ROPE, bool LOCAL, bool KVALID>
+struct VarlenPolicy {
+  const VarlenArgs* a;
+  const uint16_t* Kp;
+  const uint16_t* Vp;
+  int tok0, n, kt0, t, hl, qrow, wq_lo, wq_hi, window;
+  RopeK rk;
+  float* kmask;  // [2][kBN]: 0 or -inf per key of the tile in that slot
+  int* kflag;    // [2]: any key of the tile masked
+  const float* pen;
+
+  __device__ int key0(int i) const { return (kt0 + i) * kBN; }
+  __device__ void load(int i, uint16_t* Kt, uint16_t* Vt) {
+    tile_load_direct(Vp, a->vs[0], key0(i), n, Vt);
+    if (!ROPE) tile_load_direct(Kp, a->ks[0], key0(i), n, Kt);
+  }
+  __device__ void kfetch(KStage& st, int i) {
+    kstage_fetch(st, Kp, a->ks[0], key0(i), n);
+    rope_k_fetch(rk, a->rope, min(key0(i) + (t >> 2), n - 1), true);
+  }
+  __device__ void kcommit(KStage& st, int i, uint16_t* Kt) {
+    rope_k_apply<E>(st.k0, st.k1, rk);
+    kstage_store(st, Kt);
+  }
+  __device__ void meta(int i, int slot) {
+    if (t < kBN) {  // wave 0: one key per lane
+      const int j = key0(i) + t;
+      bool ok = j < n;
+      if (KVALID) ok = ok && a->key_valid[tok0 + j] != 0;
+      kmask[slot * kBN + t] = ok ? 0.f : -INFINITY;
+      const unsigned long long dead = __builtin_amdgcn_ballot_w64(!ok);
+      if (t == 0) kflag[slot] = dead != 0ull;
+    }
+  }
+  __device__ bool active(int i) const {
+    if (wq_lo >= n) return false;
+    if (!LOCAL) return true;
+    const int k0 = key0(i);
+    return k0 <= wq_hi + window && k0 + kBN - 1 >= wq_lo - window;
+  }
+  __device__ bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot) const {
+    if (kflag[slot]) add_by_key(s0, s1, kmask + slot * kBN + 4 * hl);
+    if (LOCAL) {
+      const int k0 = key0(i);
+      if (wq_hi - k0 > window || k0 + kBN - 1 - wq_lo > window)
+        // entry kPenOff + key - qrow, key = k0 + 4*hl + x_key(e, 0)
+        add_by_key(s0, s1, pen + (kPenOff + k0 + 4 * hl - qrow));
+    }
+    return false;
+  }
 };
 
 template <typename E, bool ROPE, bool LOCAL, bool KVALID>
 __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenArgs a) {
-  __shared__ __align__(16) uint16_t Ks[kKsElems];
-  __shared__ __align__(16) uint16_t Vt[kVtElems];
-  __shared__ float kmask[kBN];
+  __shared__ __align__(16) uint16_t buf0[kBuf2Elems];
+  __shared__ __align__(16) uint16_t buf1[kBuf2Elems];
+  __shared__ float kmask[2 * kBN];
   __shared__ int kflag[2];
+  __shared__ float pen[LOCAL ? kPenLen : 1];
 
-  const int total = gridDim.x;
-  const int work = xcd_remap(blockIdx.x, total);
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
   const int qt = work % a.nqt;
   const int h = (work / a.nqt) % a.H;
   const int s = work / (a.nqt * a.H);
@@ -44,95 +120,40 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenArgs a) {
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, hl = lane >> 5;
   const uint16_t* Qp = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)tok0 * a.qs[0] + h * a.qs[1];
-  const uint16_t* Kp = reinterpret_cast<const uint16_t*>(a.k) + (int64_t)tok0 * a.ks[0] + h * a.ks[1];
-  const uint16_t* Vp = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)tok0 * a.vs[0] + h * a.vs[1];
 
-  float invf[8];
-  if (ROPE) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) invf[i] = a.inv_freq_rev[8 * (t & 3) + i];
-  }
-
-  // key range of the workgroup (sequence-relative)
+  // key tiles of the workgroup (sequence-relative)
   int klo = 0, khi = n;
   if (LOCAL) {
     klo = max(0, q0 - a.window);
     khi = min(n, q0 + kBM + a.window);
+    for (int e = t; e < kPenLen; e += 256) {
+      const int d = e - kPenOff;
+      pen[e] = (d <= a.window && d >= -a.window) ? 0.f : -INFINITY;
+    }
   }
   const int kt_begin = klo / kBN;
   const int kt_end = (khi + kBN - 1) / kBN;
 
-  // this wave's rows and the keys they can see
   const int wq_lo = q0 + w * 32;
-  const int wq_hi = min(wq_lo + 31, n - 1);
   const int qrow = wq_lo + (lane & 31);
   const bool qvalid = qrow < n;
 
   u32x4_t qf[4];
   load_q(qf, Qp + (int64_t)qrow * a.qs[0], qvalid);
-  if (ROPE) rope_q<E>(qf, qrow, a.inv_freq_rev);
+  if (ROPE && qvalid) rope_q_table<E>(qf, a.rope + (int64_t)qrow * 64);
+
+  VarlenPolicy<E, ROPE, LOCAL, KVALID> pol;
+  pol.a = &a;
+  pol.Kp = reinterpret_cast<const uint16_t*>(a.k) + (int64_t)tok0 * a.ks[0] + h * a.ks[1];
+  pol.Vp = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)tok0 * a.vs[0] + h * a.vs[1];
+  pol.tok0 = tok0; pol.n = n; pol.kt0 = kt_begin; pol.t = t; pol.hl = hl; pol.qrow = qrow;
+  pol.wq_lo = wq_lo; pol.wq_hi = min(wq_lo + 31, n - 1); pol.window = a.window;
+  pol.kmask = kmask; pol.kflag = kflag; pol.pen = pen;
 
   float m = -INFINITY, l = 0.f;
   f32x16_t o0 = {}, o1 = {};
+  attn_loop_direct<E, ROPE>(pol, buf0, buf1, kt_end - kt_begin, qf, a.c2, m, l, o0, o1);
 
-  KVStage st;
-  int kt = kt_begin;
-  kv_load(st, Kp, a.ks[0], Vp, a.vs[0], kt * kBN, n);
-  while (kt < kt_end) {
-    const int key0 = kt * kBN;
-    if (ROPE) rope_k<E>(st, key0 + (t >> 2), invf);
-    kv_store(st, Ks, Vt);
-    if (KVALID) {
-      if (t == 0) kflag[kt & 1] = 0;
-    }
-    __syncthreads();
-    if (KVALID) {
-      if (t < kBN) {
-        const int j = key0 + t;
-        const bool ok = j >= n || a.key_valid[tok0 + j] != 0;
-        kmask[t] = ok ? 0.f : -INFINITY;
-        if (!ok) atomicOr(&kflag[kt & 1], 1);
-      }
-    }
-    if (kt + 1 < kt_end) kv_load(st, Kp, a.ks[0], Vp, a.vs[0], (kt + 1) * kBN, n);
-    if (KVALID) __syncthreads();
-
-    // does this wave see any key of the tile?
-    bool active = wq_lo < n;
-    if (LOCAL) active = active && key0 <= wq_hi + a.window && key0 + kBN - 1 >= wq_lo - a.window;
-    if (active) {
-      f32x16_t s0, s1;
-      qk_tile<E>(Ks, qf, s0, s1);
-      float x[32];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) { x[i] = s0[i]; x[16 + i] = s1[i]; }
-      if (KVALID) {
-        if (kflag[kt & 1]) {
-#pragma unroll
-          for (int i = 0; i < 32; ++i) x[i] += kmask[x_key(i, hl)];
-        }
-      }
-      bool partial = key0 + kBN > n;
-      if (LOCAL)
-        partial = partial || (wq_hi - key0 > a.window) || (key0 + kBN - 1 - wq_lo > a.window);
-      if (partial) {
-        const int rb = qrow - key0 - 4 * hl;  // qrow - key for x_key(i, 0) = 0
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const int kk = x_key(i, 0);
-          const int rel = rb - kk;
-          bool dead = key0 + kk + 4 * hl >= n;
-          if (LOCAL) dead = dead || rel > a.window || rel < -a.window;
-          if (dead) x[i] = -INFINITY;
-        }
-      }
-      u32x4_t p[4];
-      softmax_tile<E>(x, a.c2, m, l, o0, o1, p);
-      pv_tile<E>(Vt, p, o0, o1);
-    }
-    __syncthreads();
-    ++kt;
-  }
   const float l_tot = half_swap_sum(l);
   if (qvalid) {
     uint16_t* orow = reinterpret_cast<uint16_t*>(a.o) + (int64_t)(tok0 + qrow) * a.os[0] + h * a.os[1];
@@ -141,7 +162,7 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenArgs a) {
 }
 
 // fp32: one thread per query row, exact fp32 arithmetic, accurate sin/cos.
-__global__ __launch_bounds__(64) void varlen_fwd_f32_kernel(VarlenArgs a, const float* inv_freq_unused) {
+__global__ __launch_bounds__(64) void varlen_fwd_f32_kernel(VarlenArgs a) {
   __shared__ float Kt[64][kHD + 1];
   __shared__ float Vt32[64][kHD + 1];
   const int nqt64 = a.nqt * 2;
@@ -163,11 +184,10 @@ __global__ __launch_bounds__(64) void varlen_fwd_f32_kernel(VarlenArgs a, const 
     qv[d] = qvalid ? Qp[(int64_t)qrow * a.qs[0] + d] : 0.f;
     acc[d] = 0.f;
   }
-  if (a.rope) {
+  if (a.rope && qvalid) {
 #pragma unroll
     for (int f = 0; f < 32; ++f) {
-      float sn, cs;
-      sincosf((float)qrow * a.inv_freq[f], &sn, &cs);
+      const float cs = a.rope[(int64_t)qrow * 64 + 2 * f], sn = a.rope[(int64_t)qrow * 64 + 2 * f + 1];
       const float x1 = qv[f], x2 = qv[f + 32];
       qv[f] = x1 * cs - x2 * sn;
       qv[f + 32] = x2 * cs + x1 * sn;
@@ -191,8 +211,7 @@ __global__ __launch_bounds__(64) void varlen_fwd_f32_kernel(VarlenArgs a, const 
         v1 = Vp[(int64_t)j * a.vs[0] + f];
         v2 = Vp[(int64_t)j * a.vs[0] + f + 32];
         if (a.rope) {
-          float sn, cs;
-          sincosf((float)j * a.inv_freq[f], &sn, &cs);
+          const float cs = a.rope[(int64_t)j * 64 + 2 * f], sn = a.rope[(int64_t)j * 64 + 2 * f + 1];
           const float x1 = k1, x2 = k2;
           k1 = x1 * cs - x2 * sn;
           k2 = x2 * cs + x1 * sn;
@@ -251,9 +270,9 @@ static int check_thd(const vfk_tensor* t, const char* name, int dtype, int64_t T
 extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
                                    const vfk_tensor* v, const int32_t* cu_seqlens,
                                    int32_t num_seqs, int32_t max_seqlen,
-                                   int32_t window, float rope_theta,
-                                   const uint8_t* key_valid, float softmax_scale,
-                                   vfk_tensor* out, void* stream) {
+                                   int32_t window, const float* rope_cos_sin,
+                                   int32_t rope_positions, const uint8_t* key_valid,
+                                   float softmax_scale, vfk_tensor* out, void* stream) {
   int rc = check_tensor(q, "q", 3);
   if (rc) return rc;
   const int dt = q->dtype;
@@ -279,30 +298,29 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: softmax_scale must be > 0");
   a.c2 = softmax_scale * VFK_LOG2E;
   a.key_valid = key_valid;
-  a.rope = rope_theta > 0.f;
-  if (a.rope) {
-    // inv_freq exactly as the HF rotary module computes it in fp32:
-    // 1 / theta ** (arange(0, 64, 2).float() / 64)
-    for (int f = 0; f < 32; ++f) {
-      const float e = (float)(2 * f) / 64.0f;
-      const float inv = 1.0f / powf(rope_theta, e);
-      a.inv_freq[f] = inv;
-      a.inv_freq_rev[f] = inv / 6.283185307179586f;
-    }
+  if (rope_cos_sin) {
+    if (rope_positions < max_seqlen)
+      return set_error(VFK_ERR_INVALID, "rope table has %d positions < max_seqlen %d",
+                       rope_positions, max_seqlen);
+    if (!aligned16(rope_cos_sin))
+      return set_error(VFK_ERR_INVALID, "rope table must be 16-byte aligned");
   }
+  a.rope = rope_cos_sin;
   hipStream_t st = (hipStream_t)stream;
   if (dt == VFK_F32) {
     a.nqt = ceil_div(max_seqlen, 128);
     const int64_t blocks = (int64_t)a.nqt * 2 * H * num_seqs;
-    hipLaunchKernelGGL(varlen_fwd_f32_kernel, dim3((unsigned)blocks), dim3(64), 0, st, a,
-                       (const float*)nullptr);
+    hipLaunchKernelGGL(varlen_fwd_f32_kernel, dim3((unsigned)blocks), dim3(64), 0, st, a);
     return launch_status("vfk_varlen_attn_fwd");
   }
+  if (a.window >= 0 && a.window >= max_seqlen) a.window = -1;  // window covers every pair
+  if (a.window > kPenOff - kBM)
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: window %d > %d", a.window, kPenOff - kBM);
   a.nqt = ceil_div(max_seqlen, kBM);
   const int64_t blocks = (int64_t)a.nqt * H * num_seqs;
   if (blocks >= (1ll << 31))
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: grid too large");
-  const bool local = a.window >= 0, kv = key_valid != nullptr, rope = a.rope != 0;
+  const bool local = a.window >= 0, kv = key_valid != nullptr, rope = a.rope != nullptr;
 #define VFK_VL(E, R, L, K) \
   hipLaunchKernelGGL((varlen_fwd_kernel<E, R, L, K>), dim3((unsigned)blocks), dim3(256), 0, st, a)
 #define VFK_VL_E(E)                                                   \
@@ -321,4 +339,20 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
 #undef VFK_VL_E
 #undef VFK_VL
   return launch_status("vfk_varlen_attn_fwd");
+}
+
+extern "C" int vfk_rope_table(float theta, int32_t max_positions, float* out, void* stream) {
+  if (!out || max_positions < 0) return set_error(VFK_ERR_INVALID, "vfk_rope_table: bad arguments");
+  if (!(theta > 0.f)) return set_error(VFK_ERR_INVALID, "vfk_rope_table: theta must be > 0");
+  if (max_positions == 0) return VFK_OK;
+  RopeTableArgs a = {};
+  a.out = out;
+  a.npos = max_positions;
+  // inv_freq exactly as the HF rotary module computes it in fp32:
+  // 1 / theta ** (arange(0, 64, 2).float() / 64)
+  for (int f = 0; f < 32; ++f) a.inv_freq[f] = 1.0f / powf(theta, (float)(2 * f) / 64.0f);
+  const int64_t n = (int64_t)max_positions * 32;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, a);
+  return launch_status("vfk_rope_table");
 }

@@ -44,6 +44,11 @@ struct BF16 {
     bf16x2_t h = __builtin_convertvector(v, bf16x2_t);
     return __builtin_bit_cast(uint32_t, h);
   }
+  // c + a.lo + a.hi for a packed pair a (the row-sum of two probabilities)
+  __device__ static inline float dot2_ones(uint32_t a, float c) {
+    const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), one, c, false);
+  }
   __device__ static inline f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
         __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
@@ -64,6 +69,10 @@ struct F16 {
     f32x2_t v = {a, b};
     f16x2_t h = __builtin_convertvector(v, f16x2_t);
     return __builtin_bit_cast(uint32_t, h);
+  }
+  __device__ static inline float dot2_ones(uint32_t a, float c) {
+    const f16x2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), one, c, false);
   }
   __device__ static inline f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(
@@ -92,10 +101,13 @@ __device__ inline u32x4_t pack8(const float* f) {
 
 // Max of a value with the lane 32 positions away (the two half-waves hold
 // the same attention row in the S^T layout used by the attention kernels).
-__device__ inline float half_swap_max(float x) {
+__device__ inline float fmax_ieee(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// max over the lane pair (l, l ^ 32) of x, and of m.
+__device__ inline float half_swap_max(float x, float m = -__builtin_inff()) {
   int xi = __float_as_int(x);
   auto r = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
-  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+  return fmax_ieee(fmax_ieee(m, __int_as_float(r[0])), __int_as_float(r[1]));
 }
 __device__ inline float half_swap_sum(float x) {
   int xi = __float_as_int(x);

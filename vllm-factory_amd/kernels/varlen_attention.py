@@ -19,11 +19,27 @@ Rows that see no key at all are returned as zeros.
 from __future__ import annotations
 
 import math
-from typing import Optional
+from typing import Dict, Optional, Tuple
 
 import torch
 
 from . import _lib
+
+_ROPE_TABLES: Dict[Tuple[float, int, torch.device], torch.Tensor] = {}
+
+
+def rope_table(theta: float, positions: int, device: torch.device) -> torch.Tensor:
+    """fp32 [positions, 32, 2] (cos, sin) table of the HF rotary embedding
+    (vfk_rope_table), cached per (theta, size bucket, device) the way the HF
+    rotary module caches its tables."""
+    n = max(256, 1 << (max(positions, 1) - 1).bit_length())
+    key = (float(theta), n, torch.device(device))
+    t = _ROPE_TABLES.get(key)
+    if t is None:
+        t = torch.empty(n, 32, 2, dtype=torch.float32, device=device)
+        _lib.on_device("vfk_rope_table", torch.device(device), float(theta), int(n), t.data_ptr())
+        _ROPE_TABLES[key] = t
+    return t
 
 
 def varlen_rope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -50,11 +66,15 @@ def varlen_rope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         key_valid = key_valid.to(torch.uint8).contiguous()
         kv_ptr = key_valid.data_ptr()
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    tab_ptr, tab_n = None, 0
+    if rope_theta and rope_theta > 0:
+        tab = rope_table(rope_theta, int(max_seqlen), dev)
+        tab_ptr, tab_n = tab.data_ptr(), tab.shape[0]
     _lib.on_device(
         "vfk_varlen_attn_fwd", dev,
         _lib.ref(_lib.desc(qq)), _lib.ref(_lib.desc(kk)), _lib.ref(_lib.desc(vv)),
         cu_seqlens.data_ptr(), int(cu_seqlens.numel() - 1), int(max_seqlen),
-        int(window), float(rope_theta), kv_ptr, float(scale),
+        int(window), tab_ptr, int(tab_n), kv_ptr, float(scale),
         _lib.ref(_lib.desc(out)),
     )
     return out
