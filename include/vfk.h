@@ -124,10 +124,10 @@ int vfk_deberta_fused_fwd(const vfk_tensor* q, const vfk_tensor* k,
                           int32_t use_log_bucket, vfk_tensor* out,
                           void* stream);
 
-/* Varlen (packed) bidirectional attention with optional in-kernel RoPE and
- * sliding window, for ModernBERT (no counterpart kernel in the reference: it
- * replaces F.scaled_dot_product_attention with the dense O(T^2) masks at
- * models/modernbert/modernbert_encoder.py:236-255 and :491-550).
+/* Varlen (packed) bidirectional attention with optional RoPE and sliding
+ * window, for ModernBERT (no counterpart kernel in the reference: it replaces
+ * the rotary step and F.scaled_dot_product_attention with the dense O(T^2)
+ * masks at models/modernbert/modernbert_encoder.py:236-255 and :491-550).
  *   q/k/v [T,H,D] (any strides, D == 64), out [T,H,D]
  *   cu_seqlens: device int32 [num_seqs + 1]; token t of sequence s has
  *     position t - cu_seqlens[s]
@@ -135,15 +135,26 @@ int vfk_deberta_fused_fwd(const vfk_tensor* q, const vfk_tensor* k,
  *   window < 0: global; window >= 0: key j visible iff |i - j| <= window
  *   rope_cos_sin: NULL (no rotation) or the fp32 table written by
  *     vfk_rope_table with rope_positions >= max_seqlen rows; q and k are then
- *     rotated (non-interleaved halves) inside the kernel
+ *     rotated (non-interleaved halves): k by a pre-pass into the workspace, q
+ *     in the attention kernel. q, k and v are never written.
  *   key_valid: device uint8 [T] (0 = key masked) or NULL
+ *   workspace: device memory of at least vfk_varlen_attn_workspace_bytes()
+ *     bytes, 16-byte aligned (NULL when that is 0); its contents on entry do
+ *     not matter. Calls that share a workspace must not overlap.
  * Rows that see no key are written as zeros. */
 int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
                         const vfk_tensor* v, const int32_t* cu_seqlens,
                         int32_t num_seqs, int32_t max_seqlen, int32_t window,
                         const float* rope_cos_sin, int32_t rope_positions,
                         const uint8_t* key_valid, float softmax_scale,
+                        void* workspace, int64_t workspace_bytes,
                         vfk_tensor* out, void* stream);
+
+/* Workspace size of vfk_varlen_attn_fwd for total_tokens rows (q->size[0]) and
+ * num_heads heads: total_tokens * num_heads * 64 * 2 bytes for 16-bit dtypes
+ * with RoPE (the rotated K, head-major), else 0. */
+int64_t vfk_varlen_attn_workspace_bytes(int32_t dtype, int64_t total_tokens,
+                                        int32_t num_heads, int32_t rope);
 
 /* RoPE cos/sin table of transformers' ModernBertRotaryEmbedding (default rope,
  * head_dim 64; the module the reference calls at

@@ -32,7 +32,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     from kernels import _lib
-    assert _lib.load().vfk_abi_version() == 1
+    assert _lib.load().vfk_abi_version() == 2
 
 
 def _host_t5(rel, bidirectional, nb, md):
@@ -91,3 +91,12 @@ def test_product_rejects_cpu_tensors():
         flash_attention_rpb_final(q, q, q, None, 32, 128, False)
     with pytest.raises(RuntimeError, match="GPU only"):
         fused_layernorm(torch.randn(4, 8), 8)
+
+
+def test_varlen_workspace_bytes():
+    from kernels import _lib
+    lib = _lib.load()
+    assert lib.vfk_varlen_attn_workspace_bytes(_lib.BF16, 40265, 12, 1) == 40265 * 12 * 64 * 2
+    assert lib.vfk_varlen_attn_workspace_bytes(_lib.F16, 7, 3, 1) == 7 * 3 * 64 * 2
+    assert lib.vfk_varlen_attn_workspace_bytes(_lib.BF16, 40265, 12, 0) == 0
+    assert lib.vfk_varlen_attn_workspace_bytes(_lib.F32, 40265, 12, 1) == 0

@@ -149,17 +149,18 @@ __device__ inline int x_key(int i, int h) {
 }
 
 // Online softmax over one tile of raw scores (bias already added, -inf =
-// masked), held in the two S^T accumulators s0 (keys 0..31) and s1 (32..63)
-// and updated in place. c = softmax scale * log2(e), so p = exp2(c * (x - m))
-// is one FMA and one exp2 per score. m: running reference max in raw units;
-// l: this lane's partial row sum.
-// exact: evaluate (x - m) * c instead of fma(x, c, -m*c). Needed when x may
-// carry a huge finite additive mask (|x| ~ 1e30): the rounding of m*c alone
-// would then exceed the whole exponent range, while x - m stays exact.
-template <typename E>
-__device__ inline void softmax_tile(f32x16_t& s0, f32x16_t& s1, float c, float& m, float& l,
-                                    f32x16_t& o0, f32x16_t& o1,
-                                    u32x4_t (&p)[4], bool exact = false) {
+// masked), held in the two S^T accumulators s0 (keys 0..31) and s1 (32..63).
+// c = softmax scale * log2(e), so p = exp2(c * (x - m)) is one FMA and one
+// exp2 per score. m: running reference max in raw units; l: this lane's
+// partial row sum. The step is split in two so that a pipelined loop can
+// place the parts apart: softmax_ref (row max, O rescale) and softmax_exp
+// (probabilities, row sum, 16-bit packing).
+
+// m := max(m, row max of the tile), but only when the max grew by more than
+// 2^kRescaleSlack (otherwise the old reference is kept and probabilities may
+// reach 256, harmless); O and l are rescaled to the new reference.
+__device__ inline void softmax_ref(const f32x16_t& s0, const f32x16_t& s1, float c, float& m,
+                                   float& l, f32x16_t& o0, f32x16_t& o1) {
   // IEEE maximum (NaN-propagating) maps to v_maximum3_f32 without the
   // canonicalising moves fmaxf needs: 17 instructions for 32 scores.
   float ma = fmax_ieee(s0[0], s1[0]), mb = fmax_ieee(s0[1], s1[1]);
@@ -169,8 +170,6 @@ __device__ inline void softmax_tile(f32x16_t& s0, f32x16_t& s1, float c, float& 
     mb = fmax_ieee(fmax_ieee(mb, s0[i + 1]), s1[i + 1]);
   }
   const float m_new = half_swap_max(fmax_ieee(ma, mb), m);
-  // Rescale only when the max grew by more than 2^kRescaleSlack; otherwise
-  // keep the old reference (probabilities may then reach 256, harmless).
   const bool need = (m_new - m) * c > kRescaleSlack;
   if (__builtin_amdgcn_ballot_w64(need)) {
     if (m_new != -INFINITY) {
@@ -181,23 +180,39 @@ __device__ inline void softmax_tile(f32x16_t& s0, f32x16_t& s1, float c, float& 
       m = m_new;
     }
   }
+}
+
+// p := 16-bit exp2((s - m) c) (0 where m = -inf; s is overwritten with the
+// fp32 probabilities), l += their fp32 sum. The sum uses plain fp32 adds:
+// they co-issue with the matrix cores, the packed dot instructions do not.
+// exact: (x - m) * c instead of fma(x, c, -m*c). Needed when x may carry a
+// huge finite additive mask (|x| ~ 1e30): the rounding of m*c alone would
+// then exceed the whole exponent range, while x - m stays exact.
+template <typename E>
+__device__ inline void softmax_exp(f32x16_t& s0, f32x16_t& s1, float c, float m, bool exact,
+                                   u32x4_t (&p)[4], float& l) {
+  const float ms = (m == -INFINITY) ? 0.f : m;
   if (exact) {
-    const float ms = (m == -INFINITY) ? 0.f : m;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       s0[i] = fast_exp2((s0[i] - ms) * c);
       s1[i] = fast_exp2((s1[i] - ms) * c);
     }
   } else {
-    const float nmc = (m == -INFINITY) ? 0.f : -m * c;
+    const float nmc = -ms * c;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       s0[i] = fast_exp2(__builtin_fmaf(s0[i], c, nmc));
       s1[i] = fast_exp2(__builtin_fmaf(s1[i], c, nmc));
     }
   }
-  // pack to the 16-bit MFMA operand and sum the packed pairs: the row sum is
-  // that of exactly the probabilities the PV product uses
+  float la = s0[0] + s0[1], lb = s1[0] + s1[1];
+#pragma unroll
+  for (int i = 2; i < 16; ++i) {
+    la += s0[i];
+    lb += s1[i];
+  }
+  l += la + lb;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     p[0][j] = E::pack2(s0[2 * j], s0[2 * j + 1]);
@@ -205,10 +220,14 @@ __device__ inline void softmax_tile(f32x16_t& s0, f32x16_t& s1, float c, float& 
     p[2][j] = E::pack2(s1[2 * j], s1[2 * j + 1]);
     p[3][j] = E::pack2(s1[8 + 2 * j], s1[8 + 2 * j + 1]);
   }
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) l = E::dot2_ones(p[ks][j], l);
+}
+
+template <typename E>
+__device__ inline void softmax_tile(f32x16_t& s0, f32x16_t& s1, float c, float& m, float& l,
+                                    f32x16_t& o0, f32x16_t& o1,
+                                    u32x4_t (&p)[4], bool exact = false) {
+  softmax_ref(s0, s1, c, m, l, o0, o1);
+  softmax_exp<E>(s0, s1, c, m, exact, p, l);
 }
 
 // s_e = f(e, s_e) for the 32 score elements of the accumulator pair.
@@ -262,104 +281,6 @@ __device__ inline void load_q(u32x4_t (&q)[4], const uint16_t* __restrict__ qrow
 }
 
 // ---------------------------------------------------------------------------
-// Software-pipelined tile loop shared by the attention kernels.
-//
-// K/V tiles rotate through three LDS buffers so a single barrier per tile
-// suffices, and each wave's instruction stream interleaves independent work:
-//   commit tile t+1 (RoPE, V transpose, LDS stores)   | VALU  - overlaps PV(t-1)
-//   issue global loads of tile t+2                    | VMEM
-//   barrier
-//   S(t+1) = K(t+1) Q^T                               | MFMA  - overlaps softmax(t)
-//   softmax(t) (policy bias / masks first)             | VALU
-//   O += V(t)^T P(t)^T                                 | MFMA
-// The policy P supplies, for virtual tile index i in [0, n):
-//   int  key0(i)                                     first key of the tile
-//   void fetch(KVStage&, int i)                      global -> registers
-//   void commit(KVStage&, int i, int slot, uint16_t* Ks, uint16_t* Vt)
-//   bool active(int i)                               this wave computes tile i
-//   bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot)
-//                                                    add bias/masks in place;
-//                                                    returns "exact" for softmax_tile
-// ---------------------------------------------------------------------------
-constexpr int kBufElems = kKsElems + kVtElems;   // u16 per LDS buffer
-constexpr int kNumBufs = 3;
-
-template <typename E, typename P>
-__device__ inline void attn_pipeline(P& pol, uint16_t* __restrict__ lds, int n,
-                                     const u32x4_t (&qf)[4], float c, float& m,
-                                     float& l, f32x16_t& o0, f32x16_t& o1) {
-  if (n <= 0) return;
-  KVStage st;
-  pol.fetch(st, 0);
-  pol.commit(st, 0, 0, lds, lds + kKsElems);
-  if (n > 1) pol.fetch(st, 1);
-  __syncthreads();
-  f32x16_t sa0, sa1, sb0, sb1;
-  if (pol.active(0)) qk_tile<E>(lds, qf, sa0, sa1);
-
-  auto step = [&](int i, int slot, f32x16_t& c0, f32x16_t& c1, f32x16_t& n0, f32x16_t& n1) {
-    const int ns = slot == kNumBufs - 1 ? 0 : slot + 1;
-    uint16_t* nK = lds + ns * kBufElems;
-    if (i + 1 < n) {
-      pol.commit(st, i + 1, ns, nK, nK + kKsElems);
-      if (i + 2 < n) pol.fetch(st, i + 2);
-    }
-    __syncthreads();
-    const bool act = pol.active(i);
-    VOps vo;
-    if (act) pv_load(lds + slot * kBufElems + kKsElems, vo);
-    if (i + 1 < n && pol.active(i + 1)) qk_tile<E>(nK, qf, n0, n1);
-    if (act) {
-      const bool exact = pol.modify(c0, c1, i, slot);
-      u32x4_t p[4];
-      softmax_tile<E>(c0, c1, c, m, l, o0, o1, p, exact);
-      pv_mfma<E>(vo, p, o0, o1);
-    }
-  };
-
-  int slot = 0;
-  for (int i = 0; i < n; i += 2) {
-    step(i, slot, sa0, sa1, sb0, sb1);
-    slot = slot == kNumBufs - 1 ? 0 : slot + 1;
-    if (i + 1 < n) {
-      step(i + 1, slot, sb0, sb1, sa0, sa1);
-      slot = slot == kNumBufs - 1 ? 0 : slot + 1;
-    }
-  }
-}
-
-// Single-buffered tile loop with the same policy interface (slot is always
-// 0): commit tile i, barrier, prefetch tile i+1 into registers, compute tile
-// i, barrier. Fewer live registers than attn_pipeline (no second S tile, no
-// early V operands), so more waves fit on each SIMD.
-template <typename E, typename P>
-__device__ inline void attn_loop(P& pol, uint16_t* __restrict__ lds, int n,
-                                 const u32x4_t (&qf)[4], float c, float& m,
-                                 float& l, f32x16_t& o0, f32x16_t& o1) {
-  if (n <= 0) return;
-  KVStage st;
-  pol.fetch(st, 0);
-  for (int i = 0; i < n; ++i) {
-    pol.commit(st, i, 0, lds, lds + kKsElems);
-    __syncthreads();
-    if (i + 1 < n) pol.fetch(st, i + 1);
-    if (pol.active(i)) {
-      f32x16_t s0, s1;
-      qk_tile<E>(lds, qf, s0, s1);
-      // V operands are read while the softmax runs
-      VOps vo;
-      pv_load(lds + kKsElems, vo);
-      __builtin_amdgcn_sched_barrier(0);
-      const bool exact = pol.modify(s0, s1, i, 0);
-      u32x4_t p[4];
-      softmax_tile<E>(s0, s1, c, m, l, o0, o1, p, exact);
-      pv_mfma<E>(vo, p, o0, o1);
-    }
-    __syncthreads();
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Direct-to-LDS tiles (gfx950 global_load_lds_dwordx4 + ds_read_b64_tr_b16).
 //
 // A tile is 64 rows (keys) x 64 halves (d) = 64 x 128 B, stored without
@@ -371,28 +292,47 @@ __device__ inline void attn_loop(P& pol, uint16_t* __restrict__ lds, int n,
 // tile streams in while the current one is consumed; one barrier per tile.
 // ---------------------------------------------------------------------------
 constexpr int kTileElems = 64 * 64;          // u16 per K or V tile (8 KiB)
-constexpr int kBuf2Elems = 2 * kTileElems;   // one K + one V tile
 
 __device__ inline int swz(int row) { return (((row >> 1) & 1) << 2) | ((row >> 2) & 3); }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
-// Loads tile rows [row0, row0 + 64) of a [rows x 64] matrix with row stride rs
-// (elements) into LDS tile t; rows past nvalid read row nvalid - 1 instead
-// (finite data whose scores are masked). Each wave moves two 1 KiB blocks.
-__device__ inline void tile_load_direct(const uint16_t* __restrict__ base, int64_t rs, int row0,
-                                        int nvalid, uint16_t* tile) {
+// Direct-to-LDS tile loads through a buffer resource. The resource covers the
+// nvalid rows of one (sequence, head) slice; the hardware range check turns
+// every dword past nvalid rows into a zero written to LDS, so tail tiles need
+// no clamping, and the tile's row offset travels in the scalar offset, leaving
+// no per-tile address arithmetic on the vector ALU.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
+
+struct TileSrc {
+  rsrc_t r;
+  int rs2;    // row stride in bytes
+  int vo[2];  // this lane's byte offsets in the wave's two 1 KiB blocks
+};
+
+// rows * rs * 2 must stay below 2^31 (checked by the host).
+__device__ inline void tile_src_init(TileSrc& s, const uint16_t* base, int rs, int nvalid) {
+  s.r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, nvalid * rs * 2,
+                                          kRsrcWord3);
+  s.rs2 = rs * 2;
   const int w = threadIdx.x >> 6, p = threadIdx.x & 63;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int blk = 2 * w + j;  // rows 8*blk .. 8*blk + 7
-    const int row = 8 * blk + (p >> 3);
-    const int c = (p & 7) ^ swz(row);
-    const int grow = min(row0 + row, nvalid - 1);
-    __builtin_amdgcn_global_load_lds(base + (int64_t)grow * rs + 8 * c,
-                                     (lds_void_t*)(tile + blk * 512), 16, 0, 0);
+    const int row = 8 * (2 * w + j) + (p >> 3);
+    s.vo[j] = row * s.rs2 + 16 * ((p & 7) ^ swz(row));
   }
+}
+
+// Loads rows [row0, row0 + 64) into LDS tile t (swizzled 16-byte chunks).
+__device__ inline void tile_load_buf(const TileSrc& s, int row0, uint16_t* tile) {
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int soff = row0 * s.rs2;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.r, (lds_void_t*)(tile + (2 * w + j) * 512), 16,
+                                             s.vo[j], soff, 0, 0);
 }
 
 // Waits for this wave's outstanding loads and LDS traffic, then joins the
@@ -437,14 +377,14 @@ __device__ inline void qk_tile_sw(const uint16_t* __restrict__ Kt, const KOff& k
     a0[ds] = lds_at<u32x4_t>(Kt, off);
     a1[ds] = lds_at<u32x4_t>(Kt, off + 4096);
   }
+  // keys 0-31 first, so their softmax can start while keys 32-63 multiply
   const f32x16_t z = {};
   s0 = E::mfma32(a0[0], q[0], z);
+#pragma unroll
+  for (int ds = 1; ds < 4; ++ds) s0 = E::mfma32(a0[ds], q[ds], s0);
   s1 = E::mfma32(a1[0], q[0], z);
 #pragma unroll
-  for (int ds = 1; ds < 4; ++ds) {
-    s0 = E::mfma32(a0[ds], q[ds], s0);
-    s1 = E::mfma32(a1[ds], q[ds], s1);
-  }
+  for (int ds = 1; ds < 4; ++ds) s1 = E::mfma32(a1[ds], q[ds], s1);
 }
 
 // Byte offsets of the transposed V reads: for 16-key step ks (+2048 bytes), d
@@ -499,83 +439,78 @@ __device__ inline void pv_tile_sw(const uint16_t* __restrict__ Vt, const VOff& v
   }
 }
 
-// K rows staged through registers when they must be rotated (RoPE) before
-// reaching LDS: thread t holds row t>>2, chunks cp = t&3 and cp+4.
-struct KStage {
-  u32x4_t k0, k1;
-};
-__device__ inline void kstage_fetch(KStage& st, const uint16_t* __restrict__ base, int64_t rs,
-                                    int row0, int nvalid) {
-  const int t = threadIdx.x;
-  const int row = min(row0 + (t >> 2), nvalid - 1);
-  const uint16_t* g = base + (int64_t)row * rs + 8 * (t & 3);
-  st.k0 = *reinterpret_cast<const u32x4_t*>(g);
-  st.k1 = *reinterpret_cast<const u32x4_t*>(g + 32);
-}
-__device__ inline void kstage_store(const KStage& st, uint16_t* Kt) {
-  const int t = threadIdx.x, row = t >> 2, cp = t & 3, f = swz(row);
-  *reinterpret_cast<u32x4_t*>(Kt + row * 64 + 8 * (cp ^ f)) = st.k0;
-  *reinterpret_cast<u32x4_t*>(Kt + row * 64 + 8 * ((cp + 4) ^ f)) = st.k1;
+// ---------------------------------------------------------------------------
+// Tile loop over direct-to-LDS tiles. Step i:
+//   direct loads K(i+1), V(i+1) and meta(i+1) into the other buffers
+//   S = K(i) Q^T; bias / masks; online softmax; O += V(i)^T P^T
+//   barrier (tile i+1 landed, everyone is done with tile i)
+// Each K and V tile has two LDS buffers, distinct __shared__ objects named
+// statically in each unrolled step, so the compiler can tell the direct loads
+// from the operand reads and does not wait for the former before the latter.
+// The policy P supplies, for virtual tile index i in [0, n):
+//   int  key0(i)
+//   void loadK(int i, uint16_t* Kt), loadV(int i, uint16_t* Vt)   direct loads
+//   void meta(int i, int slot)          per-tile LDS metadata, slot = i & 1
+//   bool wave_active()                  the wave has a valid query row
+//   static constexpr bool kAllActive    every tile is active for such waves
+//   bool active(int i)                  the wave computes tile i
+//   bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot)   bias / masks;
+//                                       returns "exact" for softmax_exp
+// ---------------------------------------------------------------------------
+
+// Issues the loads and metadata of tiles 0 and 1; call before the Q set-up so
+// that their latency overlaps it, then attn_loop_db.
+template <typename P>
+__device__ inline void attn_pipe_start(P& pol, int n, uint16_t* __restrict__ K0,
+                                       uint16_t* __restrict__ K1, uint16_t* __restrict__ V0) {
+  if (n <= 0) return;
+  pol.loadK(0, K0);
+  pol.loadV(0, V0);
+  pol.meta(0, 0);
+  if (n > 1) {
+    pol.loadK(1, K1);
+    pol.meta(1, 1);
+  }
 }
 
-// ---------------------------------------------------------------------------
-// Tile loop over direct-to-LDS tiles. Policy P supplies, for virtual tile i:
-//   int  key0(i)
-//   void load(int i, uint16_t* Kt, uint16_t* Vt)  issue direct loads (K too
-//                                                  unless KSTAGED)
-//   void kfetch(KStage&, int i) / void kcommit(KStage&, int i, uint16_t* Kt)
-//                                                  (KSTAGED: registers, rotate,
-//                                                  store)
-//   void meta(int i, int slot)                     per-tile LDS metadata
-//   bool active(int i)
-//   bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot)
-// LDS: buf0 and buf1 (distinct __shared__ arrays) of kBuf2Elems each, K tile
-// then V tile.
-// ---------------------------------------------------------------------------
-template <typename E, bool KSTAGED, typename P>
-__device__ inline void attn_loop_direct(P& pol, uint16_t* __restrict__ buf0,
-                                        uint16_t* __restrict__ buf1, int n,
-                                        const u32x4_t (&qf)[4], float c, float& m, float& l,
-                                        f32x16_t& o0, f32x16_t& o1) {
+template <typename E, typename P>
+__device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t* __restrict__ K1,
+                                    uint16_t* __restrict__ V0, uint16_t* __restrict__ V1, int n,
+                                    const u32x4_t (&qf)[4], float c, float& m, float& l,
+                                    f32x16_t& o0, f32x16_t& o1) {
   if (n <= 0) return;
   KOff ko;
   VOff vo;
   k_offsets(ko);
   v_offsets(vo);
-  KStage ks;
-  pol.load(0, buf0, buf0 + kTileElems);
-  if (KSTAGED) {
-    pol.kfetch(ks, 0);
-    pol.kcommit(ks, 0, buf0);
-  }
-  pol.meta(0, 0);
+  const bool wave_on = __builtin_amdgcn_readfirstlane((int)pol.wave_active()) != 0;
   tile_barrier();
-  // buf0 and buf1 are distinct LDS objects and each step names them
-  // statically, so the compiler can tell that the direct loads into nxt do not
-  // alias the reads of cur and does not wait for them before computing.
-  auto step = [&](int i, uint16_t* __restrict__ cur, uint16_t* __restrict__ nxt, int b) {
+  auto step = [&](int i, uint16_t* __restrict__ Kc, uint16_t* __restrict__ Vc,
+                  uint16_t* __restrict__ Kn, uint16_t* __restrict__ Vn, int b) {
+    // tile 1's K and meta were issued with tile 0
     if (i + 1 < n) {
-      pol.load(i + 1, nxt, nxt + kTileElems);
-      if (KSTAGED) pol.kfetch(ks, i + 1);
-      pol.meta(i + 1, b ^ 1);
+      if (i > 0) {
+        pol.loadK(i + 1, Kn);
+        pol.meta(i + 1, b ^ 1);
+      }
+      pol.loadV(i + 1, Vn);
     }
-    if (pol.active(i)) {
+    if (wave_on && (P::kAllActive || __builtin_amdgcn_readfirstlane((int)pol.active(i)) != 0)) {
       f32x16_t s0, s1;
-      qk_tile_sw<E>(cur, ko, qf, s0, s1);
+      qk_tile_sw<E>(Kc, ko, qf, s0, s1);
       const bool exact = pol.modify(s0, s1, i, b);
       u32x4_t p[4];
       softmax_tile<E>(s0, s1, c, m, l, o0, o1, p, exact);
-      pv_tile_sw<E>(cur + kTileElems, vo, p, o0, o1);
+      pv_tile_sw<E>(Vc, vo, p, o0, o1);
     }
-    if (KSTAGED && i + 1 < n) pol.kcommit(ks, i + 1, nxt);
     tile_barrier();
   };
   int i = 0;
   for (; i + 1 < n; i += 2) {
-    step(i, buf0, buf1, 0);
-    step(i + 1, buf1, buf0, 1);
+    step(i, K0, V0, K1, V1, 0);
+    step(i + 1, K1, V1, K0, V0, 1);
   }
-  if (i < n) step(i, buf0, buf1, 0);
+  if (i < n) step(i, K0, V0, K1, V1, 0);
 }
 
 // Rotates the Q operand in registers (non-interleaved RoPE halves): the lane's

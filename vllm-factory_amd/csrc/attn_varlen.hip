@@ -5,10 +5,14 @@
 // (models/modernbert/modernbert_encoder.py:236-255, :491-550): work is cut per
 // sequence by cu_seqlens, so cross-sequence pairs are never computed, and a
 // sliding-window layer only visits the key tiles its rows can see.
-// RoPE (non-interleaved halves) is applied in the kernel from an fp32 cos/sin
-// table (vfk_rope_table, the HF ModernBertRotaryEmbedding values): Q once per
-// row in registers, K as each tile is staged.
+// RoPE (non-interleaved halves) uses an fp32 cos/sin table (vfk_rope_table,
+// the HF ModernBertRotaryEmbedding values). K is rotated once by a pre-pass
+// into a head-major workspace [H][T][64] (the role of the reference's separate
+// rotary step, kernels/fused_rope_global.py); Q is rotated in registers by the
+// attention kernel as it loads its rows.
 #include <math.h>
+
+#include <algorithm>
 
 #include "attn_core.h"
 #include "launch_util.h"
@@ -22,6 +26,8 @@ struct VarlenArgs {
   float c2;                 // softmax scale * log2(e)
   const float* rope;        // optional [positions][32][2] (cos, sin) table
   const uint8_t* key_valid; // optional, [T]
+  const void* kr;           // RoPE: rotated K, head-major [H][T][64]
+  int64_t T;
 };
 
 // cos/sin table of HF rotary embeddings: row p, f < 32:
@@ -49,40 +55,73 @@ __global__ __launch_bounds__(256) void rope_table_kernel(RopeTableArgs a) {
 constexpr int kPenOff = 192;
 constexpr int kPenLen = 2 * kPenOff;
 
+// K rotation pre-pass: block (s, kt) rotates rows [64 kt, 64 kt + 64) of
+// sequence s for every head; thread t handles row t >> 2 and d chunks
+// cp = t & 3 and cp + 4 (the rotate-half partners d and d + 32), loading the
+// row's cos/sin once for all heads.
+template <typename E>
+__global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int nkt) {
+  const int kt = blockIdx.x % nkt;
+  const int s = blockIdx.x / nkt;
+  const int tok0 = a.cu[s];
+  const int n = a.cu[s + 1] - tok0;
+  const int row = kt * 64 + (threadIdx.x >> 2);
+  if (row >= n) return;
+  const int cp = threadIdx.x & 3;
+  RopeK rk;
+  rope_k_fetch(rk, a.rope, row, true);
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(a.k) + (int64_t)(tok0 + row) * a.ks[0] + 8 * cp;
+  uint16_t* dst = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(a.kr)) +
+                  (int64_t)(tok0 + row) * 64 + 8 * cp;
+  const int64_t hs = (int64_t)a.T * 64;
+  constexpr int kU = 4;  // heads in flight per thread
+  for (int h0 = 0; h0 < a.H; h0 += kU) {
+    u32x4_t k0[kU], k1[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (h0 + u < a.H) {
+        const uint16_t* p = src + (int64_t)(h0 + u) * a.ks[1];
+        k0[u] = *reinterpret_cast<const u32x4_t*>(p);
+        k1[u] = *reinterpret_cast<const u32x4_t*>(p + 32);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (h0 + u < a.H) {
+        rope_k_apply<E>(k0[u], k1[u], rk);
+        uint16_t* q = dst + (h0 + u) * hs;
+        *reinterpret_cast<u32x4_t*>(q) = k0[u];
+        *reinterpret_cast<u32x4_t*>(q + 32) = k1[u];
+      }
+    }
+  }
+}
+
 template <typename E, bool ROPE, bool LOCAL, bool KVALID>
 struct VarlenPolicy {
   const VarlenArgs* a;
-  const uint16_t* Kp;
-  const uint16_t* Vp;
-  int tok0, n, kt0, t, hl, qrow, wq_lo, wq_hi, window;
-  RopeK rk;
-  float* kmask;  // [2][kBN]: 0 or -inf per key of the tile in that slot
-  int* kflag;    // [2]: any key of the tile masked
+  TileSrc ksrc, vsrc;
+  int tok0, n, kt0, t, hl, qrow, wq_lo, wq_hi, window, tail0;
+  float* kmask;  // KVALID: [2][kBN], 0 or -inf per key of the tile in slot i & 1;
+                 // else [kBN]: the mask of the sequence's last, partial tile
+  int* kflag;    // KVALID: [2], any key of the tile masked
   const float* pen;
 
   __device__ int key0(int i) const { return (kt0 + i) * kBN; }
-  __device__ void load(int i, uint16_t* Kt, uint16_t* Vt) {
-    tile_load_direct(Vp, a->vs[0], key0(i), n, Vt);
-    if (!ROPE) tile_load_direct(Kp, a->ks[0], key0(i), n, Kt);
-  }
-  __device__ void kfetch(KStage& st, int i) {
-    kstage_fetch(st, Kp, a->ks[0], key0(i), n);
-    rope_k_fetch(rk, a->rope, min(key0(i) + (t >> 2), n - 1), true);
-  }
-  __device__ void kcommit(KStage& st, int i, uint16_t* Kt) {
-    rope_k_apply<E>(st.k0, st.k1, rk);
-    kstage_store(st, Kt);
-  }
+  __device__ void loadK(int i, uint16_t* Kt) { tile_load_buf(ksrc, key0(i), Kt); }
+  __device__ void loadV(int i, uint16_t* Vt) { tile_load_buf(vsrc, key0(i), Vt); }
   __device__ void meta(int i, int slot) {
+    if (!KVALID) return;
     if (t < kBN) {  // wave 0: one key per lane
       const int j = key0(i) + t;
-      bool ok = j < n;
-      if (KVALID) ok = ok && a->key_valid[tok0 + j] != 0;
+      const bool ok = j < n && a->key_valid[tok0 + j] != 0;
       kmask[slot * kBN + t] = ok ? 0.f : -INFINITY;
       const unsigned long long dead = __builtin_amdgcn_ballot_w64(!ok);
       if (t == 0) kflag[slot] = dead != 0ull;
     }
   }
+  static constexpr bool kAllActive = !LOCAL;
+  __device__ bool wave_active() const { return wq_lo < n; }
   __device__ bool active(int i) const {
     if (wq_lo >= n) return false;
     if (!LOCAL) return true;
@@ -90,7 +129,11 @@ struct VarlenPolicy {
     return k0 <= wq_hi + window && k0 + kBN - 1 >= wq_lo - window;
   }
   __device__ bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot) const {
-    if (kflag[slot]) add_by_key(s0, s1, kmask + slot * kBN + 4 * hl);
+    if (KVALID) {
+      if (kflag[slot]) add_by_key(s0, s1, kmask + slot * kBN + 4 * hl);
+    } else if (key0(i) == tail0) {
+      add_by_key(s0, s1, kmask + 4 * hl);
+    }
     if (LOCAL) {
       const int k0 = key0(i);
       if (wq_hi - k0 > window || k0 + kBN - 1 - wq_lo > window)
@@ -103,8 +146,10 @@ struct VarlenPolicy {
 
 template <typename E, bool ROPE, bool LOCAL, bool KVALID>
 __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenArgs a) {
-  __shared__ __align__(16) uint16_t buf0[kBuf2Elems];
-  __shared__ __align__(16) uint16_t buf1[kBuf2Elems];
+  __shared__ __align__(16) uint16_t K0[kTileElems];
+  __shared__ __align__(16) uint16_t K1[kTileElems];
+  __shared__ __align__(16) uint16_t V0[kTileElems];
+  __shared__ __align__(16) uint16_t V1[kTileElems];
   __shared__ float kmask[2 * kBN];
   __shared__ int kflag[2];
   __shared__ float pen[LOCAL ? kPenLen : 1];
@@ -133,26 +178,38 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenArgs a) {
   }
   const int kt_begin = klo / kBN;
   const int kt_end = (khi + kBN - 1) / kBN;
+  // start of the sequence's partial last key tile (none: -1)
+  const int tail0 = (n % kBN) ? (n / kBN) * kBN : -1;
+  if (!KVALID && t < kBN) kmask[t] = (tail0 + t < n) ? 0.f : -INFINITY;
 
   const int wq_lo = q0 + w * 32;
   const int qrow = wq_lo + (lane & 31);
   const bool qvalid = qrow < n;
 
-  u32x4_t qf[4];
-  load_q(qf, Qp + (int64_t)qrow * a.qs[0], qvalid);
-  if (ROPE && qvalid) rope_q_table<E>(qf, a.rope + (int64_t)qrow * 64);
-
   VarlenPolicy<E, ROPE, LOCAL, KVALID> pol;
   pol.a = &a;
-  pol.Kp = reinterpret_cast<const uint16_t*>(a.k) + (int64_t)tok0 * a.ks[0] + h * a.ks[1];
-  pol.Vp = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)tok0 * a.vs[0] + h * a.vs[1];
+  if (ROPE)
+    tile_src_init(pol.ksrc, reinterpret_cast<const uint16_t*>(a.kr) + ((int64_t)h * a.T + tok0) * 64,
+                  64, n);
+  else
+    tile_src_init(pol.ksrc, reinterpret_cast<const uint16_t*>(a.k) + (int64_t)tok0 * a.ks[0] + h * a.ks[1],
+                  (int)a.ks[0], n);
+  tile_src_init(pol.vsrc, reinterpret_cast<const uint16_t*>(a.v) + (int64_t)tok0 * a.vs[0] + h * a.vs[1],
+                (int)a.vs[0], n);
   pol.tok0 = tok0; pol.n = n; pol.kt0 = kt_begin; pol.t = t; pol.hl = hl; pol.qrow = qrow;
-  pol.wq_lo = wq_lo; pol.wq_hi = min(wq_lo + 31, n - 1); pol.window = a.window;
+  pol.wq_lo = wq_lo; pol.wq_hi = min(wq_lo + 31, n - 1); pol.window = a.window; pol.tail0 = tail0;
   pol.kmask = kmask; pol.kflag = kflag; pol.pen = pen;
+
+  attn_pipe_start(pol, kt_end - kt_begin, K0, K1, V0);
+
+  u32x4_t qf[4];
+  load_q(qf, Qp + (int64_t)qrow * a.qs[0], qvalid);
+  // rows past n rotate zeros with the table row of position n - 1
+  if (ROPE) rope_q_table<E>(qf, a.rope + (int64_t)min(qrow, n - 1) * 64);
 
   float m = -INFINITY, l = 0.f;
   f32x16_t o0 = {}, o1 = {};
-  attn_loop_direct<E, ROPE>(pol, buf0, buf1, kt_end - kt_begin, qf, a.c2, m, l, o0, o1);
+  attn_loop_db<E>(pol, K0, K1, V0, V1, kt_end - kt_begin, qf, a.c2, m, l, o0, o1);
 
   const float l_tot = half_swap_sum(l);
   if (qvalid) {
@@ -267,12 +324,19 @@ static int check_thd(const vfk_tensor* t, const char* name, int dtype, int64_t T
   return VFK_OK;
 }
 
+extern "C" int64_t vfk_varlen_attn_workspace_bytes(int32_t dtype, int64_t total_tokens,
+                                                  int32_t num_heads, int32_t rope) {
+  if (!rope || dtype == VFK_F32 || total_tokens <= 0 || num_heads <= 0) return 0;
+  return total_tokens * num_heads * kHD * 2;
+}
+
 extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
                                    const vfk_tensor* v, const int32_t* cu_seqlens,
                                    int32_t num_seqs, int32_t max_seqlen,
                                    int32_t window, const float* rope_cos_sin,
                                    int32_t rope_positions, const uint8_t* key_valid,
-                                   float softmax_scale, vfk_tensor* out, void* stream) {
+                                   float softmax_scale, void* workspace,
+                                   int64_t workspace_bytes, vfk_tensor* out, void* stream) {
   int rc = check_tensor(q, "q", 3);
   if (rc) return rc;
   const int dt = q->dtype;
@@ -292,7 +356,7 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
     a.qs[i] = q->stride[i]; a.ks[i] = k->stride[i];
     a.vs[i] = v->stride[i]; a.os[i] = out->stride[i];
   }
-  a.cu = cu_seqlens; a.nseq = num_seqs; a.H = (int)H;
+  a.cu = cu_seqlens; a.nseq = num_seqs; a.H = (int)H; a.T = T;
   a.window = window < 0 ? -1 : window;
   if (!(softmax_scale > 0.f) || !isfinite(softmax_scale))
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: softmax_scale must be > 0");
@@ -313,6 +377,28 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
     hipLaunchKernelGGL(varlen_fwd_f32_kernel, dim3((unsigned)blocks), dim3(64), 0, st, a);
     return launch_status("vfk_varlen_attn_fwd");
   }
+  // buffer resources cover max_seqlen rows of one slice: byte sizes < 2^31
+  const int64_t span = (int64_t)max_seqlen * 2;
+  if (span * std::max<int64_t>(a.ks[0], 64) >= (1ll << 31) || span * a.vs[0] >= (1ll << 31))
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: max_seqlen x row stride too large");
+  const bool rope = a.rope != nullptr;
+  if (rope) {
+    const int64_t need = vfk_varlen_attn_workspace_bytes(dt, T, (int32_t)H, 1);
+    if (!workspace || workspace_bytes < need)
+      return set_error(VFK_ERR_INVALID, "vfk_varlen_attn_fwd: RoPE needs a workspace of %lld bytes",
+                       (long long)need);
+    if (!aligned16(workspace))
+      return set_error(VFK_ERR_INVALID, "workspace must be 16-byte aligned");
+    a.kr = workspace;
+    const int nkt = ceil_div(max_seqlen, 64);
+    const int64_t pblocks = (int64_t)num_seqs * nkt;
+    if (pblocks >= (1ll << 31))
+      return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: grid too large");
+    if (dt == VFK_BF16)
+      hipLaunchKernelGGL(rope_k_pack_kernel<BF16>, dim3((unsigned)pblocks), dim3(256), 0, st, a, nkt);
+    else
+      hipLaunchKernelGGL(rope_k_pack_kernel<F16>, dim3((unsigned)pblocks), dim3(256), 0, st, a, nkt);
+  }
   if (a.window >= 0 && a.window >= max_seqlen) a.window = -1;  // window covers every pair
   if (a.window > kPenOff - kBM)
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: window %d > %d", a.window, kPenOff - kBM);
@@ -320,7 +406,7 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
   const int64_t blocks = (int64_t)a.nqt * H * num_seqs;
   if (blocks >= (1ll << 31))
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: grid too large");
-  const bool local = a.window >= 0, kv = key_valid != nullptr, rope = a.rope != nullptr;
+  const bool local = a.window >= 0, kv = key_valid != nullptr;
 #define VFK_VL(E, R, L, K) \
   hipLaunchKernelGGL((varlen_fwd_kernel<E, R, L, K>), dim3((unsigned)blocks), dim3(256), 0, st, a)
 #define VFK_VL_E(E)                                                   \

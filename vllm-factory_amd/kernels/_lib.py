@@ -37,8 +37,9 @@ _P = ctypes.POINTER(VfkTensor)
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
 _f32 = ctypes.c_float
+_i64 = ctypes.c_int64
 
-# name -> argtypes (restype is always int)
+# name -> argtypes (restype int unless listed in _RESTYPES)
 _SIGNATURES = {
     "vfk_abi_version": [],
     "vfk_t5_bucket": [_vp, _vp, ctypes.c_int64, _i32, _i32, _i32],
@@ -46,7 +47,9 @@ _SIGNATURES = {
     "vfk_flash_rpb_fwd": [_P, _P, _P, _P, _i32, _i32, _i32, _P, _f32, _P, _vp],
     "vfk_flash_deberta_fwd": [_P, _P, _P, _vp, _P, _P, _i32, _f32, _i32, _i32, _i32, _P, _vp],
     "vfk_deberta_fused_fwd": [_P, _P, _P, _vp, _P, _P, _f32, _i32, _i32, _i32, _P, _vp],
-    "vfk_varlen_attn_fwd": [_P, _P, _P, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _P, _vp],
+    "vfk_varlen_attn_fwd": [_P, _P, _P, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _i64,
+                            _P, _vp],
+    "vfk_varlen_attn_workspace_bytes": [_i32, _i64, _i32, _i32],
     "vfk_rope_table": [_f32, _i32, _vp, _vp],
     "vfk_rope_fwd": [_P, _P, _P, _P, _vp],
     "vfk_layernorm_fwd": [_P, _P, _P, _P, _f32, _P, _P, _vp],
@@ -54,6 +57,8 @@ _SIGNATURES = {
     "vfk_glu_fwd": [_i32, _P, _P, _P, _vp],
     "vfk_residual_add": [_P, _P, _P, _vp],
 }
+
+_RESTYPES = {"vfk_varlen_attn_workspace_bytes": ctypes.c_int64}
 
 _lib: Optional[ctypes.CDLL] = None
 
@@ -75,7 +80,7 @@ def load() -> ctypes.CDLL:
     for name, argtypes in _SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_int
+        fn.restype = _RESTYPES.get(name, ctypes.c_int)
     lib.vfk_last_error.argtypes = []
     lib.vfk_last_error.restype = ctypes.c_char_p
     _lib = lib

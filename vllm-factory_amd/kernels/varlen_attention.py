@@ -10,8 +10,9 @@ the same attention per sequence from cu_seqlens:
     0 per sequence, which is what the reference's block mask keys on);
   * window < 0: global layer; window = w: key j visible iff |i - j| <= w
     (ModernBERT local layers use w = local_attention // 2 = 64);
-  * rope_theta > 0: q and k are rotated in the kernel with the HF
-    ModernBertRotaryEmbedding frequencies (non-interleaved halves);
+  * rope_theta > 0: q and k are rotated with the HF ModernBertRotaryEmbedding
+    frequencies (non-interleaved halves): k once by a pre-pass into a
+    workspace, q inside the attention kernel (inputs are never written);
   * key_valid[t] == 0 hides key t (the reference's token-id 50284 mask).
 
 Rows that see no key at all are returned as zeros.
@@ -67,14 +68,19 @@ def varlen_rope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         kv_ptr = key_valid.data_ptr()
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
     tab_ptr, tab_n = None, 0
-    if rope_theta and rope_theta > 0:
+    rope = bool(rope_theta and rope_theta > 0)
+    if rope:
         tab = rope_table(rope_theta, int(max_seqlen), dev)
         tab_ptr, tab_n = tab.data_ptr(), tab.shape[0]
+    ws_bytes = int(_lib.load().vfk_varlen_attn_workspace_bytes(
+        _lib.dtype_code(q.dtype), int(q.shape[0]), int(q.shape[1]), int(rope)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     _lib.on_device(
         "vfk_varlen_attn_fwd", dev,
         _lib.ref(_lib.desc(qq)), _lib.ref(_lib.desc(kk)), _lib.ref(_lib.desc(vv)),
         cu_seqlens.data_ptr(), int(cu_seqlens.numel() - 1), int(max_seqlen),
         int(window), tab_ptr, int(tab_n), kv_ptr, float(scale),
+        ws.data_ptr() if ws is not None else None, ws_bytes,
         _lib.ref(_lib.desc(out)),
     )
     return out
