@@ -3,6 +3,8 @@
 // HBM access on the fast path is a 128-bit load or store.
 #include <math.h>
 
+#include <algorithm>
+
 #include "launch_util.h"
 #include "vfk_common.h"
 
@@ -65,10 +67,29 @@ __device__ inline float ld_any(const void* base, int dt, int64_t i) {
   return F16::to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
 }
 
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of LANES (4..64) lanes, every lane gets the sum:
+// DPP quad permutes and row mirrors inside 16 lanes, then the gfx950
+// permlane16/32 swaps across rows; no LDS round trips.
 template <int LANES>
 __device__ inline float group_sum(float v) {
-#pragma unroll
-  for (int o = LANES / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  static_assert(LANES >= 4 && LANES <= 64 && (LANES & (LANES - 1)) == 0, "group size");
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+  if (LANES >= 8) v += dpp_f<0x141>(v);   // row_half_mirror: other quad of 8
+  if (LANES >= 16) v += dpp_f<0x140>(v);  // row_mirror: other 8 of 16
+  if (LANES >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = __int_as_float(r[0]) + __int_as_float(r[1]);  // lane ^ 16
+  }
+  if (LANES >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = __int_as_float(r[0]) + __int_as_float(r[1]);  // lane ^ 32
+  }
   return v;
 }
 
@@ -81,82 +102,158 @@ struct NormArgs {
   void* res_out; int64_t res_out_rs;      // optional: writes x + res
   const void* w; int w_dt;                // optional weight
   const void* b; int b_dt;                // optional bias (LayerNorm only)
+  int w_vec, b_vec;                       // 16-byte aligned: 128-bit loads allowed
   void* y; int64_t y_rs;
   int64_t rows; int n; float eps;
 };
 
-template <int DT, int LANES, int CH, bool RMS>
-__global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
+// Grid-stride over rows: each lane owns the same columns in every row, so its
+// weight / bias slices are loaded once into registers; only x (and the
+// residual) stream through, as 128-bit loads. The row loop is instantiated
+// per residual mode so that its body is straight-line: all loads of a row are
+// issued before the first use, partial chunks and rows past the end load a
+// clamped in-bounds address and are masked arithmetically.
+// This lane's slice of a [n] parameter vector (weight or bias) as fp32, or
+// `fill` where absent. 128-bit loads when its dtype matches x (the common
+// case), element loads otherwise; all issued before any use.
+template <int DT, int LANES, int CH>
+__device__ inline void load_param(const void* p, int p_dt, int p_vec, int nch, int l, float fill,
+                                  float (&v)[CH][Elt<DT>::VEC]) {
   using L = Elt<DT>;
   constexpr int VEC = L::VEC;
+  if (!p) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) v[c][i] = fill;
+    return;
+  }
+  if (p_dt == DT && p_vec) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) L::load(p, (int64_t)min(c * LANES + l, nch - 1) * VEC, v[c]);
+  } else {
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+        v[c][i] = ld_any(p, p_dt, (int64_t)min(c * LANES + l, nch - 1) * VEC + i);
+  }
+}
+
+template <int DT, int LANES, int CH, bool RES>
+__device__ inline void norm_load_row(const NormArgs& a, int64_t row, int l, int nch,
+                                     float (&x)[CH][Elt<DT>::VEC]) {
+  using L = Elt<DT>;
+  constexpr int VEC = L::VEC;
+  const int64_t rr = row < a.rows ? row : a.rows - 1;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = min(c * LANES + l, nch - 1);
+    L::load(a.x, rr * a.x_rs + (int64_t)ch * VEC, x[c]);
+  }
+  if (RES) {
+    float r[CH][VEC];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int ch = min(c * LANES + l, nch - 1);
+      L::load(a.res, rr * a.res_rs + (int64_t)ch * VEC, r[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) x[c][i] += r[c][i];
+  }
+}
+
+template <int DT, int LANES, int CH, bool RMS, bool RES, bool RES_OUT>
+__device__ inline void norm_rows(const NormArgs& a, const float (&w)[CH][Elt<DT>::VEC],
+                                 const float (&bb)[CH][Elt<DT>::VEC]) {
+  using L = Elt<DT>;
+  constexpr int VEC = L::VEC;
+  constexpr int RPW = 64 / LANES;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int sub = lane / LANES;
   const int l = lane % LANES;
-  constexpr int RPW = 64 / LANES;
-  const int64_t row = ((int64_t)blockIdx.x * 4 + wave) * RPW + sub;
-  const bool active = row < a.rows;
   const int nch = a.n / VEC;
-  float x[CH][VEC];
-  float s = 0.f;
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int ch = c * LANES + l;
-    if (active && ch < nch) {
-      L::load(a.x, row * a.x_rs + (int64_t)ch * VEC, x[c]);
-      if (a.res) {
-        float r[VEC];
-        L::load(a.res, row * a.res_rs + (int64_t)ch * VEC, r);
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) x[c][i] += r[i];
-        if (a.res_out) L::store(a.res_out, row * a.res_out_rs + (int64_t)ch * VEC, x[c]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) x[c][i] = 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) s += RMS ? x[c][i] * x[c][i] : x[c][i];
-  }
-  s = group_sum<LANES>(s);
   const float inv_n = 1.0f / (float)a.n;
-  float mean = 0.f, rstd;
-  if (RMS) {
-    rstd = 1.0f / sqrtf(s * inv_n + a.eps);
-  } else {
-    mean = s * inv_n;
-    float v = 0.f;
+  const int64_t step = (int64_t)gridDim.x * 4 * RPW;
+  int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * RPW;  // wave-uniform
+  if (row0 >= a.rows) return;
+  float x[CH][VEC];
+  norm_load_row<DT, LANES, CH, RES>(a, row0 + sub, l, nch, x);
+  for (; row0 < a.rows; row0 += step) {
+    const int64_t row = row0 + sub;
+    // the next row's loads are in flight while this row is reduced
+    float xn[CH][VEC];
+    const bool more = row0 + step < a.rows;
+    if (more) norm_load_row<DT, LANES, CH, RES>(a, row + step, l, nch, xn);
+    float s = 0.f;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int ch = c * LANES + l;
-      if (ch < nch) {
+      const float keep = (c * LANES + l < nch) ? 1.f : 0.f;  // duplicate chunk: no weight
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) t += RMS ? x[c][i] * x[c][i] : x[c][i];
+      s += keep * t;
+    }
+    s = group_sum<LANES>(s);
+    float mean = 0.f, rstd;
+    if (RMS) {
+      rstd = 1.0f / sqrtf(s * inv_n + a.eps);
+    } else {
+      mean = s * inv_n;
+      float v = 0.f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const float keep = (c * LANES + l < nch) ? 1.f : 0.f;
+        float t = 0.f;
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          float d = x[c][i] - mean;
-          v += d * d;
+          const float d = x[c][i] - mean;
+          t += d * d;
+        }
+        v += keep * t;
+      }
+      v = group_sum<LANES>(v);
+      rstd = 1.0f / sqrtf(v * inv_n + a.eps);
+    }
+    if (row < a.rows) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int ch = c * LANES + l;
+        if (ch < nch) {
+          if (RES_OUT) L::store(a.res_out, row * a.res_out_rs + (int64_t)ch * VEC, x[c]);
+          float y[VEC];
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) y[i] = (x[c][i] - mean) * rstd * w[c][i] + bb[c][i];
+          L::store(a.y, row * a.y_rs + (int64_t)ch * VEC, y);
         }
       }
     }
-    v = group_sum<LANES>(v);
-    rstd = 1.0f / sqrtf(v * inv_n + a.eps);
-  }
-  if (!active) return;
+    if (more) {
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int ch = c * LANES + l;
-    if (ch < nch) {
-      float y[VEC];
+      for (int c = 0; c < CH; ++c)
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        const int col = ch * VEC + i;
-        float t = (x[c][i] - mean) * rstd;
-        if (a.w) t *= ld_any(a.w, a.w_dt, col);
-        if (!RMS && a.b) t += ld_any(a.b, a.b_dt, col);
-        y[i] = t;
-      }
-      L::store(a.y, row * a.y_rs + (int64_t)ch * VEC, y);
+        for (int i = 0; i < VEC; ++i) x[c][i] = xn[c][i];
     }
   }
+}
+
+template <int DT, int LANES, int CH, bool RMS>
+__global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
+  constexpr int VEC = Elt<DT>::VEC;
+  const int l = (threadIdx.x & 63) % LANES;
+  const int nch = a.n / VEC;
+  float w[CH][VEC], bb[CH][VEC];
+  load_param<DT, LANES, CH>(a.w, a.w_dt, a.w_vec, nch, l, 1.f, w);
+  load_param<DT, LANES, CH>(RMS ? nullptr : a.b, a.b_dt, a.b_vec, nch, l, 0.f, bb);
+  if (!a.res)
+    norm_rows<DT, LANES, CH, RMS, false, false>(a, w, bb);
+  else if (!a.res_out)
+    norm_rows<DT, LANES, CH, RMS, true, false>(a, w, bb);
+  else
+    norm_rows<DT, LANES, CH, RMS, true, true>(a, w, bb);
 }
 
 // Any width / alignment: one 256-thread block per row, LDS reduction.
@@ -210,7 +307,11 @@ __global__ __launch_bounds__(256) void norm_scalar_kernel(NormArgs a) {
 template <int DT, int LANES, bool RMS>
 static void launch_norm_vec(const NormArgs& a, int ch, hipStream_t st) {
   const int rows_per_block = 4 * (64 / LANES);
-  dim3 grid(ceil_div(a.rows, rows_per_block));
+  // at most 2048 blocks (8 per CU), each striding over the same number of
+  // row groups so that no block is left with a partial last round
+  const int64_t groups = ceil_div(a.rows, rows_per_block);
+  const int64_t per = ceil_div(groups, 2048);
+  dim3 grid((unsigned)ceil_div(groups, per));
 #define VFK_NORM_CASE(C)                                                   \
   case C:                                                                  \
     hipLaunchKernelGGL((norm_vec_kernel<DT, LANES, C, RMS>), grid, dim3(256), \
@@ -300,13 +401,13 @@ static int norm_entry(const vfk_tensor* x, const vfk_tensor* residual,
     if ((rc = check_tensor(weight, "weight", 1))) return rc;
     if (weight->size[0] != n || weight->stride[0] != 1)
       return set_error(VFK_ERR_INVALID, "%s: weight must be contiguous [n]", name);
-    a.w = weight->data; a.w_dt = weight->dtype;
+    a.w = weight->data; a.w_dt = weight->dtype; a.w_vec = aligned16(a.w);
   }
   if (present(bias)) {
     if ((rc = check_tensor(bias, "bias", 1))) return rc;
     if (bias->size[0] != n || bias->stride[0] != 1)
       return set_error(VFK_ERR_INVALID, "%s: bias must be contiguous [n]", name);
-    a.b = bias->data; a.b_dt = bias->dtype;
+    a.b = bias->data; a.b_dt = bias->dtype; a.b_vec = aligned16(a.b);
   }
   if (rows == 0) return VFK_OK;
   hipStream_t st = (hipStream_t)stream;
