@@ -8,6 +8,8 @@
 // inner loop does one LDS read per score instead of a log and a gather.
 #include <math.h>
 
+#include <algorithm>
+
 #include "attn_core.h"
 #include "launch_util.h"
 
@@ -58,17 +60,82 @@ __device__ inline int rpb_bucket(const RpbArgs& a, int rel) {
 }
 
 // ---------------------------------------------------------------------------
-// bf16 / fp16 MFMA kernel
+// bf16 / fp16 MFMA kernel on the shared direct-to-LDS tile loop.
 // ---------------------------------------------------------------------------
-template <typename E, int MASK>
+template <typename E, int MASK, bool CAUSAL>
+struct RpbPolicy {
+  const RpbArgs* a;
+  TileSrc ksrc, vsrc;
+  const int* tiles;      // live key tiles (MASK_KEY) or nullptr = all in order
+  const int* tflag;      // MASK_KEY: per key tile, bit0 = some nonzero mask
+  float* maskt;          // MASK_KEY: [2][kBN] mask values of the tile in slot i & 1
+  const float* lut;      // bias per relative position (raw score units) or nullptr
+  int lut_base, b, h, t, hl, qrow, wq_lo, wq_hi;
+
+  static constexpr bool kAllActive = !CAUSAL;
+  __device__ int tile(int i) const { return tiles ? tiles[i] : i; }
+  __device__ int key0(int i) const { return tile(i) * kBN; }
+  __device__ void loadK(int i, uint16_t* Kt) { tile_load_buf(ksrc, key0(i), Kt); }
+  __device__ void loadV(int i, uint16_t* Vt) { tile_load_buf(vsrc, key0(i), Vt); }
+  __device__ void meta(int i, int slot) {
+    if (MASK == MASK_KEY && t < kBN) {
+      const int j = key0(i) + t;
+      maskt[slot * kBN + t] =
+          j < a->Lk ? mask_raw(ld_f(a->mask, a->mask_dt, b * a->ms[0] + h * a->ms[1] + j * a->ms[3]),
+                               a->inv_scale)
+                    : 0.f;
+    }
+  }
+  __device__ bool wave_active() const { return wq_lo < a->Lq; }
+  __device__ bool active(int i) const {
+    if (wq_lo >= a->Lq) return false;
+    return !CAUSAL || key0(i) <= wq_hi;
+  }
+  __device__ bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot) const {
+    const int k0 = key0(i);
+    if (lut) add_by_key(s0, s1, lut + k0 + lut_base);
+    bool exact = false;
+    if (MASK == MASK_KEY) {
+      if (tflag[tile(i)] & 1) {
+        add_by_key(s0, s1, maskt + slot * kBN + 4 * hl);
+        exact = true;  // tiles carrying additive mask values: exact exponent form
+      }
+    } else if (MASK == MASK_FULL) {
+      if (qrow < a->Lq) {
+        const int64_t mo = b * a->ms[0] + h * a->ms[1] + (int64_t)qrow * a->ms[2];
+        map_scores(s0, s1, [&](int e, float v) {
+          const int j = k0 + x_key(e, hl);
+          return j < a->Lk ? v + mask_raw(ld_f(a->mask, a->mask_dt, mo + (int64_t)j * a->ms[3]),
+                                          a->inv_scale)
+                           : v;
+        });
+      }
+      exact = true;
+    }
+    if (k0 + kBN > a->Lk || (CAUSAL && k0 + kBN - 1 > wq_lo)) {
+      map_scores(s0, s1, [&](int e, float v) {
+        const int j = k0 + x_key(e, hl);
+        return (j >= a->Lk || (CAUSAL && j > qrow)) ? -INFINITY : v;
+      });
+    }
+    return exact;
+  }
+};
+
+template <typename E, int MASK, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void rpb_fwd_kernel(RpbArgs a) {
+  __shared__ __align__(16) uint16_t K0[kTileElems];
+  __shared__ __align__(16) uint16_t K1[kTileElems];
+  __shared__ __align__(16) uint16_t V0[kTileElems];
+  __shared__ __align__(16) uint16_t V1[kTileElems];
+  __shared__ float maskt[MASK == MASK_KEY ? 2 * kBN : 1];
+  __shared__ int ntl;
   extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);
-  uint16_t* Vt = Ks + kKsElems;
-  float* maskt = reinterpret_cast<float*>(Vt + kVtElems);  // [kBN]
-  int* tflag = reinterpret_cast<int*>(maskt + kBN);        // [ntiles]
   const int ntiles_all = (a.Lk + kBN - 1) / kBN;
-  float* lut = reinterpret_cast<float*>(tflag + ((ntiles_all + 3) & ~3));
+  const int nt4 = (ntiles_all + 3) & ~3;
+  int* tflag = reinterpret_cast<int*>(smem);  // [nt4]
+  int* tiles = tflag + nt4;                   // [nt4]
+  float* lut = reinterpret_cast<float*>(tiles + nt4);
 
   const int nqt = (a.Lq + kBM - 1) / kBM;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
@@ -77,10 +144,6 @@ __global__ __launch_bounds__(256, 2) void rpb_fwd_kernel(RpbArgs a) {
   const int h = bh % a.H, b = bh / a.H;
   const int q0 = qt * kBM;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, hl = lane >> 5;
-
-  const uint16_t* Qp = reinterpret_cast<const uint16_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
-  const uint16_t* Kp = reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
-  const uint16_t* Vp = reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
 
   // ---- bias table over rel = key - query, rel in [-(q0+127), Lk-1-q0] ----
   const bool has_table = a.table != nullptr;
@@ -91,94 +154,65 @@ __global__ __launch_bounds__(256, 2) void rpb_fwd_kernel(RpbArgs a) {
       lut[e] = ld_f(a.table, a.table_dt, bk * a.tb0 + h * a.tb1) * a.inv_scale;
     }
   }
-  // ---- key-mask tile classification: bit0 = some nonzero, bit1 = some live
+  // ---- key tiles: causal limit, and (key mask) the tiles with a live key ----
   int kt_end = ntiles_all;
-  if (a.causal) kt_end = min(kt_end, (min(q0 + kBM, a.Lq) - 1) / kBN + 1);
-  bool any_live = true;
+  if (CAUSAL) kt_end = min(kt_end, (min(q0 + kBM, a.Lq) - 1) / kBN + 1);
+  int n = kt_end;
   if (MASK == MASK_KEY) {
-    for (int i = t; i < ntiles_all; i += 256) tflag[i] = 0;
+    for (int i = t; i < nt4; i += 256) tflag[i] = 0;
     __syncthreads();
     const char* mb = reinterpret_cast<const char*>(a.mask);
     for (int j = t; j < a.Lk; j += 256) {
       const float mv = ld_f(mb, a.mask_dt, b * a.ms[0] + h * a.ms[1] + j * a.ms[3]);
-      // live: not clamped, i.e. contributes unless a row has no live key
+      // bit0: some nonzero value; bit1: some key that is not clamped away
       const int f = (mv != 0.f ? 1 : 0) | (mask_raw(mv, a.inv_scale) > -1.0e30f ? 2 : 0);
       if (f) atomicOr(&tflag[j / kBN], f);
     }
     __syncthreads();
-    int live = 0;
-    for (int i = 0; i < kt_end; ++i) live |= tflag[i] & 2;
-    any_live = live != 0;
+    if (t == 0) {
+      // tiles whose every key is masked away are skipped, unless no key of
+      // the row range is live (then the reference averages all of them)
+      int live = 0;
+      for (int i = 0; i < kt_end; ++i) live |= tflag[i] & 2;
+      int c = 0;
+      for (int i = 0; i < kt_end; ++i)
+        if (!live || (tflag[i] & 2)) tiles[c++] = i;
+      ntl = c;
+    }
+    __syncthreads();
+    n = ntl;
   }
-  __syncthreads();
 
-  // ---- this lane's query row ----
-  const int qrow = q0 + w * 32 + (lane & 31);
-  const bool qvalid = qrow < a.Lq;
+  RpbPolicy<E, MASK, CAUSAL> pol;
+  pol.a = &a;
+  tile_src_init(pol.ksrc, reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1],
+                (int)a.ks[2], a.Lk);
+  tile_src_init(pol.vsrc, reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1],
+                (int)a.vs[2], a.Lk);
+  pol.tiles = MASK == MASK_KEY ? tiles : nullptr;
+  pol.tflag = tflag;
+  pol.maskt = maskt;
+  pol.lut = has_table ? lut : nullptr;
+  pol.b = b; pol.h = h; pol.t = t; pol.hl = hl;
+  pol.wq_lo = q0 + w * 32;
+  pol.qrow = pol.wq_lo + (lane & 31);
+  pol.wq_hi = min(pol.wq_lo + 31, a.Lq - 1);
+  // lut index of element e in the tile at key0: key0 + x_key(e, 0) + lut_base
+  pol.lut_base = 4 * hl - w * 32 - (lane & 31) + (kBM - 1);
+  attn_pipe_start(pol, n, K0, K1, V0);
+
+  const bool qvalid = pol.qrow < a.Lq;
   u32x4_t qf[4];
-  load_q(qf, Qp + (int64_t)qrow * a.qs[2], qvalid);
+  load_q(qf, reinterpret_cast<const uint16_t*>(a.q) + b * a.qs[0] + h * a.qs[1] +
+                 (int64_t)pol.qrow * a.qs[2], qvalid);
 
   float m = -INFINITY, l = 0.f;
   f32x16_t o0 = {}, o1 = {};
-  // lut index of element i in tile kt: kt*64 + x_key(i) + lut_base
-  const int lut_base = 4 * hl - w * 32 - (lane & 31) + (kBM - 1);
-
-  auto skip_tile = [&](int kt) -> bool {
-    if (MASK != MASK_KEY) return false;
-    return any_live && !(tflag[kt] & 2);
-  };
-
-  KVStage st;
-  int kt = 0;
-  while (kt < kt_end && skip_tile(kt)) ++kt;
-  if (kt < kt_end) kv_load(st, Kp, a.ks[2], Vp, a.vs[2], kt * kBN, a.Lk);
-  while (kt < kt_end) {
-    const int key0 = kt * kBN;
-    kv_store(st, Ks, Vt);
-    if (MASK == MASK_KEY) {
-      if (t < kBN) {
-        const int j = key0 + t;
-        maskt[t] = j < a.Lk ? mask_raw(ld_f(a.mask, a.mask_dt, b * a.ms[0] + h * a.ms[1] + j * a.ms[3]), a.inv_scale) : 0.f;
-      }
-    }
-    __syncthreads();
-    int nk = kt + 1;
-    while (nk < kt_end && skip_tile(nk)) ++nk;
-    if (nk < kt_end) kv_load(st, Kp, a.ks[2], Vp, a.vs[2], nk * kBN, a.Lk);
-
-    f32x16_t s0, s1;
-    qk_tile<E>(Ks, qf, s0, s1);
-    if (has_table) add_by_key(s0, s1, lut + key0 + lut_base);
-    if (MASK == MASK_KEY) {
-      if (tflag[kt] & 1) add_by_key(s0, s1, maskt + 4 * hl);
-    } else if (MASK == MASK_FULL) {
-      if (qvalid) {
-        const int64_t mo = b * a.ms[0] + h * a.ms[1] + (int64_t)qrow * a.ms[2];
-        map_scores(s0, s1, [&](int e, float v) {
-          const int j = key0 + x_key(e, hl);
-          return j < a.Lk ? v + mask_raw(ld_f(a.mask, a.mask_dt, mo + (int64_t)j * a.ms[3]), a.inv_scale) : v;
-        });
-      }
-    }
-    if (key0 + kBN > a.Lk || a.causal) {
-      map_scores(s0, s1, [&](int e, float v) {
-        const int j = key0 + x_key(e, hl);
-        return (j >= a.Lk || (a.causal && j > qrow)) ? -INFINITY : v;
-      });
-    }
-    // tiles carrying additive mask values take the exact exponent form
-    bool exact = false;
-    if (MASK == MASK_KEY) exact = (tflag[kt] & 1) != 0;
-    if (MASK == MASK_FULL) exact = true;
-    u32x4_t p[4];
-    softmax_tile<E>(s0, s1, a.c2, m, l, o0, o1, p, exact);
-    pv_tile<E>(Vt, p, o0, o1);
-    __syncthreads();
-    kt = nk;
-  }
+  attn_loop_db<E>(pol, K0, K1, V0, V1, n, qf, a.c2, m, l, o0, o1);
   const float l_tot = half_swap_sum(l);
   if (qvalid) {
-    uint16_t* orow = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1] + (int64_t)qrow * a.os[2];
+    uint16_t* orow = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1] +
+                     (int64_t)pol.qrow * a.os[2];
     store_out<E>(orow, o0, o1, l_tot);
   }
 }
@@ -336,20 +370,24 @@ extern "C" int vfk_flash_rpb_fwd(const vfk_tensor* q, const vfk_tensor* k,
       hipLaunchKernelGGL(rpb_fwd_f32_kernel<MASK_FULL>, grid, dim3(64), 0, st, a);
     return launch_status("vfk_flash_rpb_fwd");
   }
+  // tile buffer resources span Lk rows of one (batch, head): byte sizes < 2^31
+  if ((int64_t)Lk * std::max(a.ks[2], a.vs[2]) * 2 >= (1ll << 31))
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_rpb_fwd: Lk x row stride too large");
   const int ntiles = ceil_div(Lk, kBN);
   a.lut_len = a.table ? ntiles * kBN + kBM : 0;
-  const size_t lds = (size_t)(kKsElems + kVtElems) * 2 + kBN * 4 +
-                     ((ntiles + 3) & ~3) * 4 + (size_t)a.lut_len * 4;
-  if (lds > 160 * 1024)
-    return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_rpb_fwd: Lk=%lld needs %zu B of LDS",
-                     (long long)Lk, lds);
+  // dynamic LDS: tile flags and list, bias table (tiles and masks are static)
+  const size_t lds = (size_t)((ntiles + 3) & ~3) * 8 + (size_t)a.lut_len * 4;
+  if (lds + 4 * kTileElems * 2 + 2 * kBN * 4 > 160 * 1024)
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_rpb_fwd: Lk=%lld needs too much LDS",
+                     (long long)Lk);
   const int nqt = ceil_div(Lq, kBM);
   dim3 grid((unsigned)(nqt * B * H));
-#define VFK_RPB_LAUNCH(E)                                                              \
-  switch (mode) {                                                                      \
-    case MASK_NONE: hipLaunchKernelGGL((rpb_fwd_kernel<E, MASK_NONE>), grid, dim3(256), lds, st, a); break; \
-    case MASK_KEY: hipLaunchKernelGGL((rpb_fwd_kernel<E, MASK_KEY>), grid, dim3(256), lds, st, a); break;   \
-    default: hipLaunchKernelGGL((rpb_fwd_kernel<E, MASK_FULL>), grid, dim3(256), lds, st, a); break;        \
+#define VFK_RPB_GO(E, M, C) hipLaunchKernelGGL((rpb_fwd_kernel<E, M, C>), grid, dim3(256), lds, st, a)
+#define VFK_RPB_LAUNCH(E)                                                               \
+  switch (mode) {                                                                       \
+    case MASK_NONE: if (a.causal) VFK_RPB_GO(E, MASK_NONE, true); else VFK_RPB_GO(E, MASK_NONE, false); break; \
+    case MASK_KEY: if (a.causal) VFK_RPB_GO(E, MASK_KEY, true); else VFK_RPB_GO(E, MASK_KEY, false); break;    \
+    default: if (a.causal) VFK_RPB_GO(E, MASK_FULL, true); else VFK_RPB_GO(E, MASK_FULL, false); break;        \
   }
   if (dt == VFK_BF16) {
     VFK_RPB_LAUNCH(BF16)
@@ -357,5 +395,6 @@ extern "C" int vfk_flash_rpb_fwd(const vfk_tensor* q, const vfk_tensor* k,
     VFK_RPB_LAUNCH(F16)
   }
 #undef VFK_RPB_LAUNCH
+#undef VFK_RPB_GO
   return launch_status("vfk_flash_rpb_fwd");
 }
