@@ -10,7 +10,9 @@ sum_s 4*d*H*len_s^2 (global) + 4*d*H*#{|i-j| <= 64} (local).
 
 Extra figures in the same line: per-kernel roofline of the dominant kernel,
 the T5 RPB attention at mT5-large shapes, the DeBERTa disentangled attention,
-the memory-bound epilogues in GB/s, and the CPU oracle timed on the host.
+the memory-bound epilogues in GB/s, the end-to-end tokens/s of the full
+22-layer ModernBERT-base encoder over 256 packed sequences, and the CPU
+oracle timed on the host.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--only headline]
 """
@@ -217,6 +219,33 @@ def epilogue_bench(torch, args, c2):
     return res
 
 
+def encoder_config5(torch, args):
+    """Full ModernBERT-base encoder forward (22 layers, random-init bf16 weights)
+    over 256 packed sequences U{512..768}: end-to-end tokens/s and sequences/s."""
+    import workloads
+    from encoders.modernbert import modernbert_forward, random_weights
+
+    dev = torch.device("cuda:0")
+    c = workloads.config5()
+    w = random_weights().to(dev)
+    ids, cu = c.ids.to(dev), c.cu_seqlens.to(dev)
+    fn = lambda: modernbert_forward(ids, cu, c.max_seqlen, w)
+    for _ in range(max(2, args.warmup // 5)):
+        fn()
+    torch.cuda.synchronize()
+    n = max(3, args.steps // 10)
+    t0 = time.perf_counter()
+    for _ in range(n):
+        fn()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / n
+    T = int(c.lengths.sum())
+    del w
+    return dict(ms_per_forward=ms, tokens_per_s=T / (ms * 1e-3),
+                sequences_per_s=len(c.lengths) / (ms * 1e-3), tokens=T, layers=22,
+                note="wall clock per forward (embeddings to final LayerNorm), GEMMs via torch/hipBLASLt")
+
+
 def cpu_baseline(torch, c2, min_seconds=10.0):
     """The oracle (CPU restatement of the reference's eager path, fp32) on the
     host cores: global + local attention over the config-2 sequences, cycling
@@ -275,6 +304,7 @@ def main():
         extra["rpb_mt5_large_config4"] = rpb_config4(torch, args)
         extra["deberta_v3_large_config3"] = deberta_config3(torch, args)
         extra["epilogues"] = epilogue_bench(torch, args, c2)
+        extra["modernbert_encoder_config5"] = encoder_config5(torch, args)
     line = {
         "metric": "encoder attn TFLOP/s + % bf16 MFMA peak at L=512-768; end-to-end tokens/s",
         "value": head["value"],

@@ -1,0 +1,88 @@
+"""Encoder-level restatements (oracle; test infrastructure only).
+
+modernbert_encoder follows the reference's ModernBERT forward
+(models/modernbert/modernbert_encoder.py):
+  embeddings  tok_embeddings -> LayerNorm (no bias)               :102-128
+  layer i     attn_norm (Identity for layer 0, else LayerNorm)     :289-315
+              Wqkv -> RoPE -> attention -> Wo, residual add         :214-260, :329-339
+              mlp_norm -> Wi -> GELU(input) * gate -> Wo, residual  :135-178, :341-350
+  final       LayerNorm                                             :412-415, :478
+global layers are layer_id % 3 == 0 with RoPE theta 160000 and full
+attention inside each sequence; the others use theta 10000 and |i - j| <= 64
+(:198, :379-390, :539-549); key j is hidden when its token id is 50284
+(:456-460). Everything is computed per sequence in fp32 (the packed dense
+masks of :491-550 are equivalent and infeasible at benchmark sizes).
+
+Pinned by (tests/test_oracle_encoders.py): transformers' ModernBertModel with
+the same weights, one sequence at a time (an implementation independent of
+this restatement and of the reference), on a reduced configuration.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import torch
+
+from .attention import varlen_attention
+from .epilogues import gelu_erf, layernorm
+
+MASK_TOKEN_ID = 50284  # modernbert_encoder.py:456-460
+
+
+@dataclass
+class ModernBertLayerWeights:
+    wqkv: torch.Tensor       # [3 * hidden, hidden] (q, k, v row blocks; heads of 64)
+    wo: torch.Tensor         # [hidden, hidden]
+    wi: torch.Tensor         # [2 * inter, hidden] (input rows, then gate rows)
+    wo_mlp: torch.Tensor     # [hidden, inter]
+    attn_norm: Optional[torch.Tensor]   # [hidden] or None (layer 0: Identity)
+    mlp_norm: torch.Tensor   # [hidden]
+
+
+@dataclass
+class ModernBertWeights:
+    hidden: int
+    heads: int
+    inter: int
+    emb: torch.Tensor        # [vocab, hidden]
+    emb_norm: torch.Tensor   # [hidden]
+    layers: List[ModernBertLayerWeights] = field(default_factory=list)
+    final_norm: Optional[torch.Tensor] = None
+    global_every: int = 3
+    window: int = 64              # local_attention // 2
+    theta_global: float = 160000.0
+    theta_local: float = 10000.0
+    eps: float = 1e-5
+
+
+def modernbert_layer(x: torch.Tensor, w: ModernBertWeights, i: int, cu_seqlens: torch.Tensor,
+                     key_valid: Optional[torch.Tensor], dtype=torch.float32) -> torch.Tensor:
+    """One encoder layer (modernbert_encoder.py:317-352) over a packed stream [T, hidden]."""
+    lw = w.layers[i]
+    T = x.shape[0]
+    d = w.hidden // w.heads
+    h = x if lw.attn_norm is None else layernorm(x, lw.attn_norm, None, w.eps, dtype)
+    qkv = h @ lw.wqkv.to(dtype).t()
+    q, k, v = (t.reshape(T, w.heads, d) for t in qkv.chunk(3, dim=-1))
+    is_global = i % w.global_every == 0
+    att = varlen_attention(q, k, v, cu_seqlens, -1 if is_global else w.window,
+                           w.theta_global if is_global else w.theta_local,
+                           key_valid, 1.0 / math.sqrt(d), dtype)
+    x = x + att.reshape(T, w.hidden) @ lw.wo.to(dtype).t()
+    h = layernorm(x, lw.mlp_norm, None, w.eps, dtype)
+    y = h @ lw.wi.to(dtype).t()
+    inp, gate = y.chunk(2, dim=-1)
+    return x + (gelu_erf(inp) * gate) @ lw.wo_mlp.to(dtype).t()
+
+
+def modernbert_encoder(ids: torch.Tensor, cu_seqlens: torch.Tensor, w: ModernBertWeights,
+                       dtype=torch.float32, num_layers: Optional[int] = None) -> torch.Tensor:
+    """Full forward over packed token ids [T] -> final hidden states [T, hidden]."""
+    key_valid = ids != MASK_TOKEN_ID
+    x = layernorm(w.emb[ids].to(dtype), w.emb_norm, None, w.eps, dtype)
+    n = len(w.layers) if num_layers is None else num_layers
+    for i in range(n):
+        x = modernbert_layer(x, w, i, cu_seqlens, key_valid, dtype)
+    return layernorm(x, w.final_norm, None, w.eps, dtype)

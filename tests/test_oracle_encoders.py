@@ -1,0 +1,77 @@
+"""Pins oracle/encoders.py against an independent implementation:
+transformers' ModernBertModel with the same random weights, run one sequence
+at a time on a reduced configuration (hidden 128 = 2 heads of 64, 4 layers
+with global layers 0 and 3, sliding window +-8 so short sequences exercise
+it). No GPU is used."""
+import pytest
+import torch
+
+from oracle import encoders as oe
+
+
+def _small_weights(seed=7):
+    import encoders.modernbert as em
+    return em.random_weights(num_layers=4, hidden=128, heads=2, inter=192, vocab=500, seed=seed,
+                             std=0.05, dtype=torch.float32)
+
+
+def _hf_model(w, window):
+    from transformers import ModernBertConfig, ModernBertModel
+    cfg = ModernBertConfig(vocab_size=w.emb.shape[0], hidden_size=w.hidden, intermediate_size=w.inter,
+                           num_hidden_layers=len(w.layers), num_attention_heads=w.heads,
+                           local_attention=2 * window, global_attn_every_n_layers=3,
+                           hidden_activation="gelu", norm_eps=w.eps, norm_bias=False,
+                           attention_bias=False, mlp_bias=False, pad_token_id=0)
+    cfg._attn_implementation = "eager"
+    m = ModernBertModel(cfg).eval()
+    sd = {"embeddings.tok_embeddings.weight": w.emb, "embeddings.norm.weight": w.emb_norm,
+          "final_norm.weight": w.final_norm}
+    for i, lw in enumerate(w.layers):
+        p = f"layers.{i}."
+        sd[p + "attn.Wqkv.weight"] = lw.wqkv
+        sd[p + "attn.Wo.weight"] = lw.wo
+        sd[p + "mlp.Wi.weight"] = lw.wi
+        sd[p + "mlp.Wo.weight"] = lw.wo_mlp
+        sd[p + "mlp_norm.weight"] = lw.mlp_norm
+        if lw.attn_norm is not None:
+            sd[p + "attn_norm.weight"] = lw.attn_norm
+    missing, unexpected = m.load_state_dict(sd, strict=False)
+    assert not unexpected, unexpected
+    assert all("rotary" in k or "inv_freq" in k for k in missing), missing
+    return m
+
+
+def test_modernbert_oracle_matches_transformers():
+    w = _small_weights()
+    w.window = 8
+    lens = [40, 23, 17]
+    g = torch.Generator().manual_seed(3)
+    ids = torch.randint(1, 500, (sum(lens),), generator=g)
+    cu = torch.tensor([0, 40, 63, 80], dtype=torch.int32)
+    got = oe.modernbert_encoder(ids, cu, w, dtype=torch.float64)
+    m = _hf_model(w, 8).double()
+    for s in range(len(lens)):
+        a, b = int(cu[s]), int(cu[s + 1])
+        with torch.no_grad():
+            want = m(input_ids=ids[a:b][None]).last_hidden_state[0]
+        # agreement to fp32 rounding of HF's float32 rotary tables; a wrong
+        # window, theta, sign or norm placement differs by O(1e-2) or more
+        torch.testing.assert_close(got[a:b], want, rtol=0, atol=1e-6)
+
+
+def test_modernbert_oracle_mask_token_hides_key():
+    # a token with id 50284 is never seen as a key (modernbert_encoder.py:456-460):
+    # every other row is independent of that token's embedding
+    import encoders.modernbert as em
+    w = em.random_weights(num_layers=3, hidden=128, heads=2, inter=192, vocab=50368, seed=9,
+                          std=0.05, dtype=torch.float32)
+    ids = torch.randint(0, 50000, (30,), generator=torch.Generator().manual_seed(4))
+    ids[11] = oe.MASK_TOKEN_ID
+    cu = torch.tensor([0, 30], dtype=torch.int32)
+    a = oe.modernbert_encoder(ids, cu, w, dtype=torch.float64)
+    w.emb = w.emb.clone()
+    w.emb[oe.MASK_TOKEN_ID] = torch.randn(128, generator=torch.Generator().manual_seed(5))
+    b = oe.modernbert_encoder(ids, cu, w, dtype=torch.float64)
+    others = torch.arange(30) != 11
+    torch.testing.assert_close(a[others], b[others], rtol=0, atol=1e-12)
+    assert (a[11] - b[11]).abs().max() > 1e-3  # the token's own row does change

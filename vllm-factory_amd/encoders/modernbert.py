@@ -1,0 +1,117 @@
+"""ModernBERT encoder forward on the packed (varlen) stream.
+
+Follows models/modernbert/modernbert_encoder.py (embeddings :102-128, layer
+:289-352, model :430-480): tok_embeddings -> LayerNorm; 22 x [attn_norm
+(Identity in layer 0) -> Wqkv -> RoPE attention -> Wo -> + residual ->
+mlp_norm -> Wi -> GELU(input) * gate -> Wo -> + residual]; final LayerNorm.
+Global layers (layer_id % 3 == 0) attend inside each sequence with RoPE theta
+160000, local layers within |i - j| <= 64 with theta 10000; tokens with id
+50284 are hidden as keys (:456-460).
+
+Differences from the reference, all by construction of the packed path:
+sequences are given by cu_seqlens instead of position resets and dense
+[T, T] masks; each residual add is fused into the LayerNorm that follows it
+(vfk_layernorm_fwd with a residual); a query row that sees no key at all
+(every key of its sequence is token 50284) returns zeros where the reference's
+finite mask would average over the stream.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import torch
+import torch.nn.functional as F
+
+from kernels.fused_glu_mlp import fused_gelu_mul_dropout
+from kernels.fused_layernorm import fused_add_layernorm, fused_layernorm
+from kernels.varlen_attention import varlen_rope_attention
+
+MASK_TOKEN_ID = 50284
+
+
+@dataclass
+class ModernBertLayerWeights:
+    wqkv: torch.Tensor       # [3 * hidden, hidden]
+    wo: torch.Tensor         # [hidden, hidden]
+    wi: torch.Tensor         # [2 * inter, hidden] (input rows, then gate rows)
+    wo_mlp: torch.Tensor     # [hidden, inter]
+    attn_norm: Optional[torch.Tensor]   # [hidden]; None in layer 0 (Identity)
+    mlp_norm: torch.Tensor   # [hidden]
+
+
+@dataclass
+class ModernBertWeights:
+    hidden: int
+    heads: int
+    inter: int
+    emb: torch.Tensor        # [vocab, hidden]
+    emb_norm: torch.Tensor
+    layers: List[ModernBertLayerWeights] = field(default_factory=list)
+    final_norm: Optional[torch.Tensor] = None
+    global_every: int = 3
+    window: int = 64
+    theta_global: float = 160000.0
+    theta_local: float = 10000.0
+    eps: float = 1e-5
+
+    def to(self, device=None, dtype=None) -> "ModernBertWeights":
+        def mv(t):
+            return None if t is None else t.to(device=device, dtype=dtype)
+        return ModernBertWeights(
+            self.hidden, self.heads, self.inter, mv(self.emb), mv(self.emb_norm),
+            [ModernBertLayerWeights(mv(l.wqkv), mv(l.wo), mv(l.wi), mv(l.wo_mlp), mv(l.attn_norm),
+                                    mv(l.mlp_norm)) for l in self.layers],
+            mv(self.final_norm), self.global_every, self.window, self.theta_global,
+            self.theta_local, self.eps)
+
+
+def random_weights(num_layers: int = 22, hidden: int = 768, heads: int = 12, inter: int = 1152,
+                   vocab: int = 50368, seed: int = 1005, std: float = 0.02,
+                   dtype=torch.bfloat16) -> ModernBertWeights:
+    """Random-init weights ~ N(0, std) (CPU, seeded), LayerNorm weights 1."""
+    g = torch.Generator().manual_seed(seed)
+
+    def rnd(*shape):
+        return (torch.randn(*shape, generator=g) * std).to(dtype)
+
+    ones = torch.ones(hidden, dtype=dtype)
+    layers = [ModernBertLayerWeights(rnd(3 * hidden, hidden), rnd(hidden, hidden),
+                                     rnd(2 * inter, hidden), rnd(hidden, inter),
+                                     None if i == 0 else ones.clone(), ones.clone())
+              for i in range(num_layers)]
+    return ModernBertWeights(hidden, heads, inter, rnd(vocab, hidden), ones.clone(), layers,
+                             ones.clone())
+
+
+def modernbert_forward(ids: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,
+                       w: ModernBertWeights, num_layers: Optional[int] = None) -> torch.Tensor:
+    """ids [T] (device, int64), cu_seqlens int32 [n + 1] -> last hidden state [T, hidden]."""
+    T = ids.shape[0]
+    d = w.hidden // w.heads
+    key_valid = ids != MASK_TOKEN_ID
+    x = fused_layernorm(w.emb[ids], w.hidden, w.emb_norm, None, w.eps)
+    pending = None  # MLP output not yet added to the residual stream x
+    n = len(w.layers) if num_layers is None else num_layers
+    for i in range(n):
+        lw = w.layers[i]
+        if pending is None:
+            h = x if lw.attn_norm is None else fused_layernorm(x, w.hidden, lw.attn_norm, None, w.eps)
+        else:
+            h, x = fused_add_layernorm(pending, x, lw.attn_norm, None, w.eps)
+        qkv = F.linear(h, lw.wqkv).view(T, 3, w.heads, d)
+        is_global = i % w.global_every == 0
+        att = varlen_rope_attention(qkv[:, 0], qkv[:, 1], qkv[:, 2], cu_seqlens, max_seqlen,
+                                    -1 if is_global else w.window,
+                                    w.theta_global if is_global else w.theta_local,
+                                    1.0 / math.sqrt(d), key_valid)
+        o = F.linear(att.view(T, w.hidden), lw.wo)
+        h, x = fused_add_layernorm(o, x, lw.mlp_norm, None, w.eps)
+        y = F.linear(h, lw.wi)
+        g = fused_gelu_mul_dropout(y[:, :w.inter], y[:, w.inter:], "gelu")
+        pending = F.linear(g, lw.wo_mlp)
+    if pending is None:
+        return fused_layernorm(x, w.hidden, w.final_norm, None, w.eps)
+    out, _ = fused_add_layernorm(pending, x, w.final_norm, None, w.eps)
+    return out

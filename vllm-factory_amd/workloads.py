@@ -188,3 +188,25 @@ def window_pairs(n: int, w: int) -> int:
         return n * n
     # full band: n rows * (2w+1) minus the two triangles cut at the borders
     return n * (2 * w + 1) - w * (w + 1)
+
+
+# ---------------------------------------------------------------------------
+# config 5
+# ---------------------------------------------------------------------------
+@dataclass
+class EncoderCase:
+    ids: torch.Tensor          # [T] int64 token ids, U{0..vocab-1}
+    cu_seqlens: torch.Tensor   # int32 [n + 1]
+    lengths: torch.Tensor
+    max_seqlen: int
+
+
+def config5(num_seqs: int = 256, lo: int = 512, hi: int = 768, vocab: int = 50368) -> EncoderCase:
+    """ModernBERT-base encoder input: packed sequences with lengths U{lo..hi}
+    and token ids uniform over the vocabulary (ids equal to 50284 are the
+    reference's masked keys). Weights: encoders.modernbert.random_weights."""
+    g = gen(5)
+    lengths = _lengths(g, num_seqs, lo, hi)
+    T = int(lengths.sum())
+    ids = torch.randint(0, vocab, (T,), generator=g, dtype=torch.int64)
+    return EncoderCase(ids, cu_from_lengths(lengths), lengths, int(lengths.max()))
