@@ -14,7 +14,7 @@ the memory-bound epilogues in GB/s, the end-to-end tokens/s of the full
 22-layer ModernBERT-base encoder over 256 packed sequences, and the CPU
 oracle timed on the host.
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--only headline]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--only headline|traffic]
 """
 from __future__ import annotations
 
@@ -56,6 +56,45 @@ class KernelTimer:
 
     def reset(self):
         self.ms = {}
+
+
+def traffic_workload(torch):
+    """Workload of the FETCH_SIZE / WRITE_SIZE counter runs (--only traffic):
+    three plain copies of a 512 MiB bf16 tensor (calibration: known bytes,
+    larger than the last-level cache), then the config-2 global and local
+    attention calls three times each."""
+    import workloads
+    from kernels.varlen_attention import varlen_rope_attention
+
+    dev = torch.device("cuda:0")
+    x = torch.empty(256 * 1024 * 1024, dtype=torch.bfloat16, device=dev).normal_()
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    del x, y
+    c = workloads.config2(device=dev)
+    q, k, v = c.qkv[:, 0], c.qkv[:, 1], c.qkv[:, 2]
+    out = torch.empty_like(q)
+    for _ in range(3):
+        varlen_rope_attention(q, k, v, c.cu_seqlens, c.max_seqlen, -1, 160000.0, 0.125, out=out)
+        varlen_rope_attention(q, k, v, c.cu_seqlens, c.max_seqlen, 64, 10000.0, 0.125, out=out)
+    torch.cuda.synchronize()
+    print("traffic workload done", file=sys.stderr)
+
+
+def measured_traffic(name):
+    """HBM bytes per launch recorded by the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    runs summarised in profiles/<name> (line 'traffic_bytes_per_launch = N'),
+    or None when that summary is absent."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
 
 
 def device_ms(torch, fn, n):
@@ -111,9 +150,12 @@ def headline(torch, args):
     l_tf = fl_local / (l_ms * 1e-3) / 1e12
     return dict(
         value=value, ms_per_step=ms_step, tokens=int(sum(lens)),
-        roofline=dict(bound="mfma", kernel="varlen_fwd_kernel (global, RoPE theta 160000)",
+        roofline=dict(bound="mfma",
+                      kernel="global attention call: rope_k_pack_kernel + varlen_fwd_kernel "
+                             "(RoPE theta 160000)",
                       achieved=g_tf, peak=PEAK_BF16_TFLOPS, unit="TFLOP/s", frac=g_tf / PEAK_BF16_TFLOPS,
-                      traffic=None, flops_per_launch=fl_global, avg_launch_ms=g_ms),
+                      traffic=measured_traffic("varlen_global_traffic_config2.md"),
+                      flops_per_launch=fl_global, avg_launch_ms=g_ms),
         kernels=dict(
             global_attn=dict(ms=g_ms, tflops=g_tf, gflop=fl_global / 1e9, frac=g_tf / PEAK_BF16_TFLOPS),
             local_attn=dict(ms=l_ms, tflops=l_tf, gflop=fl_local / 1e9, frac=l_tf / PEAK_BF16_TFLOPS),
@@ -286,7 +328,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="'headline' to skip the extra figures")
+    ap.add_argument("--only", default="", help="'headline' to skip the extra figures; 'traffic' "
+                    "runs only the workload of the HBM-traffic counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path is "
@@ -298,6 +341,9 @@ def main():
     if not torch.cuda.is_available():
         print("no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.only == "traffic":
+        traffic_workload(torch)
+        return
     head, c2 = headline(torch, args)
     extra = {}
     if args.only != "headline":
