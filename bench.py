@@ -288,6 +288,24 @@ def encoder_config5(torch, args):
                 note="wall clock per forward (embeddings to final LayerNorm), GEMMs via torch/hipBLASLt")
 
 
+def mt5_layer_config4(torch, args):
+    """One mT5-large encoder layer (RMSNorm, RPB attention, gated-GELU FFN) at
+    config 4 (B=32, L=768, lengths U{512..768}); tokens/s over valid tokens."""
+    import workloads
+    from encoders.mt5 import mt5_layer_forward
+
+    dev = torch.device("cuda:0")
+    c = workloads.config4(device=dev)
+    ws = (c.wq, c.wk, c.wv, c.wo, c.wi0, c.wi1, c.wff_o, c.ln1, c.ln2, c.table)
+    fn = lambda: mt5_layer_forward(c.hidden, *ws, c.mask)
+    for _ in range(args.warmup):
+        fn()
+    ms = device_ms(torch, fn, args.steps)
+    tv = int(c.lengths.sum())
+    return dict(ms_per_layer=ms, valid_tokens_per_s=tv / (ms * 1e-3), valid_tokens=tv,
+                padded_tokens=int(c.hidden.shape[0] * c.hidden.shape[1]))
+
+
 def cpu_baseline(torch, c2, min_seconds=10.0):
     """The oracle (CPU restatement of the reference's eager path, fp32) on the
     host cores: global + local attention over the config-2 sequences, cycling
@@ -350,6 +368,7 @@ def main():
         extra["rpb_mt5_large_config4"] = rpb_config4(torch, args)
         extra["deberta_v3_large_config3"] = deberta_config3(torch, args)
         extra["epilogues"] = epilogue_bench(torch, args, c2)
+        extra["mt5_large_layer_config4"] = mt5_layer_config4(torch, args)
         extra["modernbert_encoder_config5"] = encoder_config5(torch, args)
     line = {
         "metric": "encoder attn TFLOP/s + % bf16 MFMA peak at L=512-768; end-to-end tokens/s",

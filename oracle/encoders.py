@@ -13,9 +13,16 @@ attention inside each sequence; the others use theta 10000 and |i - j| <= 64
 (:456-460). Everything is computed per sequence in fp32 (the packed dense
 masks of :491-550 are equivalent and infeasible at benchmark sizes).
 
-Pinned by (tests/test_oracle_encoders.py): transformers' ModernBertModel with
-the same weights, one sequence at a time (an implementation independent of
-this restatement and of the reference), on a reduced configuration.
+mt5_layer follows the reference's T5EncoderLayer (models/mt5/mt5_encoder.py
+:476-491): h = x + SelfAttention(RMSNorm1(x)); h + FF(RMSNorm2(h)), with the
+relative-position-bias attention of :234-320 (bidirectional buckets, bias
+table [buckets, heads] shared from layer 0, no 1/sqrt(d) scaling, additive
+key mask (1 - m) * finfo.min, :571-576) and the gated FFN of :411-447
+(gelu_new = tanh GELU on wi_0, times wi_1, then wo).
+
+Pinned by (tests/test_oracle_encoders.py): transformers' ModernBertModel and
+MT5EncoderModel with the same weights (implementations independent of this
+restatement and of the reference), on reduced configurations.
 """
 from __future__ import annotations
 
@@ -25,8 +32,8 @@ from typing import List, Optional
 
 import torch
 
-from .attention import varlen_attention
-from .epilogues import gelu_erf, layernorm
+from .attention import rpb_attention, varlen_attention
+from .epilogues import gelu_erf, gelu_tanh, layernorm, rmsnorm
 
 MASK_TOKEN_ID = 50284  # modernbert_encoder.py:456-460
 
@@ -86,3 +93,21 @@ def modernbert_encoder(ids: torch.Tensor, cu_seqlens: torch.Tensor, w: ModernBer
     for i in range(n):
         x = modernbert_layer(x, w, i, cu_seqlens, key_valid, dtype)
     return layernorm(x, w.final_norm, None, w.eps, dtype)
+
+
+def mt5_layer(x: torch.Tensor, wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2, table,
+              mask: Optional[torch.Tensor], num_buckets: int = 32, max_distance: int = 128,
+              eps: float = 1e-6, dtype=torch.float32) -> torch.Tensor:
+    """One mT5 encoder layer on x [B, L, d_model]; weights as x @ W ([in, out]);
+    table [buckets, heads]; mask additive [B, 1, 1, L] or None."""
+    x = x.to(dtype)
+    B, L, D = x.shape
+    H = table.shape[1]
+    d = D // H
+    h = rmsnorm(x, ln1, eps, dtype)
+    q, k, v = ((h @ w.to(dtype)).view(B, L, H, d).transpose(1, 2) for w in (wq, wk, wv))
+    att = rpb_attention(q, k, v, table.to(dtype), num_buckets, max_distance, False,
+                        None if mask is None else mask.to(dtype), 1.0, dtype=dtype)
+    x = x + att.transpose(1, 2).reshape(B, L, D) @ wo.to(dtype)
+    h = rmsnorm(x, ln2, eps, dtype)
+    return x + (gelu_tanh(h @ wi0.to(dtype)) * (h @ wi1.to(dtype))) @ wff_o.to(dtype)

@@ -75,3 +75,41 @@ def test_modernbert_oracle_mask_token_hides_key():
     others = torch.arange(30) != 11
     torch.testing.assert_close(a[others], b[others], rtol=0, atol=1e-12)
     assert (a[11] - b[11]).abs().max() > 1e-3  # the token's own row does change
+
+
+def test_mt5_layer_oracle_matches_transformers():
+    # one MT5EncoderModel block (layer 0 owns the relative-attention bias) on
+    # inputs_embeds, then its final RMSNorm; weights shared with the oracle
+    from transformers import MT5Config, MT5EncoderModel
+    g = torch.Generator().manual_seed(11)
+    B, L, D, H, F = 2, 40, 128, 2, 192
+    cfg = MT5Config(vocab_size=64, d_model=D, d_kv=64, d_ff=F, num_layers=1, num_heads=H,
+                    relative_attention_num_buckets=32, relative_attention_max_distance=128,
+                    feed_forward_proj="gated-gelu", layer_norm_epsilon=1e-6, dropout_rate=0.0)
+    m = MT5EncoderModel(cfg).eval().double()
+    r = lambda *s: torch.randn(*s, generator=g, dtype=torch.float64)
+    wq, wk, wv, wo = (r(D, D) * 0.08 for _ in range(4))
+    wi0, wi1, wff = r(D, F) * 0.08, r(D, F) * 0.08, r(F, D) * 0.08
+    ln1, ln2, lnf = 1 + 0.1 * r(D), 1 + 0.1 * r(D), 1 + 0.1 * r(D)
+    table = r(32, H) * 0.5
+    blk = m.encoder.block[0]
+    sa, ff = blk.layer[0], blk.layer[1]
+    with torch.no_grad():
+        sa.SelfAttention.q.weight.copy_(wq.t()); sa.SelfAttention.k.weight.copy_(wk.t())
+        sa.SelfAttention.v.weight.copy_(wv.t()); sa.SelfAttention.o.weight.copy_(wo.t())
+        sa.SelfAttention.relative_attention_bias.weight.copy_(table)
+        sa.layer_norm.weight.copy_(ln1)
+        ff.DenseReluDense.wi_0.weight.copy_(wi0.t()); ff.DenseReluDense.wi_1.weight.copy_(wi1.t())
+        ff.DenseReluDense.wo.weight.copy_(wff.t()); ff.layer_norm.weight.copy_(ln2)
+        m.encoder.final_layer_norm.weight.copy_(lnf)
+    x = r(B, L, D)
+    keep = torch.ones(B, L, dtype=torch.float64)
+    keep[1, 29:] = 0
+    with torch.no_grad():
+        want = m(inputs_embeds=x, attention_mask=keep).last_hidden_state
+    mask = ((1.0 - keep) * torch.finfo(torch.float64).min)[:, None, None, :]
+    got = oe.mt5_layer(x, wq, wk, wv, wo, wi0, wi1, wff, ln1, ln2, table, mask, dtype=torch.float64)
+    got = oe.rmsnorm(got, lnf, 1e-6, torch.float64)
+    # transformers' T5LayerNorm takes the variance in fp32 even for fp64
+    # models (~1e-7 relative); a wrong bucket, mask, norm or gate is >= 1e-3
+    torch.testing.assert_close(got, want, rtol=0, atol=1e-5)

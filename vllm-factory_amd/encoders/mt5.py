@@ -1,0 +1,36 @@
+"""mT5 encoder layer forward (config 4 shapes: d_model 1024, 16 heads of 64,
+gated-GELU d_ff 2816) on the hot-path kernels.
+
+Follows models/mt5/mt5_encoder.py:476-491 (T5EncoderLayer):
+    h = x + o_proj(RPB-attention(q, k, v of RMSNorm1(x)))
+    out = h + wo(gelu_new(wi_0(RMSNorm2(h))) * wi_1(RMSNorm2(h)))
+with the attention call of :269-279 (flash_attention_rpb_final, shared
+[buckets, heads] table, scale 1.0, additive [B, 1, 1, L] key mask). The first
+residual add is fused into the second RMSNorm and the second into the wo GEMM
+(beta = 1).
+"""
+from __future__ import annotations
+
+import torch
+
+from kernels.ff_fused import fused_gelu_mul_dropout
+from kernels.flash_attention_rpb import flash_attention_rpb_final
+from kernels.rms_norm import fused_add_rms_norm, rms_norm
+
+
+def mt5_layer_forward(x: torch.Tensor, wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2, table,
+                      mask, num_buckets: int = 32, max_distance: int = 128,
+                      eps: float = 1e-6) -> torch.Tensor:
+    """x [B, L, d_model] (bf16/fp16 on the GPU); weights as x @ W ([in, out])."""
+    B, L, D = x.shape
+    H = table.shape[1]
+    d = D // H
+    h = rms_norm(x, ln1, eps)
+    # [B, L, H, d] projections viewed as [B, H, L, d] (strided, no copies)
+    q, k, v = ((h @ w).view(B, L, H, d).transpose(1, 2) for w in (wq, wk, wv))
+    att = flash_attention_rpb_final(q, k, v, table, num_buckets, max_distance, False,
+                                    padding_mask=mask, softmax_scale=1.0)
+    o = att.transpose(1, 2).reshape(B, L, D) @ wo
+    h2, x1 = fused_add_rms_norm(o, x, ln2, eps)
+    g = fused_gelu_mul_dropout(h2 @ wi0, h2 @ wi1, "gelu_new")
+    return torch.addmm(x1.reshape(-1, D), g.reshape(-1, g.shape[-1]), wff_o).view(B, L, D)

@@ -26,3 +26,9 @@ class RMSNorm(torch.nn.Module):
 
 def rms_norm(x: torch.Tensor, weight: Optional[torch.Tensor], eps: float = 1e-6) -> torch.Tensor:
     return _norm(x, x.shape[-1], weight, None, eps, rms=True)
+
+
+def fused_add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: Optional[torch.Tensor],
+                       eps: float = 1e-6):
+    """(RMSNorm(x + residual), x + residual) in one pass."""
+    return _norm(x, x.shape[-1], weight, None, eps, residual=residual, rms=True, want_sum=True)
