@@ -306,6 +306,27 @@ def mt5_layer_config4(torch, args):
                 padded_tokens=int(c.hidden.shape[0] * c.hidden.shape[1]))
 
 
+def deberta_layer_config3(torch, args):
+    """One DeBERTa-v3-large encoder layer (projections, disentangled attention,
+    LayerNorms, GELU FFN) at config 3 (B=32, L=512, lengths U{256..512});
+    tokens/s over valid tokens."""
+    import workloads
+    from encoders.deberta import deberta_layer_forward, deberta_rel_embeddings, random_weights
+
+    dev = torch.device("cuda:0")
+    hidden, lens = workloads.config3_hidden()
+    x, sl = hidden.to(dev, torch.bfloat16), lens.to(dev)
+    w = random_weights(num_layers=1).to(dev)
+    rel = deberta_rel_embeddings(w)
+    fn = lambda: deberta_layer_forward(x, sl, rel, w.layers[0], w)
+    for _ in range(args.warmup):
+        fn()
+    ms = device_ms(torch, fn, args.steps)
+    tv = int(lens.sum())
+    return dict(ms_per_layer=ms, valid_tokens_per_s=tv / (ms * 1e-3), valid_tokens=tv,
+                padded_tokens=int(x.shape[0] * x.shape[1]))
+
+
 def cpu_baseline(torch, c2, min_seconds=10.0):
     """The oracle (CPU restatement of the reference's eager path, fp32) on the
     host cores: global + local attention over the config-2 sequences, cycling
@@ -369,6 +390,7 @@ def main():
         extra["deberta_v3_large_config3"] = deberta_config3(torch, args)
         extra["epilogues"] = epilogue_bench(torch, args, c2)
         extra["mt5_large_layer_config4"] = mt5_layer_config4(torch, args)
+        extra["deberta_v3_large_layer_config3"] = deberta_layer_config3(torch, args)
         extra["modernbert_encoder_config5"] = encoder_config5(torch, args)
     line = {
         "metric": "encoder attn TFLOP/s + % bf16 MFMA peak at L=512-768; end-to-end tokens/s",

@@ -197,6 +197,11 @@ int vfk_rmsnorm_fwd(const vfk_tensor* x, const vfk_tensor* residual,
 int vfk_glu_fwd(int32_t act, const vfk_tensor* a, const vfk_tensor* b,
                 vfk_tensor* out, void* stream);
 
+/* Activation out = act(x) over [rows, n] (row strides). Replaces the
+ * intermediate activation of models/deberta_v2/deberta_v2_encoder.py:535-550
+ * (DebertaV2Intermediate, ACT2FN[hidden_act]) in inference. */
+int vfk_act_fwd(int32_t act, const vfk_tensor* x, vfk_tensor* out, void* stream);
+
 /* out = a + b, elementwise over [rows, n] (row strides).
  * Replaces kernels/fused_dropout_residual.py:10-104 in inference mode. */
 int vfk_residual_add(const vfk_tensor* a, const vfk_tensor* b,

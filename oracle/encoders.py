@@ -20,9 +20,19 @@ table [buckets, heads] shared from layer 0, no 1/sqrt(d) scaling, additive
 key mask (1 - m) * finfo.min, :571-576) and the gated FFN of :411-447
 (gelu_new = tanh GELU on wi_0, times wi_1, then wo).
 
-Pinned by (tests/test_oracle_encoders.py): transformers' ModernBertModel and
-MT5EncoderModel with the same weights (implementations independent of this
-restatement and of the reference), on reduced configurations.
+deberta_encoder follows the reference's DebertaV2Encoder (models/deberta_v2/
+deberta_v2_encoder.py:734-819): LayerNorm of the relative table (:770-774),
+then per layer (:627-645) query/key/value_proj with bias, the flash
+disentangled attention of :246-330 (share_att_key: pos_key = q key_proj(rel)^T,
+pos_query = k query_proj(rel)^T, sm_scale 1/sqrt(3 d), log buckets, keys at or
+beyond the sequence length hidden, those query rows zero), dense ->
+LayerNorm(. + x) (:494-510), GELU(erf) intermediate (:535-550), dense ->
+LayerNorm(. + attention_output) (:553-568).
+
+Pinned by (tests/test_oracle_encoders.py): transformers' ModernBertModel,
+MT5EncoderModel and DebertaV2Encoder with the same weights (implementations
+independent of this restatement and of the reference), on reduced
+configurations.
 """
 from __future__ import annotations
 
@@ -32,7 +42,8 @@ from typing import List, Optional
 
 import torch
 
-from .attention import rpb_attention, varlen_attention
+from .attention import (deberta_flash_attention, deberta_position_projections, rpb_attention,
+                        varlen_attention)
 from .epilogues import gelu_erf, gelu_tanh, layernorm, rmsnorm
 
 MASK_TOKEN_ID = 50284  # modernbert_encoder.py:456-460
@@ -111,3 +122,47 @@ def mt5_layer(x: torch.Tensor, wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2, table,
     x = x + att.transpose(1, 2).reshape(B, L, D) @ wo.to(dtype)
     h = rmsnorm(x, ln2, eps, dtype)
     return x + (gelu_tanh(h @ wi0.to(dtype)) * (h @ wi1.to(dtype))) @ wff_o.to(dtype)
+
+
+def deberta_layer(x: torch.Tensor, seq_lengths: torch.Tensor, rel: torch.Tensor, lw, heads: int,
+                  position_buckets: int = 256, max_relative_positions: int = 512,
+                  eps: float = 1e-7, dtype=torch.float32) -> torch.Tensor:
+    """One DebertaV2Layer on x [B, L, hidden]; rel = LayerNorm(rel_embeddings);
+    lw has wqkv/bqkv (query, key, value rows), wo/bo, ln1_w/ln1_b, wi/bi,
+    wo2/bo2, ln2_w/ln2_b in nn.Linear layout."""
+    x = x.to(dtype)
+    B, L, D = x.shape
+    d = D // heads
+
+    def lin(t, W, b):
+        return t @ W.to(dtype).t() + b.to(dtype)
+
+    def split(t):  # [..., n, D] -> [..., H, n, d]
+        return t.reshape(*t.shape[:-1], heads, d).transpose(-2, -3)
+
+    wq, wk, wv = lw.wqkv.chunk(3, dim=0)
+    bq, bk, bv = lw.bqkv.chunk(3, dim=0)
+    q, k, v = split(lin(x, wq, bq)), split(lin(x, wk, bk)), split(lin(x, wv, bv))
+    span = position_buckets if position_buckets > 0 else max_relative_positions
+    r = rel[:2 * span].to(dtype)
+    pk, pq = deberta_position_projections(q, k, split(lin(r, wk, bk)), split(lin(r, wq, bq)), dtype)
+    ctx = deberta_flash_attention(q, k, v, seq_lengths, pk, pq, 1.0 / math.sqrt(3 * d),
+                                  position_buckets if position_buckets > 0 else span,
+                                  max_relative_positions, position_buckets > 0, dtype=dtype)
+    ctx = ctx.transpose(1, 2).reshape(B, L, D)
+    h = layernorm(lin(ctx, lw.wo, lw.bo) + x, lw.ln1_w, lw.ln1_b, eps, dtype)
+    inter = gelu_erf(lin(h, lw.wi, lw.bi))
+    return layernorm(lin(inter, lw.wo2, lw.bo2) + h, lw.ln2_w, lw.ln2_b, eps, dtype)
+
+
+def deberta_encoder(x: torch.Tensor, seq_lengths: torch.Tensor, w, dtype=torch.float32,
+                    num_layers: Optional[int] = None) -> torch.Tensor:
+    """Encoder stack on embedding output x [B, L, hidden]; w has hidden, heads,
+    rel_emb, rel_ln_w, rel_ln_b, layers, position_buckets,
+    max_relative_positions, eps."""
+    rel = layernorm(w.rel_emb.to(dtype), w.rel_ln_w, w.rel_ln_b, w.eps, dtype)
+    n = len(w.layers) if num_layers is None else num_layers
+    for i in range(n):
+        x = deberta_layer(x, seq_lengths, rel, w.layers[i], w.heads, w.position_buckets,
+                          w.max_relative_positions, w.eps, dtype)
+    return x

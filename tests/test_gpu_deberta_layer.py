@@ -1,0 +1,49 @@
+"""DeBERTa-v3-large encoder layers (config 3 shapes: hidden 1024, 16 heads,
+intermediate 4096, 256 log buckets, max_relative_positions 512) on the GPU
+against the fp32 oracle restatement, on config-3 batch rows (L = 512,
+right-padded).
+
+Tolerance: each layer ends in a LayerNorm (outputs O(1), up to ~5); the GPU
+path rounds every intermediate to bf16 (relative 2^-8), so max-abs 6e-2 per
+layer stack and cosine 0.9999, on valid rows. Padded rows are checked to be
+finite (their values are defined by the reference's zeroed attention rows)."""
+import pytest
+import torch
+
+import workloads
+from _tol import cosine
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("batch,layers", [(3, 1), (2, 2)])
+def test_deberta_layers_match_oracle(batch, layers):
+    from encoders.deberta import deberta_forward, random_weights
+    from oracle import encoders as oe
+    hidden, lens = workloads.config3_hidden(batch)
+    w = random_weights(num_layers=layers, dtype=torch.bfloat16)
+    dev = torch.device("cuda:0")
+    got = deberta_forward(hidden.to(dev, torch.bfloat16), lens.to(dev), w.to(dev)).float().cpu()
+    want = oe.deberta_encoder(hidden.to(torch.bfloat16).float(), lens, w)
+    assert torch.isfinite(got).all()
+    for b in range(batch):
+        n = int(lens[b])
+        err = (got[b, :n] - want[b, :n]).abs().max().item()
+        cs = cosine(got[b, :n], want[b, :n])
+        print(f"layers {layers} row {b} (len {n}): max-abs {err:.3e} cosine {cs:.6f}")
+        assert err <= 6e-2 and cs >= 0.9999, (b, err, cs)
+
+
+def test_activation_gelu_matches_oracle():
+    """vfk_act_fwd on a strided [rows, n] view (DeBERTa's intermediate GELU)."""
+    from kernels.activation import activation
+    from oracle.epilogues import gelu_erf, gelu_tanh
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randn(301, 4100, generator=g) * 3).to(torch.bfloat16)
+    dev = torch.device("cuda:0")
+    xd = x.to(dev)[:, 2:4098]
+    for name, ref in (("gelu", gelu_erf), ("gelu_new", gelu_tanh)):
+        got = activation(xd, name).float().cpu()
+        want = ref(x[:, 2:4098].float())
+        # one bf16 rounding of the result (relative 2^-8 of |y| <= ~10)
+        assert (got - want).abs().max().item() <= 2 ** -8 * want.abs().max().item(), name

@@ -113,3 +113,77 @@ def test_mt5_layer_oracle_matches_transformers():
     # transformers' T5LayerNorm takes the variance in fp32 even for fp64
     # models (~1e-7 relative); a wrong bucket, mask, norm or gate is >= 1e-3
     torch.testing.assert_close(got, want, rtol=0, atol=1e-5)
+
+
+def _deberta_small(seed=11):
+    import encoders.deberta as ed
+    return ed.random_weights(num_layers=3, hidden=128, heads=2, inter=256, position_buckets=16,
+                             seed=seed, std=0.05, dtype=torch.float64)
+
+
+def _hf_deberta(w):
+    from transformers import DebertaV2Config
+    from transformers.models.deberta_v2.modeling_deberta_v2 import DebertaV2Encoder
+    cfg = DebertaV2Config(hidden_size=w.hidden, num_attention_heads=w.heads,
+                          intermediate_size=w.inter, num_hidden_layers=len(w.layers),
+                          relative_attention=True, position_buckets=w.position_buckets,
+                          max_relative_positions=w.max_relative_positions,
+                          pos_att_type=["p2c", "c2p"], share_att_key=True,
+                          norm_rel_ebd="layer_norm", layer_norm_eps=w.eps, hidden_act="gelu",
+                          hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0)
+    m = DebertaV2Encoder(cfg).double().eval()
+    sd = {"rel_embeddings.weight": w.rel_emb, "LayerNorm.weight": w.rel_ln_w,
+          "LayerNorm.bias": w.rel_ln_b}
+    for i, lw in enumerate(w.layers):
+        p = f"layer.{i}."
+        for name, wt, b in zip(("query_proj", "key_proj", "value_proj"), lw.wqkv.chunk(3),
+                               lw.bqkv.chunk(3)):
+            sd[p + f"attention.self.{name}.weight"] = wt
+            sd[p + f"attention.self.{name}.bias"] = b
+        sd.update({p + "attention.output.dense.weight": lw.wo, p + "attention.output.dense.bias": lw.bo,
+                   p + "attention.output.LayerNorm.weight": lw.ln1_w,
+                   p + "attention.output.LayerNorm.bias": lw.ln1_b,
+                   p + "intermediate.dense.weight": lw.wi, p + "intermediate.dense.bias": lw.bi,
+                   p + "output.dense.weight": lw.wo2, p + "output.dense.bias": lw.bo2,
+                   p + "output.LayerNorm.weight": lw.ln2_w, p + "output.LayerNorm.bias": lw.ln2_b})
+    m.load_state_dict(sd, strict=True)
+    return m
+
+
+def test_deberta_oracle_matches_transformers():
+    """3 layers, 16 position buckets, max_relative_positions 64, L = 80 > 64 so
+    both the log buckets and the clamp at +-2S are exercised; padded rows of
+    the batch are ignored (the reference's kernel zeroes them, transformers
+    does not)."""
+    w = _deberta_small()
+    w.max_relative_positions = 64
+    lens = torch.tensor([80, 50, 33], dtype=torch.int32)
+    B, L = 3, 80
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(B, L, w.hidden, generator=g, dtype=torch.float64)
+    got = oe.deberta_encoder(x, lens, w, dtype=torch.float64)
+    m = _hf_deberta(w)
+    mask = (torch.arange(L)[None, :] < lens[:, None].long()).long()
+    with torch.no_grad():
+        want = m(x, mask, output_hidden_states=False).last_hidden_state
+    for b in range(B):
+        n = int(lens[b])
+        # float64 throughout except transformers' scale sqrt(d * 3), taken in
+        # float32 (relative error ~3e-8); a missing c2p/p2c term, a wrong
+        # bucket or clamp differs by O(1e-2)
+        torch.testing.assert_close(got[b, :n], want[b, :n], rtol=0, atol=1e-8)
+
+
+def test_deberta_oracle_padding_invariance():
+    """Valid rows do not depend on what the padded rows hold."""
+    w = _deberta_small(seed=12)
+    lens = torch.tensor([40, 21], dtype=torch.int32)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 48, w.hidden, generator=g, dtype=torch.float64)
+    y = x.clone()
+    y[0, 40:] = 7.0
+    y[1, 21:] = -3.0
+    a = oe.deberta_encoder(x, lens, w, dtype=torch.float64)
+    b = oe.deberta_encoder(y, lens, w, dtype=torch.float64)
+    torch.testing.assert_close(a[0, :40], b[0, :40], rtol=0, atol=1e-12)
+    torch.testing.assert_close(a[1, :21], b[1, :21], rtol=0, atol=1e-12)

@@ -439,17 +439,24 @@ struct BinArgs {
 };
 
 #define VFK_OP_ADD 100
+#define VFK_OP_UNARY 200  // VFK_OP_UNARY + act: act(a), b unused
+
+template <int ACT>
+__device__ inline float act_f(float a) {
+  if (ACT == VFK_ACT_GELU_ERF) return 0.5f * a * (1.0f + erff(a * 0.70710678118654752f));
+  if (ACT == VFK_ACT_GELU_TANH) {
+    const float inner = 0.7978845608028654f * (a + 0.044715f * a * a * a);
+    return 0.5f * a * (1.0f + tanhf(inner));
+  }
+  if (ACT == VFK_ACT_SILU) return a / (1.0f + expf(-a));
+  return fmaxf(a, 0.f);  // VFK_ACT_RELU
+}
 
 template <int OP>
 __device__ inline float apply_op(float a, float b) {
-  if (OP == VFK_ACT_GELU_ERF) return 0.5f * a * (1.0f + erff(a * 0.70710678118654752f)) * b;
-  if (OP == VFK_ACT_GELU_TANH) {
-    const float inner = 0.7978845608028654f * (a + 0.044715f * a * a * a);
-    return 0.5f * a * (1.0f + tanhf(inner)) * b;
-  }
-  if (OP == VFK_ACT_SILU) return a / (1.0f + expf(-a)) * b;
-  if (OP == VFK_ACT_RELU) return fmaxf(a, 0.f) * b;
-  return a + b;  // VFK_OP_ADD
+  if (OP >= VFK_OP_UNARY) return act_f<OP - VFK_OP_UNARY>(a);
+  if (OP == VFK_OP_ADD) return a + b;
+  return act_f<OP>(a) * b;
 }
 
 template <int DT, int OP>
@@ -464,7 +471,7 @@ __global__ __launch_bounds__(256) void binary_vec_kernel(BinArgs p) {
     const int64_t col = (c - r * cpr) * VEC;
     float x[VEC], y[VEC];
     L::load(p.a, r * p.a_rs + col, x);
-    L::load(p.b, r * p.b_rs + col, y);
+    if (OP < VFK_OP_UNARY) L::load(p.b, r * p.b_rs + col, y);
 #pragma unroll
     for (int i = 0; i < VEC; ++i) x[i] = apply_op<OP>(x[i], y[i]);
     L::store(p.y, r * p.y_rs + col, x);
@@ -479,8 +486,8 @@ __global__ __launch_bounds__(256) void binary_scalar_kernel(BinArgs p) {
        c += (int64_t)gridDim.x * 256) {
     const int64_t r = c / p.n;
     const int64_t col = c - r * p.n;
-    L::st1(p.y, r * p.y_rs + col,
-           apply_op<OP>(L::ld1(p.a, r * p.a_rs + col), L::ld1(p.b, r * p.b_rs + col)));
+    const float bv = OP < VFK_OP_UNARY ? L::ld1(p.b, r * p.b_rs + col) : 0.f;
+    L::st1(p.y, r * p.y_rs + col, apply_op<OP>(L::ld1(p.a, r * p.a_rs + col), bv));
   }
 }
 
@@ -536,6 +543,14 @@ static int binary_entry(int op, const vfk_tensor* a, const vfk_tensor* b,
     case VFK_ACT_SILU: dispatch_binary<VFK_ACT_SILU>(a->dtype, p, vec_ok, st); break;
     case VFK_ACT_RELU: dispatch_binary<VFK_ACT_RELU>(a->dtype, p, vec_ok, st); break;
     case VFK_OP_ADD: dispatch_binary<VFK_OP_ADD>(a->dtype, p, vec_ok, st); break;
+    case VFK_OP_UNARY + VFK_ACT_GELU_ERF:
+      dispatch_binary<VFK_OP_UNARY + VFK_ACT_GELU_ERF>(a->dtype, p, vec_ok, st); break;
+    case VFK_OP_UNARY + VFK_ACT_GELU_TANH:
+      dispatch_binary<VFK_OP_UNARY + VFK_ACT_GELU_TANH>(a->dtype, p, vec_ok, st); break;
+    case VFK_OP_UNARY + VFK_ACT_SILU:
+      dispatch_binary<VFK_OP_UNARY + VFK_ACT_SILU>(a->dtype, p, vec_ok, st); break;
+    case VFK_OP_UNARY + VFK_ACT_RELU:
+      dispatch_binary<VFK_OP_UNARY + VFK_ACT_RELU>(a->dtype, p, vec_ok, st); break;
     default: return set_error(VFK_ERR_INVALID, "%s: unknown activation %d", name, op);
   }
   return launch_status(name);
@@ -636,6 +651,13 @@ extern "C" int vfk_glu_fwd(int32_t act, const vfk_tensor* a,
   if (act < VFK_ACT_GELU_ERF || act > VFK_ACT_RELU)
     return set_error(VFK_ERR_INVALID, "vfk_glu_fwd: unknown activation %d", act);
   return binary_entry(act, a, b, out, stream, "vfk_glu_fwd");
+}
+
+extern "C" int vfk_act_fwd(int32_t act, const vfk_tensor* x, vfk_tensor* out, void* stream) {
+  if (act < VFK_ACT_GELU_ERF || act > VFK_ACT_RELU)
+    return set_error(VFK_ERR_INVALID, "vfk_act_fwd: unknown activation %d", act);
+  // b is not read for unary ops; x stands in for its shape checks
+  return binary_entry(VFK_OP_UNARY + act, x, x, out, stream, "vfk_act_fwd");
 }
 
 extern "C" int vfk_residual_add(const vfk_tensor* a, const vfk_tensor* b,

@@ -1,0 +1,138 @@
+"""DeBERTa-v3 encoder forward (padded batch [B, L, hidden]) on the hot-path kernels.
+
+Follows models/deberta_v2/deberta_v2_encoder.py: the encoder (:734-819)
+LayerNorms the relative-position table once (get_rel_embedding, :770-774)
+and runs each DebertaV2Layer (:627-645):
+    attention   query/key/value_proj (bias) -> flash disentangled attention
+                (:246-330: share_att_key, c2p|p2c, sm_scale 1/sqrt(3 d), log
+                buckets) -> dense -> LayerNorm(. + x)            (:494-510)
+    intermediate dense -> GELU (erf)                               (:535-550)
+    output      dense -> LayerNorm(. + attention_output)           (:553-568)
+
+Differences from the reference, by construction: the three projections are
+one GEMM with concatenated weights; pos_key / pos_query are not materialised
+as [B, H, L, 2S] tensors: the attention kernel computes q.key_rel and
+k.query_rel per tile from the per-head projections of the relative table
+(one [2S, hidden] x [hidden, 2 hidden] GEMM per layer); the attention writes
+its [B, L, H, d] context in place, so no permute copy precedes the dense
+projection; the residual add is folded into each LayerNorm pass. Query rows
+at or beyond a sequence's length attend nowhere and hold zeros after the
+attention, as the reference's kernel writes them.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import torch
+import torch.nn.functional as F
+
+from kernels.activation import activation
+from kernels.flash_deberta_attention import flash_deberta_attention_fused
+from kernels.fused_layernorm import fused_add_layernorm, fused_layernorm
+
+
+@dataclass
+class DebertaLayerWeights:
+    wqkv: torch.Tensor   # [3 * hidden, hidden]: query_proj, key_proj, value_proj rows
+    bqkv: torch.Tensor   # [3 * hidden]
+    wo: torch.Tensor     # attention.output.dense [hidden, hidden]
+    bo: torch.Tensor
+    ln1_w: torch.Tensor  # attention.output.LayerNorm
+    ln1_b: torch.Tensor
+    wi: torch.Tensor     # intermediate.dense [inter, hidden]
+    bi: torch.Tensor
+    wo2: torch.Tensor    # output.dense [hidden, inter]
+    bo2: torch.Tensor
+    ln2_w: torch.Tensor  # output.LayerNorm
+    ln2_b: torch.Tensor
+
+
+@dataclass
+class DebertaWeights:
+    hidden: int
+    heads: int
+    inter: int
+    rel_emb: torch.Tensor     # rel_embeddings.weight [2 * att_span, hidden]
+    rel_ln_w: torch.Tensor    # encoder.LayerNorm (norm_rel_ebd = layer_norm)
+    rel_ln_b: torch.Tensor
+    layers: List[DebertaLayerWeights] = field(default_factory=list)
+    position_buckets: int = 256
+    max_relative_positions: int = 512
+    eps: float = 1e-7
+
+    def to(self, device=None, dtype=None) -> "DebertaWeights":
+        def mv(t):
+            return t.to(device=device, dtype=dtype)
+        return DebertaWeights(
+            self.hidden, self.heads, self.inter, mv(self.rel_emb), mv(self.rel_ln_w),
+            mv(self.rel_ln_b),
+            [DebertaLayerWeights(*(mv(getattr(l, f)) for f in DebertaLayerWeights.__dataclass_fields__))
+             for l in self.layers],
+            self.position_buckets, self.max_relative_positions, self.eps)
+
+
+def random_weights(num_layers: int = 24, hidden: int = 1024, heads: int = 16, inter: int = 4096,
+                   position_buckets: int = 256, seed: int = 1003, std: float = 0.02,
+                   dtype=torch.bfloat16) -> DebertaWeights:
+    """DeBERTa-v3-large shapes, random-init ~ N(0, std) (CPU, seeded);
+    LayerNorm weights 1 + N(0, std), biases N(0, std)."""
+    g = torch.Generator().manual_seed(seed)
+
+    def rnd(*shape):
+        return (torch.randn(*shape, generator=g) * std).to(dtype)
+
+    def ln():
+        return (1.0 + torch.randn(hidden, generator=g) * std).to(dtype), rnd(hidden)
+
+    layers = []
+    for _ in range(num_layers):
+        wqkv, bqkv = rnd(3 * hidden, hidden), rnd(3 * hidden)
+        wo, bo = rnd(hidden, hidden), rnd(hidden)
+        ln1 = ln()
+        wi, bi = rnd(inter, hidden), rnd(inter)
+        wo2, bo2 = rnd(hidden, inter), rnd(hidden)
+        layers.append(DebertaLayerWeights(wqkv, bqkv, wo, bo, *ln1, wi, bi, wo2, bo2, *ln()))
+    rel = rnd(2 * position_buckets, hidden)
+    return DebertaWeights(hidden, heads, inter, rel, *ln(), layers, position_buckets)
+
+
+def deberta_rel_embeddings(w: DebertaWeights) -> torch.Tensor:
+    """LayerNorm(rel_embeddings.weight) (deberta_v2_encoder.py:770-774)."""
+    return fused_layernorm(w.rel_emb, w.hidden, w.rel_ln_w, w.rel_ln_b, w.eps)
+
+
+def deberta_layer_forward(x: torch.Tensor, seq_lengths: torch.Tensor, rel: torch.Tensor,
+                          lw: DebertaLayerWeights, w: DebertaWeights) -> torch.Tensor:
+    """One DebertaV2Layer on x [B, L, hidden]; seq_lengths int32 [B] on the
+    device; rel = deberta_rel_embeddings(w)."""
+    B, L, D = x.shape
+    H = w.heads
+    d = D // H
+    span = w.position_buckets if w.position_buckets > 0 else w.max_relative_positions
+    qkv = F.linear(x, lw.wqkv, lw.bqkv).view(B, L, 3, H, d)
+    q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+    # query_proj / key_proj of the relative table in one GEMM: [2S, 2, H, d]
+    pr = F.linear(rel[:2 * span], lw.wqkv[:2 * D], lw.bqkv[:2 * D]).view(2 * span, 2, H, d)
+    query_rel, key_rel = pr[:, 0].transpose(0, 1), pr[:, 1].transpose(0, 1)
+    ctx = torch.empty(B, L, H, d, dtype=x.dtype, device=x.device)
+    flash_deberta_attention_fused(q, k, v, seq_lengths, key_rel, query_rel, 1.0 / math.sqrt(3 * d),
+                                  w.position_buckets if w.position_buckets > 0 else span,
+                                  w.max_relative_positions, w.position_buckets > 0,
+                                  out=ctx.transpose(1, 2))
+    h = fused_add_layernorm(F.linear(ctx.view(B, L, D), lw.wo, lw.bo), x, lw.ln1_w, lw.ln1_b,
+                            w.eps, return_sum=False)
+    inter = activation(F.linear(h, lw.wi, lw.bi), "gelu")
+    return fused_add_layernorm(F.linear(inter, lw.wo2, lw.bo2), h, lw.ln2_w, lw.ln2_b, w.eps,
+                               return_sum=False)
+
+
+def deberta_forward(x: torch.Tensor, seq_lengths: torch.Tensor, w: DebertaWeights,
+                    num_layers: Optional[int] = None) -> torch.Tensor:
+    """Encoder stack on embedding output x [B, L, hidden] -> last hidden state."""
+    rel = deberta_rel_embeddings(w)
+    n = len(w.layers) if num_layers is None else num_layers
+    for i in range(n):
+        x = deberta_layer_forward(x, seq_lengths, rel, w.layers[i], w)
+    return x

@@ -92,12 +92,15 @@ def flash_deberta_attention_fused(
     position_buckets: int = 256,
     max_relative_distance: int = 512,
     use_log_bucket: bool = True,
+    out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Disentangled attention with c2p / p2c computed inside the kernel.
 
     key_rel, query_rel: [H, 2*ATT_SPAN, D] per-head projections of the
     relative-position embeddings. Equivalent to flash_deberta_attention with
-    pos_key = q @ key_rel^T and pos_query = k @ query_rel^T.
+    pos_key = q @ key_rel^T and pos_query = k @ query_rel^T. `out` may be a
+    strided [B, H, M, D] view (e.g. of a [B, M, H, D] buffer) with contiguous
+    16-byte-aligned rows; it is written in place and returned.
     """
     dev = _lib.require_gpu(q, k, v, key_rel, query_rel)
     B = q.shape[0]
@@ -105,7 +108,11 @@ def flash_deberta_attention_fused(
     kr = _lib.rows_aligned(key_rel.to(q.dtype)) if key_rel is not None else None
     qr = _lib.rows_aligned(query_rel.to(q.dtype)) if query_rel is not None else None
     sl = _seq_lengths(seq_lengths, B, dev)
-    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    elif (out.shape != q.shape or out.dtype != q.dtype or out.device != q.device
+          or _lib.rows_aligned(out) is not out):
+        raise ValueError("out must match q's shape, dtype and device, with contiguous 16-byte rows")
     _lib.on_device(
         "vfk_deberta_fused_fwd", dev,
         _lib.ref(_lib.desc(qq)), _lib.ref(_lib.desc(kk)), _lib.ref(_lib.desc(vv)),

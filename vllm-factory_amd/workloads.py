@@ -137,6 +137,16 @@ def config3(batch: int = 32, device="cpu", dtype=torch.bfloat16) -> DebertaCase:
     return DebertaCase(q, k, v, key_rel, query_rel, lengths.to(torch.int32).to(device))
 
 
+def config3_hidden(batch: int = 32):
+    """The config-3 layer input: (hidden [B, 512, 1024] ~ N(0, 1), lengths
+    int32 [B]), the same draws config3 starts from. Layer weights:
+    encoders.deberta.random_weights."""
+    g = gen(3)
+    lengths = _lengths(g, 32, 256, 512)[:batch]
+    hidden = torch.randn(32, 512, 1024, generator=g)[:batch]
+    return hidden, lengths.to(torch.int32)
+
+
 # ---------------------------------------------------------------------------
 # config 4
 # ---------------------------------------------------------------------------
