@@ -106,3 +106,45 @@ def test_zero_length_rows(dev):
     pk, pq = oa.deberta_position_projections(q, k, kr, qr)
     want = oa.deberta_flash_attention(q, k, v, lens, pk, pq, SM, 64, 128, True)
     assert_attn_close(got[1], want[1], "zero-length batch row")
+
+
+@pytest.mark.parametrize("which", ["c2p", "p2c", "none"])
+def test_fused_partial_projections_linear_buckets(dev, which):
+    """One or neither position projection, linear buckets clamped at +-S
+    (L = 200 > S = 64)."""
+    q, k, v, kr, qr, lens = _case(3, 2, 200, 64, torch.bfloat16, 7, lens=[200, 130, 63])
+    pk, pq = oa.deberta_position_projections(q, k, kr, qr)
+    pk = pk if which == "c2p" else None
+    pq = pq if which == "p2c" else None
+    want = oa.deberta_flash_attention(q, k, v, lens, pk, pq, SM, 64, 128, False)
+    got = _k().flash_deberta_attention_fused(
+        q.to(dev), k.to(dev), v.to(dev), lens.to(dev), kr.to(dev) if which == "c2p" else None,
+        qr.to(dev) if which == "p2c" else None, SM, 64, 128, False)
+    for b, n in enumerate(lens.tolist()):
+        assert_attn_close(got[b, :, :n], want[b, :, :n], f"fused {which} b={b}")
+        assert torch.all(got[b, :, n:] == 0)
+
+
+def test_fused_strided_views_and_out(dev):
+    """q/k/v as head-transposed views of one [B, L, 3, H, 64] projection,
+    key_rel / query_rel as views of one [2S, 2, H, 64] projection, and the
+    output written in place into a [B, L, H, 64] buffer."""
+    B, L, H, S = 2, 150, 3, 64
+    g = torch.Generator().manual_seed(8)
+    qkv = (torch.randn(B, L, 3, H, 64, generator=g) * 0.8).to(torch.bfloat16)
+    rel = (torch.randn(2 * S, 2, H, 64, generator=g) * 0.8).to(torch.bfloat16)
+    lens = torch.tensor([150, 91], dtype=torch.int32)
+    qd, reld = qkv.to(dev), rel.to(dev)
+    buf = torch.full((B, L, H, 64), float("nan"), dtype=torch.bfloat16, device=dev)
+    got = _k().flash_deberta_attention_fused(
+        qd[:, :, 0].transpose(1, 2), qd[:, :, 1].transpose(1, 2), qd[:, :, 2].transpose(1, 2),
+        lens.to(dev), reld[:, 1].transpose(0, 1), reld[:, 0].transpose(0, 1), SM, S, 128, True,
+        out=buf.transpose(1, 2))
+    assert got.data_ptr() == buf.data_ptr()
+    q, k, v = (qkv[:, :, i].transpose(1, 2).contiguous() for i in range(3))
+    kr, qr = rel[:, 1].transpose(0, 1).contiguous(), rel[:, 0].transpose(0, 1).contiguous()
+    pk, pq = oa.deberta_position_projections(q, k, kr, qr)
+    want = oa.deberta_flash_attention(q, k, v, lens, pk, pq, SM, S, 128, True)
+    for b, n in enumerate(lens.tolist()):
+        assert_attn_close(got[b, :, :n], want[b, :, :n], f"strided b={b}")
+        assert torch.all(buf[b, n:] == 0)

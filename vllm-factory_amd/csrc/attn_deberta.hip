@@ -203,33 +203,83 @@ __global__ __launch_bounds__(64) void deberta_gather_f32_kernel(DebArgs a) {
 //   c2p(i,j) = q_i . Kr[c(i-j)],   p2c(i,j) = k_j . Qr[c(i-j)].
 // For a workgroup (128 rows from q0) and a key tile (64 keys from key0) the
 // indices c(i-j) lie in a window of at most 191 rows starting at
-// wbase = c(q0 - key0 - 63) (c is monotone). Per tile:
-//   P^T[idx][key] = Qr[wbase+idx] . K[key]  (MFMA, shared, LDS "PT")
-//   C^T[idx][row] = Kr[cw+idx] . q[row]     (MFMA, per wave, 96-row window)
-// then every score gathers C[c - cw][row] and PT[key][c - wbase].
+// wlo = c(q0 - key0 - 63) (c is monotone); for one wave's 32 rows, in a window
+// of at most 95 rows from cwl = c(qw0 - key0 - 63). Per tile:
+//   P^T[key][idx] = Qr[wlo+idx] . K[key]  (MFMA, shared by the workgroup:
+//                   wave w computes index blocks w and w + 4 for both key
+//                   blocks, so every Qr row is fetched once)
+//   C[row][idx]   = Kr[cwl+idx] . q[row]  (MFMA, per wave)
+// only over the 32-row index blocks that hold a used c (fewer where the log
+// buckets compress distances), both rounded to the element type (the
+// precision of the reference's pos_key / pos_query tensors) and written to
+// LDS as 8-byte runs; every score then adds C[row][c - cwl] and
+// P^T[key][c - wlo], with c read from a table of 2 c(d) over the
+// workgroup's relative positions. The Qr operands of tile i + 1 are fetched
+// into registers during tile i; the Kr operands at the start of the tile.
+//
+// Step for key tile i (K(i) resident since the previous step):
+//   direct load V(i); Kr loads; P^T and C blocks; S = K(i) Q^T; barrier;
+//   direct load K(i+1), Qr loads of tile i + 1; bias gathers; online
+//   softmax; O += V(i)^T P; barrier (K(i+1) landed, V / P^T / C free again)
 // ---------------------------------------------------------------------------
-constexpr int kPwin = 192;              // WG window rows (6 blocks of 32)
-constexpr int kCwin = 96;               // wave window rows (3 blocks of 32)
-constexpr int kPTs = kPwin + 8;         // PT row stride (u16), 8B-aligned rows
-constexpr int kCs = 33;                 // C row stride (u16): conflict-free reads
+constexpr int kPTs = 204;               // P^T row stride (u16): 8-byte rows, odd dword pairs
+constexpr int kCs = 100;                // C row stride (u16): 8-byte rows
 constexpr int kPTElems = kBN * kPTs;
-constexpr int kCElems = kCwin * kCs;    // per wave
+constexpr int kCElems = 32 * kCs;       // per wave
+constexpr int kFusedStaticLds = (3 * kTileElems + kPTElems + 4 * kCElems) * 2;
 
-// Rel-table MFMA operand: row r (clamped into the table), d chunk of lane.
-__device__ inline u32x4_t rel_row(const uint16_t* __restrict__ base, int64_t rs, int r, int rmax, int ds) {
-  const int h = (threadIdx.x & 63) >> 5;
-  r = min(r, rmax);
-  return *reinterpret_cast<const u32x4_t*>(base + (int64_t)r * rs + ds * 16 + 8 * h);
+// Rel-table MFMA operand through a buffer resource over the table's 2S rows
+// (rows past the table read as zeros; their products are never used): lane
+// byte offset voff = row-in-block * rs2 + 16 h, block row offset in soff.
+__device__ inline u32x4_t rel_ld(rsrc_t r, int voff, int soff, int ds) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 32 * ds, soff, 0));
 }
 
+// Writes the lane's four 4-element runs of an MFMA output block (rows
+// 8j + 4h .. +3 of the block, this lane's column) to a row-major array:
+// run j lands at byte offset off + 16 j.
 template <typename E>
+__device__ inline void store_runs(uint16_t* __restrict__ base, int off, const f32x16_t& acc) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    u32x2_t wv;
+    wv[0] = E::pack2(acc[4 * j], acc[4 * j + 1]);
+    wv[1] = E::pack2(acc[4 * j + 2], acc[4 * j + 3]);
+    *reinterpret_cast<u32x2_t*>(reinterpret_cast<char*>(base) + off + 16 * j) = wv;
+  }
+}
+
+// C blocks ib < NB of one wave: C[row][idx] = Kr[cwl + idx] . q[row].
+template <int NB>
+__device__ inline void c_loads(rsrc_t kr_r, int kr_lane, int cwl, int kr_rs2, u32x4_t (&ca)[3][4]) {
+#pragma unroll
+  for (int ib = 0; ib < NB; ++ib)
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) ca[ib][ds] = rel_ld(kr_r, kr_lane, (cwl + ib * 32) * kr_rs2, ds);
+}
+template <typename E, int NB>
+__device__ inline void c_blocks(const u32x4_t (&ca)[3][4], const u32x4_t (&qf)[4],
+                                uint16_t* __restrict__ Cm, int c_row) {
+  f32x16_t acc[NB] = {};
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+    for (int ib = 0; ib < NB; ++ib) acc[ib] = E::mfma32(ca[ib][ds], qf[ds], acc[ib]);
+  // lane holds row cl, indices ib*32 + 8j + 4h + 0..3
+  const int hl = (threadIdx.x & 63) >> 5;
+#pragma unroll
+  for (int ib = 0; ib < NB; ++ib) store_runs<E>(Cm, c_row + (ib * 32 + 4 * hl) * 2, acc[ib]);
+}
+
+template <typename E, bool C2P, bool P2C>
 __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
+  __shared__ __align__(16) uint16_t K0[kTileElems];
+  __shared__ __align__(16) uint16_t K1[kTileElems];
+  __shared__ __align__(16) uint16_t Vs[kTileElems];
+  __shared__ __align__(16) uint16_t PT[P2C ? kPTElems : 8];
+  __shared__ __align__(16) uint16_t Cm[C2P ? 4 * kCElems : 8];
   extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);
-  uint16_t* Vt = Ks + kKsElems;
-  uint16_t* PT = Vt + kVtElems;
-  uint16_t* Cw0 = PT + kPTElems;
-  int16_t* lut = reinterpret_cast<int16_t*>(Cw0 + 4 * kCElems);
+  int16_t* lut = reinterpret_cast<int16_t*>(smem);  // 2 c(dmin + e)
 
   const int nqt = (a.M + kBM - 1) / kBM;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
@@ -237,119 +287,148 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
   const int bh = work / nqt;
   const int h = bh % a.H, b = bh / a.H;
   const int q0 = qt * kBM;
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6, hl = lane >> 5, cl = lane & 31;
+  const int t = threadIdx.x, lane = t & 63, hl = lane >> 5, cl = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int len = a.seq_lengths ? min(max(a.seq_lengths[b], 0), a.N) : a.N;
-  const int qrow = q0 + w * 32 + cl;
+  const int qw0 = q0 + w * 32;
+  const int qrow = qw0 + cl;
   const bool qstore = qrow < a.M;
   const bool qvalid = qrow < min(len, a.M);
   uint16_t* orow = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1] + (int64_t)qrow * a.os[2];
-  const int kend = len;
-  const int kt_end = (max(kend, 0) + kBN - 1) / kBN;
-  if (q0 >= len || kt_end == 0) {
+  if (q0 >= len) {  // every row of the tile is padding (len may be 0): zeros
     if (qstore) {
       f32x16_t z = {};
       store_out<E>(orow, z, z, 0.f);
     }
     return;
   }
+  const int kt_end = (len + kBN - 1) / kBN;
   const int dmin = q0 - (kt_end * kBN - 1);
-  for (int e = t; e < a.lut_len; e += 256) lut[e] = (int16_t)deb_index(a, dmin + e);
+  for (int e = t; e < a.lut_len; e += 256) lut[e] = (int16_t)(2 * deb_index(a, dmin + e));
 
   const uint16_t* Qp = reinterpret_cast<const uint16_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
-  const uint16_t* Kp = reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
-  const uint16_t* Vp = reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
-  const uint16_t* Kr = a.kr ? reinterpret_cast<const uint16_t*>(a.kr) + h * a.krs[0] : nullptr;
-  const uint16_t* Qr = a.qr ? reinterpret_cast<const uint16_t*>(a.qr) + h * a.qrs[0] : nullptr;
-  const int rmax = 2 * a.span - 1;
-  uint16_t* Cw = Cw0 + w * kCElems;
+  TileSrc ksrc, vsrc;
+  tile_src_init(ksrc, reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1], (int)a.ks[2], len);
+  tile_src_init(vsrc, reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1], (int)a.vs[2], len);
+  tile_load_buf(ksrc, 0, K0);
+  const int kr_rs2 = C2P ? (int)a.krs[1] * 2 : 0, qr_rs2 = P2C ? (int)a.qrs[1] * 2 : 0;
+  const rsrc_t kr_r = __builtin_amdgcn_make_buffer_rsrc(
+      C2P ? const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(a.kr) + h * a.krs[0]) : nullptr, 0,
+      2 * a.span * kr_rs2, kRsrcWord3);
+  const rsrc_t qr_r = __builtin_amdgcn_make_buffer_rsrc(
+      P2C ? const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(a.qr) + h * a.qrs[0]) : nullptr, 0,
+      2 * a.span * qr_rs2, kRsrcWord3);
+  const int kr_lane = cl * kr_rs2 + 16 * hl, qr_lane = cl * qr_rs2 + 16 * hl;
 
   u32x4_t qf[4];
   load_q(qf, Qp + (int64_t)qrow * a.qs[2], qvalid);
   float m = -INFINITY, l = 0.f;
   f32x16_t o0 = {}, o1 = {};
-  const int lut_lane = qrow - 4 * hl - dmin;
-  const int qw0 = q0 + w * 32;
+  KOff ko;
+  VOff vo;
+  k_offsets(ko);
+  v_offsets(vo);
+  const bool wave_on = __builtin_amdgcn_readfirstlane((int)(qw0 < min(len, a.M))) != 0;
+  const int lut_lane = qrow - 4 * hl - dmin;  // table index of (qrow, key0 + 4hl) is lut_lane - key0
+  const int c_row = (w * 32 + cl) * kCs * 2;  // byte offset of this lane's C row
+  const int pt_row = 4 * hl * kPTs * 2;       // byte offset of P^T row 4h
+  tile_barrier();  // table and K(0) ready
 
-  KVStage st;
-  kv_load(st, Kp, a.ks[2], Vp, a.vs[2], 0, kend);
-  __syncthreads();  // lut ready
-  for (int kt = 0; kt < kt_end; ++kt) {
-    const int key0 = kt * kBN;
-    kv_store(st, Ks, Vt);
-    const int wbase = lut[q0 - key0 - 63 - dmin];
-    const int whi = lut[min(q0 + kBM - 1, a.M - 1) - key0 - dmin];
-    const int cw = lut[qw0 - key0 - 63 - dmin];
-    const int cwhi = lut[min(qw0 + 31, a.M - 1) - key0 - dmin];
-    __syncthreads();  // K tile in LDS
-    if (kt + 1 < kt_end) kv_load(st, Kp, a.ks[2], Vp, a.vs[2], (kt + 1) * kBN, kend);
+  // P^T blocks of this wave: index blocks w and (waves 0, 1) w + 4, both key
+  // blocks; their Qr operands are loaded one tile ahead into pa
+  const bool two = w < 2;
+  u32x4_t pa[2][4];
+  // index blocks of the workgroup's window that hold a used c (1 to 6)
+  auto pt_blocks = [&](int i) {
+    const int wl = __builtin_amdgcn_readfirstlane(lut[q0 - i * kBN - 63 - dmin]) >> 1;
+    const int wh = __builtin_amdgcn_readfirstlane(lut[q0 + kBM - 1 - i * kBN - dmin]) >> 1;
+    return (wh - wl) / 32 + 1;
+  };
+  auto pt_loads = [&](int i) {
+    const int wl = __builtin_amdgcn_readfirstlane(lut[q0 - i * kBN - 63 - dmin]) >> 1;
+    const int nbp = pt_blocks(i);
+    if (w < nbp) {
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) pa[0][ds] = rel_ld(qr_r, qr_lane, (wl + w * 32) * qr_rs2, ds);
+    }
+    if (two && w + 4 < nbp) {
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) pa[1][ds] = rel_ld(qr_r, qr_lane, (wl + (w + 4) * 32) * qr_rs2, ds);
+    }
+  };
+  if (P2C) pt_loads(0);
 
-    // ---- P^T blocks (WG-shared): wave w takes blocks w, w+4, w+8 of 6x2
-    if (Qr) {
-      const int nbp = (whi - wbase) / 32 + 1;
+  auto step = [&](int i, const uint16_t* __restrict__ Kc, uint16_t* __restrict__ Kn) {
+    const int key0 = i * kBN;
+    tile_load_buf(vsrc, key0, Vs);
+    const int wlo = __builtin_amdgcn_readfirstlane(lut[q0 - key0 - 63 - dmin]) >> 1;
+    const int cwl = __builtin_amdgcn_readfirstlane(lut[qw0 - key0 - 63 - dmin]) >> 1;
+    // C blocks of the wave's window that hold a used c (1 to 3)
+    const int cwh = __builtin_amdgcn_readfirstlane(lut[qw0 + 31 - key0 - dmin]) >> 1;
+    const int nbc = (cwh - cwl) / 32 + 1;
+    u32x4_t ca[3][4];
+    if (C2P && wave_on) {
+      if (nbc >= 3) c_loads<3>(kr_r, kr_lane, cwl, kr_rs2, ca);
+      else if (nbc == 2) c_loads<2>(kr_r, kr_lane, cwl, kr_rs2, ca);
+      else c_loads<1>(kr_r, kr_lane, cwl, kr_rs2, ca);
+    }
+    const int nbp = P2C ? pt_blocks(i) : 0;
+    const bool two_i = two && w + 4 < nbp;
+    if (P2C && w < nbp) {
 #pragma unroll
-      for (int bi = 0; bi < 3; ++bi) {
-        const int blk = w + 4 * bi;
-        const int ib = blk >> 1, kb = blk & 1;
-        if (ib < nbp) {
-          f32x16_t acc = {};
+      for (int kb = 0; kb < 2; ++kb) {
+        u32x4_t kf[4];
 #pragma unroll
-          for (int ds = 0; ds < 4; ++ds) {
-            const u32x4_t av = rel_row(Qr, a.qrs[1], wbase + ib * 32 + cl, rmax, ds);
-            const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(Ks + (kb * 32 + cl) * kKsStride + ds * 16 + 8 * hl);
-            acc = E::mfma32(av, bv, acc);
-          }
-          // lane holds key kb*32+cl, idx ib*32 + 8*(r/4) + 4*hl + r%4
-          uint16_t* prow = PT + (kb * 32 + cl) * kPTs + ib * 32 + 4 * hl;
+        for (int ds = 0; ds < 4; ++ds) kf[ds] = lds_at<u32x4_t>(Kc, lds_opaque(ko.o[ds]) + kb * 4096);
+        f32x16_t acc0 = {}, acc1 = {};
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            u32x2_t wv;
-            wv[0] = E::pack2(acc[4 * j], acc[4 * j + 1]);
-            wv[1] = E::pack2(acc[4 * j + 2], acc[4 * j + 3]);
-            *reinterpret_cast<u32x2_t*>(prow + 8 * j) = wv;
-          }
+        for (int ds = 0; ds < 4; ++ds) {
+          acc0 = E::mfma32(pa[0][ds], kf[ds], acc0);
+          if (two_i) acc1 = E::mfma32(pa[1][ds], kf[ds], acc1);
         }
+        // lane holds key kb*32 + cl, indices ib*32 + 8j + 4h + 0..3
+        store_runs<E>(PT, ((kb * 32 + cl) * kPTs + w * 32 + 4 * hl) * 2, acc0);
+        if (two_i) store_runs<E>(PT, ((kb * 32 + cl) * kPTs + (w + 4) * 32 + 4 * hl) * 2, acc1);
       }
     }
-    // ---- C^T for this wave's 32 rows over [cw, cw + 96)
-    if (Kr) {
-      const int nbc = (cwhi - cw) / 32 + 1;
-#pragma unroll
-      for (int ib = 0; ib < 3; ++ib) {
-        if (ib < nbc) {
-          f32x16_t acc = {};
-#pragma unroll
-          for (int ds = 0; ds < 4; ++ds) {
-            const u32x4_t av = rel_row(Kr, a.krs[1], cw + ib * 32 + cl, rmax, ds);
-            acc = E::mfma32(av, qf[ds], acc);
-          }
-          // lane holds row cl, idx ib*32 + 8*(r/4) + 4*hl + r%4
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int idx = ib * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
-            Cw[idx * kCs + cl] = E::from_f32(acc[r]);
-          }
-        }
-      }
+    if (C2P && wave_on) {
+      if (nbc >= 3) c_blocks<E, 3>(ca, qf, Cm, c_row);
+      else if (nbc == 2) c_blocks<E, 2>(ca, qf, Cm, c_row);
+      else c_blocks<E, 1>(ca, qf, Cm, c_row);
     }
-    __syncthreads();  // PT and C complete
-
     f32x16_t s0, s1;
-    qk_tile<E>(Ks, qf, s0, s1);
-    const int16_t* lp = lut + (lut_lane - key0);
-    map_scores(s0, s1, [&](int e, float v) {
-      const int xk = x_key(e, 0);
-      const int c = lp[-xk];
-      float bias = 0.f;
-      if (Kr) bias += E::to_f32(Cw[(c - cw) * kCs + cl]);
-      if (Qr) bias += E::to_f32(PT[(xk + 4 * hl) * kPTs + (c - wbase)]);
-      v += bias;
-      return (key0 + xk + 4 * hl >= kend) ? -INFINITY : v;
-    });
-    u32x4_t p[4];
-    softmax_tile<E>(s0, s1, a.c2, m, l, o0, o1, p);
-    pv_tile<E>(Vt, p, o0, o1);
-    __syncthreads();
+    if (wave_on) qk_tile_sw<E>(Kc, ko, qf, s0, s1);
+    tile_barrier();  // V(i), P^T and C visible
+    if (i + 1 < kt_end) {
+      tile_load_buf(ksrc, key0 + kBN, Kn);
+      if (P2C) pt_loads(i + 1);
+    }
+    if (wave_on) {
+      const int lb = lut_lane - key0;
+      const int cb = lds_opaque(c_row - 2 * cwl), pb = lds_opaque(pt_row - 2 * wlo);
+      map_scores(s0, s1, [&](int e, float v) {
+        const int xk = x_key(e, 0);
+        const int c2 = lut[lb - xk];
+        if (C2P) v += E::to_f32(lds_at<uint16_t>(Cm, cb + c2));
+        if (P2C) v += E::to_f32(lds_at<uint16_t>(PT, pb + xk * (kPTs * 2) + c2));
+        return v;
+      });
+      if (key0 + kBN > len) {
+        map_scores(s0, s1, [&](int e, float v) { return key0 + x_key(e, hl) >= len ? -INFINITY : v; });
+      }
+      u32x4_t p[4];
+      softmax_tile<E>(s0, s1, a.c2, m, l, o0, o1, p);
+      pv_tile_sw<E>(Vs, vo, p, o0, o1);
+    }
+    tile_barrier();  // K(i+1) landed; V, P^T, C free
+  };
+  int i = 0;
+  for (; i + 1 < kt_end; i += 2) {
+    step(i, K0, K1);
+    step(i + 1, K1, K0);
   }
+  if (i < kt_end) step(i, K0, K1);
+
   const float l_tot = half_swap_sum(l);
   if (qstore) {
     if (!qvalid) {
@@ -564,13 +643,33 @@ extern "C" int vfk_deberta_fused_fwd(const vfk_tensor* q, const vfk_tensor* k, c
   }
   const int ntk = ceil_div(a.N, kBN);
   a.lut_len = ntk * kBN + kBM;
-  const size_t lds = (size_t)(kKsElems + kVtElems + kPTElems + 4 * kCElems) * 2 + (size_t)a.lut_len * 2;
-  if (lds > 160 * 1024) return set_error(VFK_ERR_UNSUPPORTED, "vfk_deberta_fused_fwd: N too large");
+  const size_t dyn = (size_t)a.lut_len * 2;
+  if (kFusedStaticLds + dyn > 160 * 1024)
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_deberta_fused_fwd: N too large");
+  // the table holds 2 c in int16; the K / V buffer resources span N rows
+  if (a.span > 8192)
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_deberta_fused_fwd: att_span above 8192");
+  if ((a.kr && 4 * (int64_t)a.span * a.krs[1] >= ((int64_t)1 << 31)) ||
+      (a.qr && 4 * (int64_t)a.span * a.qrs[1] >= ((int64_t)1 << 31)))
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_deberta_fused_fwd: rel tables span 2 GiB or more");
+  if ((int64_t)a.N * (a.ks[2] > a.vs[2] ? a.ks[2] : a.vs[2]) * 2 >= ((int64_t)1 << 31))
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_deberta_fused_fwd: K / V rows span 2 GiB or more");
   const int nqt = ceil_div(a.M, kBM);
   dim3 grid((unsigned)(nqt * a.B * a.H));
-  if (q->dtype == VFK_BF16)
-    hipLaunchKernelGGL(deberta_fused_kernel<BF16>, grid, dim3(256), lds, st, a);
-  else
-    hipLaunchKernelGGL(deberta_fused_kernel<F16>, grid, dim3(256), lds, st, a);
+#define VFK_DEB_GO(E, C, P) \
+  hipLaunchKernelGGL((deberta_fused_kernel<E, C, P>), grid, dim3(256), dyn, st, a)
+  const bool c2p = a.kr != nullptr, p2c = a.qr != nullptr;
+  if (q->dtype == VFK_BF16) {
+    if (c2p && p2c) VFK_DEB_GO(BF16, true, true);
+    else if (c2p) VFK_DEB_GO(BF16, true, false);
+    else if (p2c) VFK_DEB_GO(BF16, false, true);
+    else VFK_DEB_GO(BF16, false, false);
+  } else {
+    if (c2p && p2c) VFK_DEB_GO(F16, true, true);
+    else if (c2p) VFK_DEB_GO(F16, true, false);
+    else if (p2c) VFK_DEB_GO(F16, false, true);
+    else VFK_DEB_GO(F16, false, false);
+  }
+#undef VFK_DEB_GO
   return launch_status("vfk_deberta_fused_fwd");
 }
