@@ -361,6 +361,10 @@ def cpu_baseline(torch, c2, min_seconds=10.0):
                        f"{dt:.1f} s")
 
 
+def _progress(what):
+    print(f"[bench] {what} done", file=sys.stderr, flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -384,14 +388,17 @@ def main():
         traffic_workload(torch)
         return
     head, c2 = headline(torch, args)
+    _progress("headline")
     extra = {}
     if args.only != "headline":
-        extra["rpb_mt5_large_config4"] = rpb_config4(torch, args)
-        extra["deberta_v3_large_config3"] = deberta_config3(torch, args)
-        extra["epilogues"] = epilogue_bench(torch, args, c2)
-        extra["mt5_large_layer_config4"] = mt5_layer_config4(torch, args)
-        extra["deberta_v3_large_layer_config3"] = deberta_layer_config3(torch, args)
-        extra["modernbert_encoder_config5"] = encoder_config5(torch, args)
+        for key, fn in (("rpb_mt5_large_config4", lambda: rpb_config4(torch, args)),
+                        ("deberta_v3_large_config3", lambda: deberta_config3(torch, args)),
+                        ("epilogues", lambda: epilogue_bench(torch, args, c2)),
+                        ("mt5_large_layer_config4", lambda: mt5_layer_config4(torch, args)),
+                        ("deberta_v3_large_layer_config3", lambda: deberta_layer_config3(torch, args)),
+                        ("modernbert_encoder_config5", lambda: encoder_config5(torch, args))):
+            extra[key] = fn()
+            _progress(key)
     line = {
         "metric": "encoder attn TFLOP/s + % bf16 MFMA peak at L=512-768; end-to-end tokens/s",
         "value": head["value"],
@@ -415,6 +422,7 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, c2)
+        _progress("cpu_baseline")
     print(json.dumps(line))
 
 
