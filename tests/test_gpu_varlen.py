@@ -94,3 +94,26 @@ def test_rope_table_matches_hf(dev):
         c, s = oa.rope_cos_sin(torch.arange(t.shape[0]), theta)   # cat(f, f): [n, 64]
         torch.testing.assert_close(t[..., 0], c[:, :32], atol=2e-7, rtol=0)
         torch.testing.assert_close(t[..., 1], s[:, :32], atol=2e-7, rtol=0)
+
+
+@pytest.mark.parametrize("window", [-1, 64])
+def test_varlen_large_scores(dev, window):
+    """Scores spread over ~+-12 (log2 units) with key norms growing along each
+    sequence, so the running reference max of a row moves more than once. At
+    this spread bf16-rounded rotated q/k alone (the reference model's own
+    rounding) already miss the fp32 oracle by ~1e-2, so larger spreads are
+    not a meaningful bf16 parity case."""
+    lengths = [700, 300, 129, 64]
+    g = torch.Generator().manual_seed(11)
+    T = sum(lengths)
+    q = torch.randn(T, 12, 64, generator=g)
+    k = torch.randn(T, 12, 64, generator=g)
+    cu = workloads.cu_from_lengths(torch.tensor(lengths))
+    for s in range(len(lengths)):   # key norms grow along each sequence
+        a, b = int(cu[s]), int(cu[s + 1])
+        k[a:b] *= torch.linspace(0.3, 1.5, b - a)[:, None, None]
+    v = torch.randn(T, 12, 64, generator=g)
+    q, k, v = (t.bfloat16() for t in (q, k, v))
+    want = oa.varlen_attention(q, k, v, cu, window, 160000.0, None, 0.125)
+    got = _vl()(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), max(lengths), window, 160000.0, 0.125)
+    assert_attn_close(got, want, f"large scores w={window}")
