@@ -28,6 +28,11 @@ struct Elt<VFK_F32> {
     f32x4_t v = {f[0], f[1], f[2], f[3]};
     *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(base) + i) = v;
   }
+  __device__ static inline void load_nt(const void* base, int64_t i, float* f) {
+    const f32x4_t v = __builtin_nontemporal_load(
+        reinterpret_cast<const f32x4_t*>(reinterpret_cast<const float*>(base) + i));
+    f[0] = v[0]; f[1] = v[1]; f[2] = v[2]; f[3] = v[3];
+  }
   __device__ static inline float ld1(const void* base, int64_t i) {
     return reinterpret_cast<const float*>(base)[i];
   }
@@ -47,6 +52,16 @@ struct Elt16 {
   __device__ static inline void store(void* base, int64_t i, const float* f) {
     *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(base) + i) =
         pack8<E>(f);
+  }
+  // streaming load for the large, read-once operands of the gated
+  // activations (the FFN up/gate projections, larger than the last-level
+  // cache): they are kept out of the caches, which then still hold the output
+  // for the GEMM that consumes it. Inputs that a previous kernel has just
+  // written and that fit in the caches (the norms' rows) use plain loads.
+  __device__ static inline void load_nt(const void* base, int64_t i, float* f) {
+    const u32x4_t v = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(base) + i));
+    unpack8<E>(v, f);
   }
   __device__ static inline float ld1(const void* base, int64_t i) {
     return E::to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
@@ -441,14 +456,37 @@ struct BinArgs {
 #define VFK_OP_ADD 100
 #define VFK_OP_UNARY 200  // VFK_OP_UNARY + act: act(a), b unused
 
+// a * sigmoid(t) = a / (1 + e^-t) with the hardware exp2 and reciprocal
+// (relative error a few ulp; e^-t = inf gives 0, the limit).
+__device__ inline float mul_sigmoid(float a, float t) {
+  return a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-t * 1.4426950408889634f));
+}
+
+// erf(u) by Abramowitz & Stegun, Handbook of Mathematical Functions, 7.1.26
+// (absolute error <= 1.5e-7): 1 - (a1 t + ... + a5 t^5) e^(-u^2), t = 1 / (1 + p|u|).
+__device__ inline float erf_as(float u) {
+  const float x = fabsf(u);
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * x);
+  float poly = 1.061405429f;
+  poly = poly * t - 1.453152027f;
+  poly = poly * t + 1.421413741f;
+  poly = poly * t - 0.284496736f;
+  poly = poly * t + 0.254829592f;
+  const float y = 1.0f - poly * t * __builtin_amdgcn_exp2f(-x * x * 1.4426950408889634f);
+  return copysignf(y, u);
+}
+
 template <int ACT>
 __device__ inline float act_f(float a) {
-  if (ACT == VFK_ACT_GELU_ERF) return 0.5f * a * (1.0f + erff(a * 0.70710678118654752f));
+  if (ACT == VFK_ACT_GELU_ERF) return 0.5f * a * (1.0f + erf_as(a * 0.70710678118654752f));
   if (ACT == VFK_ACT_GELU_TANH) {
-    const float inner = 0.7978845608028654f * (a + 0.044715f * a * a * a);
-    return 0.5f * a * (1.0f + tanhf(inner));
+    // 0.5 a (1 + tanh(z)) = a sigmoid(2 z): the same identity as the
+    // reference's kernels/ff_fused.py:47-53, without the cancellation of
+    // 1 + tanh(z) for large negative z
+    const float z = 0.7978845608028654f * (a + 0.044715f * a * a * a);
+    return mul_sigmoid(a, 2.0f * z);
   }
-  if (ACT == VFK_ACT_SILU) return a / (1.0f + expf(-a));
+  if (ACT == VFK_ACT_SILU) return mul_sigmoid(a, a);
   return fmaxf(a, 0.f);  // VFK_ACT_RELU
 }
 
@@ -459,22 +497,50 @@ __device__ inline float apply_op(float a, float b) {
   return act_f<OP>(a) * b;
 }
 
-template <int DT, int OP>
-__global__ __launch_bounds__(256) void binary_vec_kernel(BinArgs p) {
+// 128-bit chunks. FLAT: every operand is one dense [rows * n] run, so chunk c
+// sits at element c * VEC of each. Otherwise chunk c is (row c / cpr, column
+// chunk c % cpr), with the quotient from a multiply-high by a host-computed
+// magic number (exact for c < 2^32: q = (umulhi(c, m) + c) >> l with
+// l = ceil(log2 cpr), m = 2^32 (2^l - cpr) / cpr + 1).
+// Each thread takes kBinU chunks per pass (blockDim apart, so a wave's
+// accesses stay contiguous) and issues all their loads before any use.
+constexpr int kBinU = 8;
+template <int DT, int OP, bool FLAT>
+__global__ __launch_bounds__(256) void binary_vec_kernel(BinArgs p, uint32_t cpr, uint32_t magic,
+                                                         int shift, uint32_t total) {
   using L = Elt<DT>;
   constexpr int VEC = L::VEC;
-  const int64_t cpr = p.n / VEC;
-  const int64_t total = p.rows * cpr;
-  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total;
-       c += (int64_t)gridDim.x * 256) {
-    const int64_t r = c / cpr;
-    const int64_t col = (c - r * cpr) * VEC;
-    float x[VEC], y[VEC];
-    L::load(p.a, r * p.a_rs + col, x);
-    if (OP < VFK_OP_UNARY) L::load(p.b, r * p.b_rs + col, y);
+  const uint32_t stride = gridDim.x * 256 * kBinU;
+  for (uint32_t c0 = blockIdx.x * 256 * kBinU + threadIdx.x; c0 < total; c0 += stride) {
+    int64_t ao[kBinU], bo[kBinU], yo[kBinU];
+    bool ok[kBinU];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) x[i] = apply_op<OP>(x[i], y[i]);
-    L::store(p.y, r * p.y_rs + col, x);
+    for (int u = 0; u < kBinU; ++u) {
+      const uint32_t c = c0 + u * 256;
+      ok[u] = c < total;
+      const uint32_t cc = ok[u] ? c : c0;  // in-bounds address for masked chunks
+      if (FLAT) {
+        ao[u] = bo[u] = yo[u] = (int64_t)cc * VEC;
+      } else {
+        const uint32_t r = (uint32_t)(((uint64_t)__umulhi(cc, magic) + cc) >> shift);
+        const int64_t col = (int64_t)(cc - r * cpr) * VEC;
+        ao[u] = (int64_t)r * p.a_rs + col;
+        bo[u] = (int64_t)r * p.b_rs + col;
+        yo[u] = (int64_t)r * p.y_rs + col;
+      }
+    }
+    float x[kBinU][VEC], y[kBinU][VEC];
+#pragma unroll
+    for (int u = 0; u < kBinU; ++u) {
+      L::load_nt(p.a, ao[u], x[u]);
+      if (OP < VFK_OP_UNARY) L::load_nt(p.b, bo[u], y[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kBinU; ++u) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) x[u][i] = apply_op<OP>(x[u][i], y[u][i]);
+      if (ok[u]) L::store(p.y, yo[u], x[u]);
+    }
   }
 }
 
@@ -499,10 +565,24 @@ static void launch_binary(const BinArgs& p, bool vec_ok, hipStream_t st) {
   int64_t blocks = (work + 255) / 256;
   if (blocks > 256 * 16) blocks = 256 * 16;
   if (blocks < 1) blocks = 1;
-  if (vec_ok)
-    hipLaunchKernelGGL((binary_vec_kernel<DT, OP>), dim3((unsigned)blocks), dim3(256), 0, st, p);
-  else
+  if (vec_ok && work < (1ll << 31)) {
+    blocks = std::min<int64_t>(blocks, (work + 256 * kBinU - 1) / (256 * kBinU));
+    const uint32_t cpr = (uint32_t)(p.n / VEC);
+    const bool flat = p.rows == 1 || (p.a_rs == p.n && p.y_rs == p.n &&
+                                      (OP >= VFK_OP_UNARY || p.b_rs == p.n));
+    if (flat) {
+      hipLaunchKernelGGL((binary_vec_kernel<DT, OP, true>), dim3((unsigned)blocks), dim3(256), 0, st,
+                         p, cpr, 0u, 0, (uint32_t)work);
+    } else {
+      int l = 0;
+      while ((1ull << l) < cpr) ++l;
+      const uint32_t m = (uint32_t)((((1ull << 32) * ((1ull << l) - cpr)) / cpr) + 1);
+      hipLaunchKernelGGL((binary_vec_kernel<DT, OP, false>), dim3((unsigned)blocks), dim3(256), 0, st,
+                         p, cpr, m, l, (uint32_t)work);
+    }
+  } else {
     hipLaunchKernelGGL((binary_scalar_kernel<DT, OP>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  }
 }
 
 template <int OP>
