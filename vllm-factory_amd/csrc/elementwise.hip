@@ -647,6 +647,83 @@ struct RopeArgs {
   int64_t B, S, H; int D;
 };
 
+// One thread per (row b*S + s, 128-bit chunk pair c) covering every head of
+// the row: the row's cos/sin chunks are loaded once for all heads, the loads
+// of 4 heads are issued before any of them is used, and (row, c) and (b, s)
+// come from multiply-high divisions by host-computed magic numbers.
+struct Magic {
+  uint32_t d, m;
+  int l;
+};
+static Magic magic_for(uint32_t d) {
+  Magic r;
+  r.d = d;
+  r.l = 0;
+  while ((1ull << r.l) < d) ++r.l;
+  r.m = (uint32_t)((((1ull << 32) * ((1ull << r.l) - d)) / d) + 1);
+  return r;
+}
+__device__ inline uint32_t magic_div(uint32_t x, const Magic& g) {
+  return (uint32_t)(((uint64_t)__umulhi(x, g.m) + x) >> g.l);
+}
+
+// Thread item t = ((b * S + s) * H + h) * cpr + c (chunk pair c of head h of
+// row (b, s)), consecutive items covering consecutive 16-byte chunks of the
+// row; kRopeU items per thread and pass, all loads issued before any use.
+constexpr int kRopeU = 4;
+template <int DT>
+__global__ __launch_bounds__(256) void rope_item_kernel(RopeArgs p, Magic gc, Magic gh, Magic gs,
+                                                        uint32_t total) {
+  using L = Elt<DT>;
+  constexpr int VEC = L::VEC;
+  const int half = p.D / 2;
+  const uint32_t stride = gridDim.x * 256 * kRopeU;
+  for (uint32_t t0 = blockIdx.x * 256 * kRopeU + threadIdx.x; t0 < total; t0 += stride) {
+    int64_t xo[kRopeU], yo[kRopeU], co[kRopeU], so[kRopeU];
+    bool ok[kRopeU];
+#pragma unroll
+    for (int u = 0; u < kRopeU; ++u) {
+      const uint32_t t = t0 + u * 256;
+      ok[u] = t < total;
+      const uint32_t tt = ok[u] ? t : t0;
+      const uint32_t rh = magic_div(tt, gc);
+      const int d0 = (int)(tt - rh * gc.d) * VEC;
+      const uint32_t r = magic_div(rh, gh);
+      const uint32_t h = rh - r * gh.d;
+      const uint32_t b = magic_div(r, gs);
+      const uint32_t sq = r - b * gs.d;
+      xo[u] = (int64_t)b * p.xs[0] + (int64_t)sq * p.xs[1] + (int64_t)h * p.xs[2] + d0;
+      yo[u] = (int64_t)b * p.ys[0] + (int64_t)sq * p.ys[1] + (int64_t)h * p.ys[2] + d0;
+      co[u] = (int64_t)b * p.cs[0] + (int64_t)sq * p.cs[1] + d0;
+      so[u] = (int64_t)b * p.ss[0] + (int64_t)sq * p.ss[1] + d0;
+    }
+    float x1[kRopeU][VEC], x2[kRopeU][VEC], c1[kRopeU][VEC], c2[kRopeU][VEC], s1[kRopeU][VEC],
+        s2[kRopeU][VEC];
+#pragma unroll
+    for (int u = 0; u < kRopeU; ++u) {
+      L::load(p.x, xo[u], x1[u]);
+      L::load(p.x, xo[u] + half, x2[u]);
+      L::load(p.c, co[u], c1[u]);
+      L::load(p.c, co[u] + half, c2[u]);
+      L::load(p.s, so[u], s1[u]);
+      L::load(p.s, so[u] + half, s2[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kRopeU; ++u) {
+      float y1[VEC], y2[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        y1[i] = x1[u][i] * c1[u][i] - x2[u][i] * s1[u][i];
+        y2[i] = x2[u][i] * c2[u][i] + x1[u][i] * s2[u][i];
+      }
+      if (ok[u]) {
+        L::store(p.y, yo[u], y1);
+        L::store(p.y, yo[u] + half, y2);
+      }
+    }
+  }
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs p) {
   using L = Elt<DT>;
@@ -789,8 +866,17 @@ extern "C" int vfk_rope_fwd(const vfk_tensor* x, const vfk_tensor* cos,
   int64_t blocks = (work + 255) / 256;
   if (blocks > 256 * 16) blocks = 256 * 16;
   hipStream_t st = (hipStream_t)stream;
+  const bool by_item = vec_ok && work < (1ll << 31);
+  const Magic gc = magic_for((uint32_t)std::max<int64_t>(1, D / 2 / VEC));
+  const Magic gh = magic_for((uint32_t)std::max<int64_t>(1, H));
+  const Magic gs = magic_for((uint32_t)std::max<int64_t>(1, S));
+  const unsigned item_blocks =
+      (unsigned)std::min<int64_t>(blocks, (work + 256 * kRopeU - 1) / (256 * kRopeU));
 #define VFK_ROPE(DT)                                                               \
-  if (vec_ok)                                                                      \
+  if (by_item)                                                                     \
+    hipLaunchKernelGGL((rope_item_kernel<DT>), dim3(item_blocks), dim3(256), 0, st, p, gc, gh, \
+                       gs, (uint32_t)work);                                        \
+  else if (vec_ok)                                                                 \
     hipLaunchKernelGGL((rope_vec_kernel<DT>), dim3((unsigned)blocks), dim3(256), 0, st, p); \
   else                                                                             \
     hipLaunchKernelGGL((rope_scalar_kernel<DT>), dim3((unsigned)blocks), dim3(256), 0, st, p);
