@@ -283,8 +283,16 @@ def encoder_config5(torch, args):
     ms = (time.perf_counter() - t0) * 1e3 / n
     T = int(c.lengths.sum())
     del w
+    # sequence boundaries from the flat position ids (the reference's input),
+    # on the device: 4 small launches, int64 positions in, cu_seqlens out
+    from kernels.varlen_attention import seq_metadata
+    pos = torch.cat([torch.arange(int(n)) for n in c.lengths]).to(dev)
+    for _ in range(args.warmup):
+        seq_metadata(pos)
+    meta_ms = device_ms(torch, lambda: seq_metadata(pos), args.steps)
     return dict(ms_per_forward=ms, tokens_per_s=T / (ms * 1e-3),
                 sequences_per_s=len(c.lengths) / (ms * 1e-3), tokens=T, layers=22,
+                seq_metadata_us=meta_ms * 1e3,
                 note="wall clock per forward (embeddings to final LayerNorm), GEMMs via torch/hipBLASLt")
 
 

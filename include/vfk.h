@@ -156,6 +156,30 @@ int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
 int64_t vfk_varlen_attn_workspace_bytes(int32_t dtype, int64_t total_tokens,
                                         int32_t num_heads, int32_t rope);
 
+/* Packed-sequence metadata from vLLM's flat position ids, on the device
+ * (no counterpart kernel in the reference: it replaces the boundary detection
+ * and cumsum of models/modernbert/modernbert_encoder.py:491-516
+ * (ModernBertModel._build_seq_block_mask), whose [T, T] masks the varlen
+ * attention does not need).
+ *   positions: device int32 or int64 [total_tokens] (pos_dtype_bytes 4 or 8);
+ *     a sequence starts at token 0 and at every i with pos[i] <= pos[i-1]
+ *   cu_seqlens: device int32 [total_tokens + 1]; entries 0..num_seqs are
+ *     written (start of each sequence, then total_tokens)
+ *   meta: device int32 [4] = {num_seqs, max_seqlen, bad, total_tokens}; bad
+ *     counts breaks in the run of positions (a sequence start whose position
+ *     is not 0, or a token whose position is not its predecessor's + 1); it
+ *     is 0 exactly when every position equals t - cu_seqlens[s], the position
+ *     vfk_varlen_attn_fwd gives token t (the reference's RoPE positions)
+ *   workspace: device memory of vfk_varlen_meta_workspace_bytes() bytes,
+ *     4-byte aligned; calls that share it must not overlap.
+ * Four small launches on `stream`; nothing is read back to the host. */
+int vfk_varlen_meta(const void* positions, int32_t pos_dtype_bytes,
+                    int64_t total_tokens, int32_t* cu_seqlens, int32_t* meta,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace size of vfk_varlen_meta: 4 bytes per 1024 tokens. */
+int64_t vfk_varlen_meta_workspace_bytes(int64_t total_tokens);
+
 /* RoPE cos/sin table of transformers' ModernBertRotaryEmbedding (default rope,
  * head_dim 64; the module the reference calls at
  * models/modernbert/modernbert_encoder.py:236-242): out[p][f] = (cos, sin) of

@@ -40,3 +40,16 @@ def test_modernbert_encoder_matches_oracle(layers, max_abs, min_cos):
     cs = cosine(got.float().cpu(), want)
     print(f"layers {layers}: max-abs {err:.3e} cosine {cs:.6f}")
     assert err <= max_abs and cs >= min_cos, (err, cs)
+
+
+def test_modernbert_from_position_ids_matches_cu_path():
+    """The reference's flat call (input_ids + position_ids, modernbert_encoder.py:430-480)
+    gives exactly the cu_seqlens-driven forward: same kernels, same boundaries."""
+    import encoders.modernbert as em
+    w, ids, cu, mx = _case()
+    dev = torch.device("cuda:0")
+    wd = w.to(dev)
+    pos = torch.cat([torch.arange(int(b - a)) for a, b in zip(cu[:-1], cu[1:])])
+    got = em.modernbert_forward_positions(ids.to(dev)[None], pos.to(dev)[None], wd, num_layers=2)
+    want = em.modernbert_forward(ids.to(dev), cu.to(dev), mx, wd, num_layers=2)
+    assert torch.equal(got, want)

@@ -100,3 +100,25 @@ def test_varlen_workspace_bytes():
     assert lib.vfk_varlen_attn_workspace_bytes(_lib.F16, 7, 3, 1) == 7 * 3 * 64 * 2
     assert lib.vfk_varlen_attn_workspace_bytes(_lib.BF16, 40265, 12, 0) == 0
     assert lib.vfk_varlen_attn_workspace_bytes(_lib.F32, 40265, 12, 1) == 0
+
+
+def test_varlen_meta_workspace_and_argument_checks():
+    """Rejected before any HIP call, so these run without a GPU."""
+    from kernels import _lib
+    from kernels.varlen_attention import seq_metadata
+    lib = _lib.load()
+    assert lib.vfk_varlen_meta_workspace_bytes(1) == 4
+    assert lib.vfk_varlen_meta_workspace_bytes(1024) == 4
+    assert lib.vfk_varlen_meta_workspace_bytes(163736) == 160 * 4
+    assert lib.vfk_varlen_meta_workspace_bytes(0) == 0
+    with pytest.raises(ValueError, match="NULL"):
+        _lib.call("vfk_varlen_meta", None, 8, 10, None, None, None, 0, None)
+    fake = 1 << 20  # never dereferenced: every case below fails its host checks
+    with pytest.raises(ValueError, match="int32 or int64"):
+        _lib.call("vfk_varlen_meta", fake, 2, 10, fake, fake, fake, 4, None)
+    with pytest.raises(ValueError, match="total_tokens"):
+        _lib.call("vfk_varlen_meta", fake, 8, 0, fake, fake, fake, 4, None)
+    with pytest.raises(ValueError, match="workspace"):
+        _lib.call("vfk_varlen_meta", fake, 8, 5000, fake, fake, fake, 16, None)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        seq_metadata(torch.arange(5))

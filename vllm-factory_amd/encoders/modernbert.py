@@ -26,7 +26,7 @@ import torch.nn.functional as F
 
 from kernels.fused_glu_mlp import fused_gelu_mul_dropout
 from kernels.fused_layernorm import fused_add_layernorm, fused_layernorm
-from kernels.varlen_attention import varlen_rope_attention
+from kernels.varlen_attention import varlen_from_positions, varlen_rope_attention
 
 MASK_TOKEN_ID = 50284
 
@@ -115,3 +115,14 @@ def modernbert_forward(ids: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: 
         return fused_layernorm(x, w.hidden, w.final_norm, None, w.eps)
     out, _ = fused_add_layernorm(pending, x, w.final_norm, None, w.eps)
     return out
+
+
+def modernbert_forward_positions(input_ids: torch.Tensor, position_ids: torch.Tensor,
+                                 w: ModernBertWeights,
+                                 num_layers: Optional[int] = None) -> torch.Tensor:
+    """The reference's flat vLLM call (models/modernbert/modernbert_encoder.py:430-480:
+    input_ids and position_ids of the packed stream): sequence boundaries come
+    from the position resets on the device (varlen_from_positions) instead of
+    [T, T] masks."""
+    cu, max_len = varlen_from_positions(position_ids)
+    return modernbert_forward(input_ids.reshape(-1), cu, max_len, w, num_layers)

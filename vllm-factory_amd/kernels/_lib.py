@@ -51,6 +51,8 @@ _SIGNATURES = {
                             _P, _vp],
     "vfk_varlen_attn_workspace_bytes": [_i32, _i64, _i32, _i32],
     "vfk_rope_table": [_f32, _i32, _vp, _vp],
+    "vfk_varlen_meta": [_vp, _i32, _i64, _vp, _vp, _vp, _i64, _vp],
+    "vfk_varlen_meta_workspace_bytes": [_i64],
     "vfk_rope_fwd": [_P, _P, _P, _P, _vp],
     "vfk_layernorm_fwd": [_P, _P, _P, _P, _f32, _P, _P, _vp],
     "vfk_rmsnorm_fwd": [_P, _P, _P, _f32, _P, _P, _vp],
@@ -59,7 +61,8 @@ _SIGNATURES = {
     "vfk_residual_add": [_P, _P, _P, _vp],
 }
 
-_RESTYPES = {"vfk_varlen_attn_workspace_bytes": ctypes.c_int64}
+_RESTYPES = {"vfk_varlen_attn_workspace_bytes": ctypes.c_int64,
+             "vfk_varlen_meta_workspace_bytes": ctypes.c_int64}
 
 _lib: Optional[ctypes.CDLL] = None
 
