@@ -257,7 +257,18 @@ def epilogue_bench(torch, args, c2):
     gate = torch.randn(32 * 768, 2816, generator=g).bfloat16().to(dev)
     up = torch.randn(32 * 768, 2816, generator=g).bfloat16().to(dev)
     bench("gated_gelu", lambda: ffg(gate, up, "gelu_new"), 3 * gate.numel() * 2)
-    del c4
+    del c4, gate, up
+    # flat <-> padded rows of the DeBERTa-v3-large GLiNER flat call at config 3
+    # sizes: 32 sequences U{256..512} of 1024 bf16 hidden values
+    from kernels.packing import pad_packed, unpad_packed
+    hid, lens3 = workloads.config3_hidden(32)
+    cu3 = workloads.cu_from_lengths(lens3.long()).to(dev)
+    T3, L3 = int(lens3.sum()), int(lens3.max())
+    flat = torch.cat([hid[b, :int(n)] for b, n in enumerate(lens3)]).bfloat16().to(dev)
+    padded, _ = pad_packed(flat, cu3, 32, L3)
+    row = 1024 * 2
+    bench("pad_rows", lambda: pad_packed(flat, cu3, 32, L3), (T3 + 32 * L3) * row)
+    bench("unpad_rows", lambda: unpad_packed(padded, cu3, T3), 2 * T3 * row)
     return res
 
 

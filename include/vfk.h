@@ -158,11 +158,14 @@ int64_t vfk_varlen_attn_workspace_bytes(int32_t dtype, int64_t total_tokens,
 
 /* Packed-sequence metadata from vLLM's flat position ids, on the device
  * (no counterpart kernel in the reference: it replaces the boundary detection
- * and cumsum of models/modernbert/modernbert_encoder.py:491-516
- * (ModernBertModel._build_seq_block_mask), whose [T, T] masks the varlen
- * attention does not need).
- *   positions: device int32 or int64 [total_tokens] (pos_dtype_bytes 4 or 8);
- *     a sequence starts at token 0 and at every i with pos[i] <= pos[i-1]
+ * of models/modernbert/modernbert_encoder.py:491-516
+ * (ModernBertModel._build_seq_block_mask, whose [T, T] masks the varlen
+ * attention does not need) and the host-side split of
+ * plugins/deberta_gliner/model.py:166-170).
+ *   positions: device int32 or int64 [total_tokens] (pos_dtype_bytes 4 or 8)
+ *   rule: VFK_SEQ_RESET: a sequence starts at token 0 and at every i with
+ *     pos[i] <= pos[i-1] (ModernBERT); VFK_SEQ_ZERO: at token 0 and at every
+ *     i with pos[i] == 0 (the GLiNER plugins)
  *   cu_seqlens: device int32 [total_tokens + 1]; entries 0..num_seqs are
  *     written (start of each sequence, then total_tokens)
  *   meta: device int32 [4] = {num_seqs, max_seqlen, bad, total_tokens}; bad
@@ -173,12 +176,41 @@ int64_t vfk_varlen_attn_workspace_bytes(int32_t dtype, int64_t total_tokens,
  *   workspace: device memory of vfk_varlen_meta_workspace_bytes() bytes,
  *     4-byte aligned; calls that share it must not overlap.
  * Four small launches on `stream`; nothing is read back to the host. */
+#define VFK_SEQ_RESET 0
+#define VFK_SEQ_ZERO 1
 int vfk_varlen_meta(const void* positions, int32_t pos_dtype_bytes,
-                    int64_t total_tokens, int32_t* cu_seqlens, int32_t* meta,
-                    void* workspace, int64_t workspace_bytes, void* stream);
+                    int64_t total_tokens, int32_t rule, int32_t* cu_seqlens,
+                    int32_t* meta, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 
 /* Workspace size of vfk_varlen_meta: 4 bytes per 1024 tokens. */
 int64_t vfk_varlen_meta_workspace_bytes(int64_t total_tokens);
+
+/* Flat rows -> padded batch. Replaces the per-row copy loop of
+ * plugins/deberta_gliner/model.py:171-191 (batched_ids[row, :length] =
+ * input_ids[start:end] with the rest pad_id).
+ *   src: device [T, row_bytes] (rows contiguous); dst: device
+ *     [num_seqs, max_len, row_bytes]; sequence b = src rows
+ *     cu_seqlens[b] .. cu_seqlens[b+1]-1 goes to dst[b, 0 .. len-1] and
+ *     dst[b, len .. max_len-1] is filled with the elem_bytes-wide value
+ *     fill_bits (little-endian low bytes)
+ *   cu_seqlens: device int32 [num_seqs + 1], non-decreasing, last = T
+ *   max_len: >= every sequence length (longer sequences are cut at max_len)
+ *   seq_lengths: device int32 [num_seqs] receiving the lengths, or NULL
+ * num_seqs <= 65535, max_len * row_bytes < 2^31; row_bytes and both
+ * addresses multiples of elem_bytes (1, 2, 4 or 8). */
+int vfk_pad_rows(const void* src, int64_t row_bytes, const int32_t* cu_seqlens,
+                 int32_t num_seqs, int32_t max_len, int32_t elem_bytes,
+                 uint64_t fill_bits, void* dst, int32_t* seq_lengths,
+                 void* stream);
+
+/* Padded batch -> flat rows, the inverse of vfk_pad_rows. Replaces
+ * torch.cat([encoded[row, :length] ...]) at plugins/deberta_gliner/
+ * model.py:197-200. src [num_seqs, max_len, row_bytes], dst [T, row_bytes];
+ * padded rows are not read. Same limits as vfk_pad_rows. */
+int vfk_unpad_rows(const void* src, int64_t row_bytes,
+                   const int32_t* cu_seqlens, int32_t num_seqs,
+                   int32_t max_len, void* dst, void* stream);
 
 /* RoPE cos/sin table of transformers' ModernBertRotaryEmbedding (default rope,
  * head_dim 64; the module the reference calls at

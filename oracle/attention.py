@@ -174,27 +174,3 @@ def varlen_attention(q, k, v, cu_seqlens, window: int = -1, rope_theta: float = 
         p = torch.nan_to_num(p, nan=0.0)  # rows with no visible key
         out[a:b] = torch.einsum("hij,jhd->ihd", p, vs)
     return out
-
-
-def seq_metadata(position_ids: torch.Tensor):
-    """Sequence boundaries of a packed stream from its flat position ids, as
-    models/modernbert/modernbert_encoder.py:505-513 (_build_seq_block_mask)
-    finds them: token 0 starts a sequence and so does every token with
-    pos[i] <= pos[i-1]; segment ids are the cumsum of those starts.
-
-    Returns (cu_seqlens int32 [n + 1], n, longest length, bad) where bad counts
-    the breaks in the run of positions: a sequence start whose position is not
-    0, or a token inside a sequence whose position is not its predecessor's + 1.
-    bad == 0 exactly when every position equals the token's offset in its
-    sequence (the position the varlen attention uses for RoPE)."""
-    pos = position_ids.reshape(-1).to(torch.int64)
-    T = pos.numel()
-    starts = torch.zeros(T, dtype=torch.bool)
-    starts[0] = True
-    if T > 1:
-        starts[1:] = pos[1:] <= pos[:-1]
-    idx = torch.nonzero(starts).flatten()
-    cu = torch.cat([idx, torch.tensor([T])]).to(torch.int32)
-    lens = cu[1:] - cu[:-1]
-    bad = int((starts & (pos != 0)).sum()) + int((~starts[1:] & (pos[1:] != pos[:-1] + 1)).sum())
-    return cu, int(idx.numel()), int(lens.max()), bad

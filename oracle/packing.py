@@ -1,0 +1,66 @@
+"""CPU oracle of the packed-stream plumbing — TEST INFRASTRUCTURE ONLY.
+
+Restates how the reference finds sequences in vLLM's flat position ids and
+re-pads them for a padded encoder:
+  * seq_metadata: models/modernbert/modernbert_encoder.py:505-513 (rule
+    "reset") and plugins/deberta_gliner/model.py:166-170 (rule "zero");
+  * gliner_batch / gliner_unbatch: plugins/deberta_gliner/model.py:171-200.
+Pinned in tests/test_oracle_packing.py by construction (positions built from
+known lengths), hand cases, a pairwise brute force and round trips.
+"""
+from __future__ import annotations
+
+import torch
+
+
+def seq_metadata(position_ids: torch.Tensor, rule: str = "reset"):
+    """Sequence boundaries of a packed stream from its flat position ids.
+
+    rule "reset" (modernbert_encoder.py:505-513, _build_seq_block_mask):
+    token 0 starts a sequence and so does every token with pos[i] <= pos[i-1];
+    segment ids are the cumsum of those starts. rule "zero"
+    (deberta_gliner/model.py:168, starts = (pos == 0).nonzero()): every token
+    at position 0 starts one; token 0 is taken as a start as well (the
+    reference's start list begins at the first zero).
+
+    Returns (cu_seqlens int32 [n + 1], n, longest length, bad) where bad counts
+    the breaks in the run of positions: a sequence start whose position is not
+    0, or a token inside a sequence whose position is not its predecessor's + 1.
+    bad == 0 exactly when every position equals the token's offset in its
+    sequence (the position the varlen attention uses for RoPE)."""
+    pos = position_ids.reshape(-1).to(torch.int64)
+    T = pos.numel()
+    starts = torch.zeros(T, dtype=torch.bool)
+    starts[0] = True
+    if T > 1:
+        starts[1:] = pos[1:] <= pos[:-1] if rule == "reset" else pos[1:] == 0
+    idx = torch.nonzero(starts).flatten()
+    cu = torch.cat([idx, torch.tensor([T])]).to(torch.int32)
+    lens = cu[1:] - cu[:-1]
+    bad = int((starts & (pos != 0)).sum()) + int((~starts[1:] & (pos[1:] != pos[:-1] + 1)).sum())
+    return cu, int(idx.numel()), int(lens.max()), bad
+
+
+def gliner_batch(input_ids: torch.Tensor, positions: torch.Tensor, pad_id: int = 0):
+    """The padded batch of plugins/deberta_gliner/model.py:166-191, written as
+    its per-row loop: starts at position 0, rows padded with pad_id (ids) and 0
+    (positions), attention mask 1 on valid tokens. Returns (batched_ids,
+    batched_positions, attention_mask, lengths)."""
+    pos = positions
+    starts = (pos == 0).nonzero(as_tuple=False).flatten().tolist()
+    ends = starts[1:] + [input_ids.shape[0]]
+    lengths = [e - s for s, e in zip(starts, ends)]
+    max_len = max(lengths)
+    ids = input_ids.new_full((len(lengths), max_len), pad_id)
+    bpos = pos.new_zeros((len(lengths), max_len))
+    mask = torch.zeros((len(lengths), max_len), dtype=torch.long)
+    for row, (s, e, n) in enumerate(zip(starts, ends, lengths)):
+        ids[row, :n] = input_ids[s:e]
+        bpos[row, :n] = pos[s:e]
+        mask[row, :n] = 1
+    return ids, bpos, mask, lengths
+
+
+def gliner_unbatch(encoded: torch.Tensor, lengths):
+    """torch.cat of the valid rows, plugins/deberta_gliner/model.py:197-200."""
+    return torch.cat([encoded[row, :n] for row, n in enumerate(lengths)], dim=0)

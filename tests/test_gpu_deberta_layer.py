@@ -47,3 +47,24 @@ def test_activation_gelu_matches_oracle():
         want = ref(x[:, 2:4098].float())
         # one bf16 rounding of the result (relative 2^-8 of |y| <= ~10)
         assert (got - want).abs().max().item() <= 2 ** -8 * want.abs().max().item(), name
+
+
+def test_deberta_flat_call_matches_padded_batch():
+    """The GLiNER plugins' flat call (plugins/deberta_gliner/model.py:166-202),
+    re-padded on the device, gives exactly the valid rows of the padded
+    forward: same kernels on the same padded batch."""
+    from encoders.deberta import deberta_forward, deberta_forward_flat, random_weights
+    hidden, lens = workloads.config3_hidden(3)
+    w = random_weights(num_layers=2, dtype=torch.bfloat16).to(torch.device("cuda:0"))
+    dev = torch.device("cuda:0")
+    xb = hidden.to(dev, torch.bfloat16)
+    L = int(lens.max())
+    xb = xb[:, :L].contiguous()     # the flat call pads to the longest sequence, with zeros
+    for b, n in enumerate(lens):
+        xb[b, int(n):] = 0
+    flat = torch.cat([xb[b, :int(n)] for b, n in enumerate(lens)])
+    pos = torch.cat([torch.arange(int(n)) for n in lens]).to(dev)
+    got = deberta_forward_flat(flat, pos, w)
+    want_b = deberta_forward(xb, lens.to(dev, torch.int32), w)
+    want = torch.cat([want_b[b, :int(n)] for b, n in enumerate(lens)])
+    assert torch.equal(got, want)

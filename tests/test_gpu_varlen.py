@@ -119,54 +119,6 @@ def test_varlen_large_scores(dev, window):
     assert_attn_close(got, want, f"large scores w={window}")
 
 
-# ------------------------------------------------ packed-sequence metadata (positions -> cu)
-def _meta_case(name):
-    g = torch.Generator().manual_seed(sum(map(ord, name)))
-    if name == "one_token":
-        return torch.tensor([0])
-    if name == "one_sequence":
-        return torch.arange(777)
-    if name == "all_length_one":          # 5000 resets: every block full of starts
-        return torch.zeros(5000, dtype=torch.int64)
-    if name == "pairs":
-        return torch.arange(2).repeat(3000)
-    if name == "config5":                 # 256 sequences of U{512..768}, 163 736 tokens
-        lens = workloads.config5().lengths
-        return torch.cat([torch.arange(int(n)) for n in lens])
-    if name == "many_blocks":             # > 1024 scan blocks: the scan's carry loop
-        lens = torch.randint(1, 3000, (900,), generator=g)
-        return torch.cat([torch.arange(int(n)) for n in lens])
-    if name == "no_restart":              # non-reset gaps and a non-zero first position
-        return torch.tensor([3, 4, 5, 9, 10, 0, 1, 1, 2, 7] * 300)
-    if name == "random":
-        return torch.randint(0, 40, (20000,), generator=g)
-    raise KeyError(name)
-
-
-@pytest.mark.parametrize("pos_dtype", [torch.int64, torch.int32])
-@pytest.mark.parametrize("name", ["one_token", "one_sequence", "all_length_one", "pairs",
-                                  "config5", "many_blocks", "no_restart", "random"])
-def test_seq_metadata_matches_oracle(dev, name, pos_dtype):
-    """Bit-exact cu_seqlens, count, longest length and off-offset count."""
-    from kernels.varlen_attention import seq_metadata
-    pos = _meta_case(name).to(pos_dtype)
-    cu, n, mx, bad = oa.seq_metadata(pos)
-    print(f"seq_metadata case {name} T={pos.numel()} {pos_dtype}", flush=True)
-    got_cu, meta = seq_metadata(pos.to(dev)[None])   # the reference's [1, T] layout
-    meta = meta.cpu().tolist()
-    assert meta == [n, mx, bad, pos.numel()], (meta, [n, mx, bad])
-    assert torch.equal(got_cu[:n + 1].cpu(), cu)
-
-
-def test_seq_metadata_repeat_calls_reset_counters(dev):
-    """The maximum and the off-offset count start from zero on every call."""
-    from kernels.varlen_attention import seq_metadata
-    _, meta1 = seq_metadata(_meta_case("no_restart").to(dev))
-    _, meta2 = seq_metadata(torch.arange(10, device=dev))
-    assert meta1.cpu().tolist()[2] > 0
-    assert meta2.cpu().tolist() == [1, 10, 0, 10]
-
-
 def test_varlen_from_positions_drives_attention(dev):
     """Attention on cu_seqlens derived from position ids on the device equals
     the oracle on the lengths the positions were built from."""

@@ -32,7 +32,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     from kernels import _lib
-    assert _lib.load().vfk_abi_version() == 3
+    assert _lib.load().vfk_abi_version() == 4
 
 
 def _host_t5(rel, bidirectional, nb, md):
@@ -102,23 +102,43 @@ def test_varlen_workspace_bytes():
     assert lib.vfk_varlen_attn_workspace_bytes(_lib.F32, 40265, 12, 1) == 0
 
 
-def test_varlen_meta_workspace_and_argument_checks():
+def test_packing_argument_checks():
     """Rejected before any HIP call, so these run without a GPU."""
     from kernels import _lib
-    from kernels.varlen_attention import seq_metadata
+    from kernels.packing import pad_packed, seq_metadata
     lib = _lib.load()
     assert lib.vfk_varlen_meta_workspace_bytes(1) == 4
     assert lib.vfk_varlen_meta_workspace_bytes(1024) == 4
     assert lib.vfk_varlen_meta_workspace_bytes(163736) == 160 * 4
     assert lib.vfk_varlen_meta_workspace_bytes(0) == 0
+    meta = lambda *a: _lib.call("vfk_varlen_meta", *a)
     with pytest.raises(ValueError, match="NULL"):
-        _lib.call("vfk_varlen_meta", None, 8, 10, None, None, None, 0, None)
+        meta(None, 8, 10, 0, None, None, None, 0, None)
     fake = 1 << 20  # never dereferenced: every case below fails its host checks
     with pytest.raises(ValueError, match="int32 or int64"):
-        _lib.call("vfk_varlen_meta", fake, 2, 10, fake, fake, fake, 4, None)
+        meta(fake, 2, 10, 0, fake, fake, fake, 4, None)
+    with pytest.raises(ValueError, match="rule"):
+        meta(fake, 8, 10, 2, fake, fake, fake, 4, None)
     with pytest.raises(ValueError, match="total_tokens"):
-        _lib.call("vfk_varlen_meta", fake, 8, 0, fake, fake, fake, 4, None)
+        meta(fake, 8, 0, 0, fake, fake, fake, 4, None)
     with pytest.raises(ValueError, match="workspace"):
-        _lib.call("vfk_varlen_meta", fake, 8, 5000, fake, fake, fake, 16, None)
+        meta(fake, 8, 5000, 1, fake, fake, fake, 16, None)
+    pad = lambda *a: _lib.call("vfk_pad_rows", *a)
+    with pytest.raises(ValueError, match="NULL"):
+        pad(None, 16, fake, 2, 8, 2, 0, fake, None, None)
+    with pytest.raises(ValueError, match="num_seqs"):
+        pad(fake, 16, fake, 70000, 8, 2, 0, fake, None, None)
+    with pytest.raises(ValueError, match="2\\^31"):
+        pad(fake, 1 << 20, fake, 2, 4096, 2, 0, fake, None, None)
+    with pytest.raises(ValueError, match="elem_bytes"):
+        pad(fake, 6, fake, 2, 8, 4, 0, fake, None, None)
+    with pytest.raises(ValueError, match="elem_bytes must be"):
+        pad(fake, 16, fake, 2, 8, 3, 0, fake, None, None)
+    with pytest.raises(ValueError, match="max_len"):
+        _lib.call("vfk_unpad_rows", fake, 16, fake, 2, 0, fake, None)
     with pytest.raises(RuntimeError, match="GPU only"):
         seq_metadata(torch.arange(5))
+    with pytest.raises(ValueError, match="rule"):
+        seq_metadata(torch.arange(5), "other")
+    with pytest.raises(RuntimeError, match="GPU only"):
+        pad_packed(torch.arange(5), torch.tensor([0, 5]), 1, 5)

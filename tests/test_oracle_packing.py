@@ -1,0 +1,143 @@
+"""Pins the oracle's packed-stream plumbing (oracle/packing.py): positions
+built from known lengths, hand cases, a pairwise brute force of the segment
+rule, the reference's dense-mask formulation of ModernBERT attention, and the
+GLiNER re-padding loop's round trip."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as oa
+from oracle import packing as op
+
+D64 = torch.float64
+
+
+def _r(*shape, seed=0):
+    return torch.randn(*shape, generator=torch.Generator().manual_seed(seed), dtype=D64)
+
+
+# ------------------------------------------------------- packed-sequence metadata
+def _positions(lens):
+    return torch.cat([torch.arange(n) for n in lens])
+
+
+@pytest.mark.parametrize("lens", [[1], [5], [1, 1, 1], [3, 1, 4, 1, 5], [700, 300, 129, 64],
+                                  [2] * 50])
+def test_seq_metadata_recovers_lengths(lens):
+    """Positions built from known lengths give those lengths back (a '<' for
+    '<=' merges the runs of length 1; an off-by-one shifts every start)."""
+    cu, n, mx, bad = op.seq_metadata(_positions(lens))
+    assert cu.tolist() == [0] + torch.tensor(lens).cumsum(0).tolist()
+    assert (n, mx, bad) == (len(lens), max(lens), 0)
+
+
+@pytest.mark.parametrize("pos, cu, bad", [
+    ([0, 1, 2, 5, 6], [0, 5], 1),        # no reset: one sequence, one gap
+    ([0, 1, 2, 1, 2], [0, 3, 5], 1),     # reset to 1: a sequence that does not start at 0
+    ([3, 4, 0, 0, 1], [0, 2, 3, 5], 1),  # first sequence starts at 3
+    ([0, 0, 0], [0, 1, 2, 3], 0),        # equal positions are resets
+    ([7], [0, 1], 1),
+    ([3, 4, 5, 9, 10, 0, 1, 1, 2, 7], [0, 5, 7, 10], 4),
+])
+def test_seq_metadata_hand_cases(pos, cu, bad):
+    got_cu, n, mx, got_bad = op.seq_metadata(torch.tensor(pos))
+    assert got_cu.tolist() == cu and got_bad == bad and n == len(cu) - 1
+    assert mx == max(b - a for a, b in zip(cu[:-1], cu[1:]))
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_seq_metadata_bad_is_zero_iff_positions_are_offsets(seed):
+    """bad == 0 exactly when each token's position is its index minus the
+    start of its sequence (checked on random streams, some built valid)."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1, 9, (40,), generator=g).tolist()
+    pos = _positions(lens)
+    if seed % 2:
+        i = int(torch.randint(0, pos.numel(), (1,), generator=g))
+        pos[i] += int(torch.randint(1, 3, (1,), generator=g))
+    cu, _, _, bad = op.seq_metadata(pos)
+    offset = torch.cat([torch.arange(int(b - a)) for a, b in zip(cu[:-1], cu[1:])])
+    assert (bad == 0) == bool(torch.equal(pos, offset)), (seed, bad)
+    assert (bad == 0) == (seed % 2 == 0)
+
+
+def test_seq_metadata_pairwise_brute_force():
+    """Tokens i < j share a sequence iff no reset lies in (i, j]: the
+    reference's segment-id equality written as a pairwise loop."""
+    g = torch.Generator().manual_seed(3)
+    pos = torch.randint(0, 6, (60,), generator=g)
+    cu, _, _, _ = op.seq_metadata(pos)
+    seg = torch.zeros(60, dtype=torch.int64)
+    for s in range(len(cu) - 1):
+        seg[cu[s]:cu[s + 1]] = s
+    for i in range(60):
+        for j in range(i, 60):
+            same = all(pos[t] > pos[t - 1] for t in range(i + 1, j + 1))
+            assert (seg[i] == seg[j]) == same, (i, j)
+
+
+def test_seq_metadata_drives_varlen_like_dense_masks():
+    """The reference's own formulation at modernbert_encoder.py:236-255 and
+    :491-550 (RoPE by position id, one SDPA over the whole stream with the
+    block-diagonal and sliding-window masks) equals the per-sequence varlen
+    oracle run on the cu_seqlens the metadata derives."""
+    lens, w, theta = [9, 1, 23, 14], 4, 10000.0
+    pos = _positions(lens)
+    T = pos.numel()
+    q, k, v = _r(T, 2, 64, seed=40), _r(T, 2, 64, seed=41), _r(T, 2, 64, seed=42)
+    cu, _, _, _ = op.seq_metadata(pos)
+    starts = torch.zeros(T, dtype=torch.bool)
+    starts[0] = True
+    starts[1:] = pos[1:] <= pos[:-1]
+    seg = starts.cumsum(0)
+    cos, sin = oa.rope_cos_sin(pos, theta)
+    qr, kr = oa.apply_rope(q, cos.to(D64), sin.to(D64)), oa.apply_rope(k, cos.to(D64), sin.to(D64))
+    for window in (-1, w):
+        vis = seg[:, None] == seg[None, :]
+        if window >= 0:
+            idx = torch.arange(T)
+            vis &= (idx[:, None] - idx[None, :]).abs() <= window
+        want = F.scaled_dot_product_attention(qr.transpose(0, 1), kr.transpose(0, 1),
+                                              v.transpose(0, 1), attn_mask=vis,
+                                              scale=0.125).transpose(0, 1)
+        got = oa.varlen_attention(q, k, v, cu, window, theta, None, 0.125, dtype=D64)
+        torch.testing.assert_close(got, want)
+
+
+# ------------------------------------------------------- rule "zero" (GLiNER plugins)
+@pytest.mark.parametrize("pos, reset_cu, zero_cu", [
+    ([0, 1, 2, 0, 1], [0, 3, 5], [0, 3, 5]),            # well-formed: the rules agree
+    ([0, 1, 1, 2, 0], [0, 2, 4, 5], [0, 4, 5]),         # a repeat resets only under "reset"
+    ([0, 5, 3, 4], [0, 2, 4], [0, 4]),                  # a decrease resets only under "reset"
+    ([0, 0, 0], [0, 1, 2, 3], [0, 1, 2, 3]),
+])
+def test_seq_metadata_rules(pos, reset_cu, zero_cu):
+    assert op.seq_metadata(torch.tensor(pos), "reset")[0].tolist() == reset_cu
+    assert op.seq_metadata(torch.tensor(pos), "zero")[0].tolist() == zero_cu
+
+
+@pytest.mark.parametrize("lens", [[1], [4, 1, 7], [300, 2, 129], [1] * 20])
+def test_gliner_batch_matches_known_lengths(lens):
+    """The loop restatement puts sequence b's ids in row b, pad_id after it,
+    and its lengths agree with the metadata's cu_seqlens under rule "zero"."""
+    g = torch.Generator().manual_seed(len(lens))
+    pos = torch.cat([torch.arange(n) for n in lens])
+    ids = torch.randint(1, 1000, (pos.numel(),), generator=g)
+    bids, bpos, mask, got_lens = op.gliner_batch(ids, pos, pad_id=-7)
+    assert got_lens == lens
+    cu, n, mx, bad = op.seq_metadata(pos, "zero")
+    assert (n, mx, bad) == (len(lens), max(lens), 0)
+    assert cu.tolist() == [0] + torch.tensor(lens).cumsum(0).tolist()
+    for b, L in enumerate(lens):
+        a = int(cu[b])
+        assert torch.equal(bids[b, :L], ids[a:a + L])
+        assert bool((bids[b, L:] == -7).all()) and bool((bpos[b, L:] == 0).all())
+        assert torch.equal(bpos[b, :L], torch.arange(L))
+        assert mask[b].tolist() == [1] * L + [0] * (mx - L)
+    # round trip: the valid rows, concatenated, are the flat stream again
+    assert torch.equal(op.gliner_unbatch(bids, got_lens), ids)
+    h = torch.randn(pos.numel(), 3, generator=g)
+    hb = torch.zeros(len(lens), mx, 3)
+    for b, L in enumerate(lens):
+        hb[b, :L] = h[int(cu[b]):int(cu[b]) + L]
+    assert torch.equal(op.gliner_unbatch(hb, got_lens), h)

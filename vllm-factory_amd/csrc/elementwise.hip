@@ -647,26 +647,6 @@ struct RopeArgs {
   int64_t B, S, H; int D;
 };
 
-// One thread per (row b*S + s, 128-bit chunk pair c) covering every head of
-// the row: the row's cos/sin chunks are loaded once for all heads, the loads
-// of 4 heads are issued before any of them is used, and (row, c) and (b, s)
-// come from multiply-high divisions by host-computed magic numbers.
-struct Magic {
-  uint32_t d, m;
-  int l;
-};
-static Magic magic_for(uint32_t d) {
-  Magic r;
-  r.d = d;
-  r.l = 0;
-  while ((1ull << r.l) < d) ++r.l;
-  r.m = (uint32_t)((((1ull << 32) * ((1ull << r.l) - d)) / d) + 1);
-  return r;
-}
-__device__ inline uint32_t magic_div(uint32_t x, const Magic& g) {
-  return (uint32_t)(((uint64_t)__umulhi(x, g.m) + x) >> g.l);
-}
-
 // Thread item t = ((b * S + s) * H + h) * cpr + c (chunk pair c of head h of
 // row (b, s)), consecutive items covering consecutive 16-byte chunks of the
 // row; kRopeU items per thread and pass, all loads issued before any use.

@@ -1,0 +1,362 @@
+// Packed-stream plumbing on the device: sequence metadata from vLLM's flat
+// position ids, and the flat <-> padded row copies around padded encoders.
+//
+// Metadata replaces the reference's host/dense constructions for packed
+// batches: ModernBERT's block mask (models/modernbert/modernbert_encoder.py:
+// 491-516, _build_seq_block_mask: a sequence starts at token 0 and wherever
+// pos[i] <= pos[i-1]) and the GLiNER plugins' split at zero positions
+// (plugins/deberta_gliner/model.py:166-170: starts = (pos == 0).nonzero()).
+// The starts become cu_seqlens directly, in three passes over 1024-token
+// blocks:
+//   1. count the starts of each block,
+//   2. one workgroup scans the block counts (exclusive) and writes the
+//      totals,
+//   3. each block writes the indices of its starts at its offset and counts
+//      breaks in the run of positions; a fourth small pass takes the longest
+//      sequence from cu_seqlens.
+// meta[0] = number of sequences, meta[1] = longest sequence, meta[2] = breaks
+// in the run of positions (a start whose position is not 0, or a token whose
+// position is not its predecessor's + 1; 0 exactly when every position equals
+// index - sequence start), meta[3] = T.
+//
+// Pad / unpad replace the per-row Python loop of plugins/deberta_gliner/
+// model.py:171-202 (batched_ids[row, :length] = input_ids[start:end], then
+// torch.cat of encoded[row, :length]). Sequence b's rows are contiguous in
+// both layouts, so workgroup row b copies len_b rows' bytes as one run and
+// fills the rest of its padded block; no per-element index arithmetic.
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "launch_util.h"
+#include "vfk_common.h"
+
+namespace vfk {
+
+constexpr int kMetaBlock = 1024;  // tokens per block (256 threads x 4)
+
+// RULE 0 (VFK_SEQ_RESET): start where the position does not increase;
+// RULE 1 (VFK_SEQ_ZERO): start where the position is 0. Token 0 always starts.
+template <int RULE, typename P>
+__device__ inline bool seq_start(const P* pos, int64_t i) {
+  if (i == 0) return true;
+  return RULE == 0 ? pos[i] <= pos[i - 1] : pos[i] == 0;
+}
+
+template <int RULE, typename P>
+__global__ __launch_bounds__(256) void meta_count_kernel(const P* __restrict__ pos, int64_t T,
+                                                         int32_t* __restrict__ counts) {
+  __shared__ int red[4];
+  const int64_t base = (int64_t)blockIdx.x * kMetaBlock;
+  int c = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t i = base + u * 256 + threadIdx.x;
+    if (i < T && seq_start<RULE>(pos, i)) ++c;
+  }
+  for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) counts[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+// One workgroup: offsets[b] = counts[0] + ... + counts[b-1] (in place);
+// meta[0] = total starts, meta[1] = meta[2] = 0, meta[3] = T; cu[total] = T.
+__global__ __launch_bounds__(1024) void meta_scan_kernel(int32_t* __restrict__ counts, int nblk,
+                                                         int64_t T, int32_t* __restrict__ cu,
+                                                         int32_t* __restrict__ meta) {
+  __shared__ int part[1024];
+  __shared__ int carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int b0 = 0; b0 < nblk; b0 += 1024) {
+    const int b = b0 + threadIdx.x;
+    const int v = b < nblk ? counts[b] : 0;
+    part[threadIdx.x] = v;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {  // inclusive Hillis-Steele scan
+      const int add = threadIdx.x >= o ? part[threadIdx.x - o] : 0;
+      __syncthreads();
+      part[threadIdx.x] += add;
+      __syncthreads();
+    }
+    const int c0 = carry;
+    if (b < nblk) counts[b] = c0 + part[threadIdx.x] - v;
+    __syncthreads();
+    if (threadIdx.x == 1023) carry = c0 + part[1023];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    meta[0] = carry;
+    meta[1] = 0;
+    meta[2] = 0;
+    meta[3] = (int32_t)T;
+    cu[carry] = (int32_t)T;
+  }
+}
+
+template <int RULE, typename P>
+__global__ __launch_bounds__(256) void meta_write_kernel(const P* __restrict__ pos, int64_t T,
+                                                         const int32_t* __restrict__ offsets,
+                                                         int32_t* __restrict__ cu,
+                                                         int32_t* __restrict__ meta) {
+  __shared__ int red[4];
+  const int64_t base = (int64_t)blockIdx.x * kMetaBlock;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // rank of each start inside the block: 4 rounds of 256 tokens, each a
+  // workgroup-wide exclusive count built from wave ballots
+  int off = offsets[blockIdx.x];
+  int bad = 0;
+  for (int u = 0; u < 4; ++u) {
+    const int64_t i = base + u * 256 + threadIdx.x;
+    const bool st = i < T && seq_start<RULE>(pos, i);
+    if (i < T && !st && pos[i] != pos[i - 1] + 1) ++bad;
+    if (i < T && st && pos[i] != 0) ++bad;
+    const unsigned long long m = __builtin_amdgcn_ballot_w64(st);
+    const int before_in_wave = __builtin_popcountll(m & ((1ull << lane) - 1ull));
+    if (lane == 0) red[w] = __builtin_popcountll(m);
+    __syncthreads();
+    int before = before_in_wave;
+    for (int j = 0; j < w; ++j) before += red[j];
+    const int total = red[0] + red[1] + red[2] + red[3];
+    if (st) cu[off + before] = (int32_t)i;
+    off += total;
+    __syncthreads();
+  }
+  for (int o = 32; o > 0; o >>= 1) bad += __shfl_xor(bad, o, 64);
+  if (lane == 0 && bad) atomicAdd(&meta[2], bad);
+}
+
+// Longest sequence: one pass over cu once it is complete.
+__global__ __launch_bounds__(256) void meta_maxlen_kernel(const int32_t* __restrict__ cu,
+                                                          int32_t* __restrict__ meta) {
+  const int ns = meta[0];
+  int mx = 0;
+  for (int s = blockIdx.x * 256 + threadIdx.x; s < ns; s += gridDim.x * 256)
+    mx = max(mx, cu[s + 1] - cu[s]);
+  for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o, 64));
+  if ((threadIdx.x & 63) == 0 && mx > 0) atomicMax(&meta[1], mx);
+}
+
+// ---------------------------------------------------------------------------
+// flat [T, row] <-> padded [B, L, row]
+// ---------------------------------------------------------------------------
+constexpr int kPadU = 4;  // units per thread and pass, issued loads-first
+
+// Workgroup row b = sequence b. Units t < min(len_b, L) * upr of the padded
+// block come from flat row cu[b] + t / upr; the rest get `fill`. The main loop
+// takes kPadU units per thread with every load and store unconditional (loads
+// at indices clamped into the sequence, so the compiler cannot sink them into
+// predicated stores and serialise them); one predicated pass takes the tail.
+template <typename U>
+__global__ __launch_bounds__(256) void pad_rows_kernel(const U* __restrict__ src,
+                                                       U* __restrict__ dst,
+                                                       const int32_t* __restrict__ cu,
+                                                       int32_t* __restrict__ seq_lengths,
+                                                       uint32_t L, uint32_t upr, U fill) {
+  const int b = blockIdx.y;
+  const int start = cu[b];
+  const int len = cu[b + 1] - start;
+  if (seq_lengths && blockIdx.x == 0 && threadIdx.x == 0) seq_lengths[b] = len;
+  const uint32_t n = L * upr;
+  const uint32_t valid = (uint32_t)min(max(len, 0), (int)L) * upr;
+  U* d = dst + (size_t)b * n;
+  const uint32_t step = gridDim.x * 256 * kPadU;
+  uint32_t t0 = blockIdx.x * 256 * kPadU + threadIdx.x;
+  if (valid == 0) {  // empty sequence: its flat rows may not exist, fill only
+    for (uint32_t t = blockIdx.x * 256 + threadIdx.x; t < n; t += gridDim.x * 256) d[t] = fill;
+    return;
+  }
+  const U* s = src + (size_t)start * upr;
+  const uint32_t last = valid - 1;
+  for (; t0 + (kPadU - 1) * 256 < n; t0 += step) {
+    U v[kPadU];
+#pragma unroll
+    for (int u = 0; u < kPadU; ++u) {
+      const uint32_t t = t0 + u * 256;
+      const U x = s[min(t, last)];
+      v[u] = t < valid ? x : fill;
+    }
+#pragma unroll
+    for (int u = 0; u < kPadU; ++u) d[t0 + u * 256] = v[u];
+  }
+  if (t0 < n) {
+#pragma unroll
+    for (int u = 0; u < kPadU; ++u) {
+      const uint32_t t = t0 + u * 256;
+      const U x = s[min(t, last)];
+      if (t < n) d[t] = t < valid ? x : fill;
+    }
+  }
+}
+
+// Workgroup row b = sequence b: its first min(len_b, L) padded rows go to
+// flat rows cu[b]...; workgroups past the end of a short sequence exit. Same
+// main-loop / tail split as pad_rows_kernel.
+template <typename U>
+__global__ __launch_bounds__(256) void unpad_rows_kernel(const U* __restrict__ src,
+                                                         U* __restrict__ dst,
+                                                         const int32_t* __restrict__ cu,
+                                                         uint32_t L, uint32_t upr) {
+  const int b = blockIdx.y;
+  const int start = cu[b];
+  const int len = cu[b + 1] - start;
+  const uint32_t valid = (uint32_t)min(max(len, 0), (int)L) * upr;
+  const U* s = src + (size_t)b * L * upr;
+  U* d = dst + (size_t)start * upr;
+  const uint32_t step = gridDim.x * 256 * kPadU;
+  uint32_t t0 = blockIdx.x * 256 * kPadU + threadIdx.x;
+  for (; t0 + (kPadU - 1) * 256 < valid; t0 += step) {
+    U v[kPadU];
+#pragma unroll
+    for (int u = 0; u < kPadU; ++u) v[u] = s[t0 + u * 256];
+#pragma unroll
+    for (int u = 0; u < kPadU; ++u) d[t0 + u * 256] = v[u];
+  }
+  if (t0 < valid) {
+#pragma unroll
+    for (int u = 0; u < kPadU; ++u) {
+      const uint32_t t = t0 + u * 256;
+      const U x = s[min(t, valid - 1)];
+      if (t < valid) d[t] = x;
+    }
+  }
+}
+
+}  // namespace vfk
+
+using namespace vfk;
+
+extern "C" int64_t vfk_varlen_meta_workspace_bytes(int64_t total_tokens) {
+  if (total_tokens <= 0) return 0;
+  return ((total_tokens + kMetaBlock - 1) / kMetaBlock) * (int64_t)sizeof(int32_t);
+}
+
+template <int RULE, typename P>
+static void launch_meta(const P* p, int64_t T, int nblk, int32_t* counts, int32_t* cu,
+                        int32_t* meta, hipStream_t st) {
+  hipLaunchKernelGGL((meta_count_kernel<RULE, P>), dim3(nblk), dim3(256), 0, st, p, T, counts);
+  hipLaunchKernelGGL(meta_scan_kernel, dim3(1), dim3(1024), 0, st, counts, nblk, T, cu, meta);
+  hipLaunchKernelGGL((meta_write_kernel<RULE, P>), dim3(nblk), dim3(256), 0, st, p, T, counts, cu,
+                     meta);
+  hipLaunchKernelGGL(meta_maxlen_kernel, dim3(std::min(nblk, 1024)), dim3(256), 0, st, cu, meta);
+}
+
+extern "C" int vfk_varlen_meta(const void* positions, int32_t pos_dtype_bytes, int64_t total_tokens,
+                               int32_t rule, int32_t* cu_seqlens, int32_t* meta, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  if (!positions || !cu_seqlens || !meta)
+    return set_error(VFK_ERR_INVALID, "vfk_varlen_meta: NULL pointer");
+  if (pos_dtype_bytes != 4 && pos_dtype_bytes != 8)
+    return set_error(VFK_ERR_INVALID, "vfk_varlen_meta: positions must be int32 or int64");
+  if (rule != VFK_SEQ_RESET && rule != VFK_SEQ_ZERO)
+    return set_error(VFK_ERR_INVALID, "vfk_varlen_meta: unknown boundary rule %d", rule);
+  if (total_tokens <= 0 || total_tokens >= (1ll << 31) - 1)
+    return set_error(VFK_ERR_INVALID, "vfk_varlen_meta: total_tokens must be in [1, 2^31 - 2]");
+  const int64_t need = vfk_varlen_meta_workspace_bytes(total_tokens);
+  if (!workspace || workspace_bytes < need)
+    return set_error(VFK_ERR_INVALID, "vfk_varlen_meta: needs a workspace of %lld bytes",
+                     (long long)need);
+  const int nblk = ceil_div(total_tokens, kMetaBlock);
+  int32_t* counts = reinterpret_cast<int32_t*>(workspace);
+  hipStream_t st = (hipStream_t)stream;
+  const bool wide = pos_dtype_bytes == 8;
+  const int64_t T = total_tokens;
+  if (rule == VFK_SEQ_RESET) {
+    if (wide) launch_meta<0>(static_cast<const int64_t*>(positions), T, nblk, counts, cu_seqlens, meta, st);
+    else launch_meta<0>(static_cast<const int32_t*>(positions), T, nblk, counts, cu_seqlens, meta, st);
+  } else {
+    if (wide) launch_meta<1>(static_cast<const int64_t*>(positions), T, nblk, counts, cu_seqlens, meta, st);
+    else launch_meta<1>(static_cast<const int32_t*>(positions), T, nblk, counts, cu_seqlens, meta, st);
+  }
+  return launch_status("vfk_varlen_meta");
+}
+
+// Copy unit: the widest of 16/8/4/2/1 bytes dividing the row size and both
+// base addresses.
+static int unit_bytes(int64_t row_bytes, const void* a, const void* b) {
+  const uintptr_t m = (uintptr_t)row_bytes | reinterpret_cast<uintptr_t>(a) |
+                      reinterpret_cast<uintptr_t>(b);
+  for (int u = 16; u > 1; u >>= 1)
+    if ((m & (uintptr_t)(u - 1)) == 0) return u;
+  return 1;
+}
+
+static int check_rows(const char* name, const void* src, const void* dst, const int32_t* cu,
+                      int64_t row_bytes, int32_t num_seqs, int32_t max_len) {
+  if (!src || !dst || !cu) return set_error(VFK_ERR_INVALID, "%s: NULL pointer", name);
+  if (row_bytes <= 0) return set_error(VFK_ERR_INVALID, "%s: row_bytes must be positive", name);
+  if (num_seqs <= 0 || num_seqs > 65535)
+    return set_error(VFK_ERR_INVALID, "%s: num_seqs must be in [1, 65535]", name);
+  if (max_len <= 0) return set_error(VFK_ERR_INVALID, "%s: max_len must be positive", name);
+  // unit indices within one padded block, plus a grid stride, stay in 32 bits
+  if ((int64_t)max_len * row_bytes >= (1ll << 31))
+    return set_error(VFK_ERR_INVALID, "%s: max_len * row_bytes must be below 2^31", name);
+  return VFK_OK;
+}
+
+template <typename U>
+static void fill_unit(U& u, uint64_t bits, int elem_bytes) {
+  unsigned char* p = reinterpret_cast<unsigned char*>(&u);
+  for (int i = 0; i < (int)sizeof(U); ++i) p[i] = (unsigned char)(bits >> (8 * (i % elem_bytes)));
+}
+
+template <typename U>
+static void launch_pad(const void* src, void* dst, const int32_t* cu, int32_t* lens, int B, int L,
+                       int64_t row_bytes, uint64_t fill_bits, int elem_bytes, hipStream_t st) {
+  U fill;
+  fill_unit(fill, fill_bits, elem_bytes);
+  const uint32_t upr = (uint32_t)(row_bytes / (int64_t)sizeof(U));
+  const int64_t n = (int64_t)L * upr;
+  const int gx = (int)std::min<int64_t>(ceil_div(n, 256 * kPadU), 1024);
+  hipLaunchKernelGGL(pad_rows_kernel<U>, dim3(gx, B), dim3(256), 0, st,
+                     static_cast<const U*>(src), static_cast<U*>(dst), cu, lens, (uint32_t)L, upr,
+                     fill);
+}
+
+template <typename U>
+static void launch_unpad(const void* src, void* dst, const int32_t* cu, int B, int L,
+                         int64_t row_bytes, hipStream_t st) {
+  const uint32_t upr = (uint32_t)(row_bytes / (int64_t)sizeof(U));
+  const int64_t n = (int64_t)L * upr;
+  const int gx = (int)std::min<int64_t>(ceil_div(n, 256 * kPadU), 1024);
+  hipLaunchKernelGGL(unpad_rows_kernel<U>, dim3(gx, B), dim3(256), 0, st,
+                     static_cast<const U*>(src), static_cast<U*>(dst), cu, (uint32_t)L, upr);
+}
+
+extern "C" int vfk_pad_rows(const void* src, int64_t row_bytes, const int32_t* cu_seqlens,
+                            int32_t num_seqs, int32_t max_len, int32_t elem_bytes,
+                            uint64_t fill_bits, void* dst, int32_t* seq_lengths, void* stream) {
+  const char* name = "vfk_pad_rows";
+  if (int rc = check_rows(name, src, dst, cu_seqlens, row_bytes, num_seqs, max_len)) return rc;
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8)
+    return set_error(VFK_ERR_INVALID, "%s: elem_bytes must be 1, 2, 4 or 8", name);
+  const int ub = unit_bytes(row_bytes, src, dst);
+  if (ub < elem_bytes)
+    return set_error(VFK_ERR_INVALID,
+                     "%s: row_bytes and both addresses must be multiples of elem_bytes", name);
+  hipStream_t st = (hipStream_t)stream;
+  switch (ub) {
+    case 16: launch_pad<u32x4_t>(src, dst, cu_seqlens, seq_lengths, num_seqs, max_len, row_bytes, fill_bits, elem_bytes, st); break;
+    case 8: launch_pad<u32x2_t>(src, dst, cu_seqlens, seq_lengths, num_seqs, max_len, row_bytes, fill_bits, elem_bytes, st); break;
+    case 4: launch_pad<uint32_t>(src, dst, cu_seqlens, seq_lengths, num_seqs, max_len, row_bytes, fill_bits, elem_bytes, st); break;
+    case 2: launch_pad<uint16_t>(src, dst, cu_seqlens, seq_lengths, num_seqs, max_len, row_bytes, fill_bits, elem_bytes, st); break;
+    default: launch_pad<uint8_t>(src, dst, cu_seqlens, seq_lengths, num_seqs, max_len, row_bytes, fill_bits, elem_bytes, st); break;
+  }
+  return launch_status(name);
+}
+
+extern "C" int vfk_unpad_rows(const void* src, int64_t row_bytes, const int32_t* cu_seqlens,
+                              int32_t num_seqs, int32_t max_len, void* dst, void* stream) {
+  const char* name = "vfk_unpad_rows";
+  if (int rc = check_rows(name, src, dst, cu_seqlens, row_bytes, num_seqs, max_len)) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  switch (unit_bytes(row_bytes, src, dst)) {
+    case 16: launch_unpad<u32x4_t>(src, dst, cu_seqlens, num_seqs, max_len, row_bytes, st); break;
+    case 8: launch_unpad<u32x2_t>(src, dst, cu_seqlens, num_seqs, max_len, row_bytes, st); break;
+    case 4: launch_unpad<uint32_t>(src, dst, cu_seqlens, num_seqs, max_len, row_bytes, st); break;
+    case 2: launch_unpad<uint16_t>(src, dst, cu_seqlens, num_seqs, max_len, row_bytes, st); break;
+    default: launch_unpad<uint8_t>(src, dst, cu_seqlens, num_seqs, max_len, row_bytes, st); break;
+  }
+  return launch_status(name);
+}

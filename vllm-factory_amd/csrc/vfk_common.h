@@ -134,5 +134,25 @@ __device__ inline int xcd_remap(int bid, int n) {
   return rem * (per + 1) + (xcd - rem) * per + slot;
 }
 
+// Division of a 32-bit index by a runtime divisor d >= 1 with a multiply-high
+// (round-up method of Granlund and Montgomery): l = ceil(log2 d),
+// m = floor(2^32 (2^l - d) / d) + 1, x / d = (umulhi(x, m) + x) >> l, exact
+// for every x < 2^32 (the sum is formed in 64 bits).
+struct Magic {
+  uint32_t d, m;
+  int l;
+};
+inline Magic magic_for(uint32_t d) {
+  Magic r;
+  r.d = d;
+  r.l = 0;
+  while ((1ull << r.l) < d) ++r.l;
+  r.m = (uint32_t)((((1ull << 32) * ((1ull << r.l) - d)) / d) + 1);
+  return r;
+}
+__device__ inline uint32_t magic_div(uint32_t x, const Magic& g) {
+  return (uint32_t)(((uint64_t)__umulhi(x, g.m) + x) >> g.l);
+}
+
 }  // namespace vfk
 

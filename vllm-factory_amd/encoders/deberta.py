@@ -31,6 +31,7 @@ import torch.nn.functional as F
 from kernels.activation import activation
 from kernels.flash_deberta_attention import flash_deberta_attention_fused
 from kernels.fused_layernorm import fused_add_layernorm, fused_layernorm
+from kernels.packing import pad_packed, read_metadata, seq_metadata, unpad_packed
 
 
 @dataclass
@@ -136,3 +137,16 @@ def deberta_forward(x: torch.Tensor, seq_lengths: torch.Tensor, w: DebertaWeight
     for i in range(n):
         x = deberta_layer_forward(x, seq_lengths, rel, w.layers[i], w)
     return x
+
+
+def deberta_forward_flat(x: torch.Tensor, positions: torch.Tensor, w: DebertaWeights,
+                         num_layers: Optional[int] = None) -> torch.Tensor:
+    """The GLiNER plugins' flat call (plugins/deberta_gliner/model.py:166-202):
+    embedding output x [T, hidden] of a packed stream whose sequences start at
+    position 0 -> last hidden state [T, hidden]. The re-padding and the
+    concatenation of valid rows run on the device (kernels.packing); the
+    number of sequences and the longest length are read back once."""
+    cu, meta = seq_metadata(positions, "zero")
+    cu, n, max_len, _ = read_metadata(cu, meta)
+    xb, lens = pad_packed(x, cu, n, max_len)
+    return unpad_packed(deberta_forward(xb, lens, w, num_layers), cu, x.shape[0])

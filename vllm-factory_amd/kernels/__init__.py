@@ -15,7 +15,7 @@ with `vllm-factory_amd/` on sys.path gets the HIP implementation:
     fused_dropout_residual   -> fused_dropout_residual
 
 plus ops with no reference kernel: varlen_attention.varlen_rope_attention
-(ModernBERT packed local/global attention) with varlen_attention.seq_metadata
-and varlen_from_positions (sequence boundaries from position resets, on the
-device), rms_norm.RMSNorm, and flash_deberta_attention.flash_deberta_attention_fused.
+(ModernBERT packed local/global attention), packing (sequence boundaries from
+flat position ids and flat <-> padded row copies, on the device),
+rms_norm.RMSNorm, and flash_deberta_attention.flash_deberta_attention_fused.
 """

@@ -18,6 +18,7 @@ LIB_PATH = os.path.normpath(os.path.join(_HERE, "..", "lib", "libvfk.so"))
 
 F32, BF16, F16 = 0, 1, 2
 OK, ERR_INVALID, ERR_UNSUPPORTED = 0, -1, -2
+SEQ_RESET, SEQ_ZERO = 0, 1
 ACT_GELU_ERF, ACT_GELU_TANH, ACT_SILU, ACT_RELU = 0, 1, 2, 3
 
 _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -51,7 +52,9 @@ _SIGNATURES = {
                             _P, _vp],
     "vfk_varlen_attn_workspace_bytes": [_i32, _i64, _i32, _i32],
     "vfk_rope_table": [_f32, _i32, _vp, _vp],
-    "vfk_varlen_meta": [_vp, _i32, _i64, _vp, _vp, _vp, _i64, _vp],
+    "vfk_varlen_meta": [_vp, _i32, _i64, _i32, _vp, _vp, _vp, _i64, _vp],
+    "vfk_pad_rows": [_vp, _i64, _vp, _i32, _i32, _i32, ctypes.c_uint64, _vp, _vp, _vp],
+    "vfk_unpad_rows": [_vp, _i64, _vp, _i32, _i32, _vp, _vp],
     "vfk_varlen_meta_workspace_bytes": [_i64],
     "vfk_rope_fwd": [_P, _P, _P, _P, _vp],
     "vfk_layernorm_fwd": [_P, _P, _P, _P, _f32, _P, _P, _vp],

@@ -25,6 +25,7 @@ from typing import Dict, Optional, Tuple
 import torch
 
 from . import _lib
+from .packing import seq_metadata, varlen_from_positions  # noqa: F401  (re-exported)
 
 _ROPE_TABLES: Dict[Tuple[float, int, torch.device], torch.Tensor] = {}
 
@@ -84,47 +85,3 @@ def varlen_rope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         _lib.ref(_lib.desc(out)),
     )
     return out
-
-
-def seq_metadata(position_ids: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Device-side packed-sequence metadata from vLLM's flat position ids.
-
-    Follows the boundary rule of models/modernbert/modernbert_encoder.py:491-516
-    (ModernBertModel._build_seq_block_mask): token 0 starts a sequence, and so
-    does every token whose position does not exceed its predecessor's.
-    position_ids: int32/int64 [T] or [1, T] on the device. Returns
-    (cu_seqlens int32 [T + 1], meta int32 [4]) on the device, nothing read
-    back: cu_seqlens[0..n] hold the n sequence starts and T, meta =
-    (n, longest sequence, breaks in the run of positions, T); the break count
-    (a start whose position is not 0, or a step other than +1) is 0 exactly
-    when every token's position is t - cu_seqlens[s]."""
-    dev = _lib.require_gpu(position_ids)
-    pos = position_ids.reshape(-1)
-    if pos.dtype not in (torch.int32, torch.int64):
-        raise ValueError("position_ids must be int32 or int64")
-    T = pos.numel()
-    if T == 0:
-        raise ValueError("position_ids is empty")
-    pos = pos.contiguous()
-    cu = torch.empty(T + 1, dtype=torch.int32, device=dev)
-    meta = torch.empty(4, dtype=torch.int32, device=dev)
-    ws_bytes = int(_lib.load().vfk_varlen_meta_workspace_bytes(T))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    _lib.on_device("vfk_varlen_meta", dev, pos.data_ptr(), pos.element_size(), T,
-                   cu.data_ptr(), meta.data_ptr(), ws.data_ptr(), ws_bytes)
-    return cu, meta
-
-
-def varlen_from_positions(position_ids: torch.Tensor,
-                          require_restart: bool = True) -> Tuple[torch.Tensor, int]:
-    """(cu_seqlens int32 [n + 1] on the device, max_seqlen) for
-    varlen_rope_attention, from the reference's position ids; one 16-byte read
-    back. require_restart: raise if some token's position is not its offset in
-    its sequence (the reference would rotate it by its own position id, the
-    varlen op by its offset)."""
-    cu, meta = seq_metadata(position_ids)
-    n, max_len, bad, _ = (int(x) for x in meta.cpu())
-    if require_restart and bad:
-        raise ValueError(f"position ids do not count up from 0 within their sequence "
-                         f"({bad} breaks)")
-    return cu[:n + 1], max_len
