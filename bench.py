@@ -346,6 +346,29 @@ def deberta_layer_config3(torch, args):
                 padded_tokens=int(x.shape[0] * x.shape[1]))
 
 
+def deberta_v1_layer_config3(torch, args):
+    """One DeBERTa v1 (deberta-base: hidden 768, 12 heads, GELU 3072, linear
+    relative positions, max_relative_positions 512) encoder layer on the
+    config-3 batch shape (B=32, L=512, lengths U{256..512}); tokens/s over
+    valid tokens."""
+    import workloads
+    from encoders.deberta import deberta_v1_layer_forward, random_weights_v1
+
+    dev = torch.device("cuda:0")
+    _, lens = workloads.config3_hidden()
+    g = torch.Generator().manual_seed(1013)
+    x = torch.randn(32, 512, 768, generator=g).to(dev, torch.bfloat16)
+    sl = lens.to(dev)
+    w = random_weights_v1(num_layers=1).to(dev)
+    fn = lambda: deberta_v1_layer_forward(x, sl, w.layers[0], w)
+    for _ in range(args.warmup):
+        fn()
+    ms = device_ms(torch, fn, args.steps)
+    tv = int(lens.sum())
+    return dict(ms_per_layer=ms, valid_tokens_per_s=tv / (ms * 1e-3), valid_tokens=tv,
+                padded_tokens=32 * 512)
+
+
 def cpu_baseline(torch, c2, min_seconds=10.0):
     """The oracle (CPU restatement of the reference's eager path, fp32) on the
     host cores: global + local attention over the config-2 sequences, cycling
@@ -415,6 +438,7 @@ def main():
                         ("epilogues", lambda: epilogue_bench(torch, args, c2)),
                         ("mt5_large_layer_config4", lambda: mt5_layer_config4(torch, args)),
                         ("deberta_v3_large_layer_config3", lambda: deberta_layer_config3(torch, args)),
+                        ("deberta_v1_base_layer_config3", lambda: deberta_v1_layer_config3(torch, args)),
                         ("modernbert_encoder_config5", lambda: encoder_config5(torch, args))):
             extra[key] = fn()
             _progress(key)

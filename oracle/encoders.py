@@ -29,10 +29,19 @@ beyond the sequence length hidden, those query rows zero), dense ->
 LayerNorm(. + x) (:494-510), GELU(erf) intermediate (:535-550), dense ->
 LayerNorm(. + attention_output) (:553-568).
 
+deberta_v1_layer follows the reference's DeBERTa v1 DebertaLayer
+(models/deberta/deberta_encoder.py:132-548, flash path :246-309): one in_proj
+without bias whose rows hold [q, k, v] per head, q_bias and v_bias added
+after it, att_span = min(L, max_relative_positions), the relative table
+rel_embeddings[max_rel - span : max_rel + span] projected by pos_proj (no
+bias, c2p) and pos_q_proj (bias, p2c), sm_scale 1/sqrt(3 d), linear relative
+positions; then the same post-LN blocks as v2 with DebertaLayerNorm (:71-92,
+eps inside the square root; identical to LayerNorm in fp32).
+
 Pinned by (tests/test_oracle_encoders.py): transformers' ModernBertModel,
-MT5EncoderModel and DebertaV2Encoder with the same weights (implementations
-independent of this restatement and of the reference), on reduced
-configurations.
+MT5EncoderModel, DebertaV2Encoder and DebertaEncoder (v1) with the same
+weights (implementations independent of this restatement and of the
+reference), on reduced configurations.
 """
 from __future__ import annotations
 
@@ -166,3 +175,39 @@ def deberta_encoder(x: torch.Tensor, seq_lengths: torch.Tensor, w, dtype=torch.f
         x = deberta_layer(x, seq_lengths, rel, w.layers[i], w.heads, w.position_buckets,
                           w.max_relative_positions, w.eps, dtype)
     return x
+
+
+def deberta_v1_layer(x: torch.Tensor, seq_lengths: torch.Tensor, rel_emb: torch.Tensor, lw,
+                     heads: int, max_relative_positions: int = 512, eps: float = 1e-7,
+                     dtype=torch.float32) -> torch.Tensor:
+    """One DeBERTa v1 DebertaLayer on x [B, L, hidden] (deberta_encoder.py:528-548).
+    rel_emb = encoder.rel_embeddings.weight [2 max_rel, hidden]; lw has in_proj
+    [3 hidden, hidden] (per head: q, k, v rows), q_bias, v_bias, pos_proj
+    [hidden, hidden], pos_q_proj / pos_q_bias, wo/bo, ln1_w/ln1_b, wi/bi,
+    wo2/bo2, ln2_w/ln2_b."""
+    x = x.to(dtype)
+    B, L, D = x.shape
+    d = D // heads
+
+    def lin(t, W, b=None):
+        y = t @ W.to(dtype).t()
+        return y if b is None else y + b.to(dtype)
+
+    def split(t):  # [..., n, D] -> [..., H, n, d]
+        return t.reshape(*t.shape[:-1], heads, d).transpose(-2, -3)
+
+    qkv = lin(x, lw.in_proj).view(B, L, heads, 3 * d).transpose(1, 2)  # :219-220
+    q, k, v = qkv.chunk(3, dim=-1)
+    q = q + lw.q_bias.to(dtype).view(heads, 1, d)
+    v = v + lw.v_bias.to(dtype).view(heads, 1, d)
+    span = min(L, max_relative_positions)                               # :261
+    r = rel_emb[max_relative_positions - span:max_relative_positions + span].to(dtype)
+    key_rel = split(lin(r, lw.pos_proj))                                # :272-274
+    query_rel = split(lin(r, lw.pos_q_proj, lw.pos_q_bias))             # :281-283
+    pk, pq = deberta_position_projections(q, k, key_rel, query_rel, dtype)
+    ctx = deberta_flash_attention(q, k, v, seq_lengths, pk, pq, 1.0 / math.sqrt(3 * d), span,
+                                  max_relative_positions, False, dtype=dtype)
+    ctx = ctx.transpose(1, 2).reshape(B, L, D)
+    h = layernorm(lin(ctx, lw.wo, lw.bo) + x, lw.ln1_w, lw.ln1_b, eps, dtype)
+    inter = gelu_erf(lin(h, lw.wi, lw.bi))
+    return layernorm(lin(inter, lw.wo2, lw.bo2) + h, lw.ln2_w, lw.ln2_b, eps, dtype)

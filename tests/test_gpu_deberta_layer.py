@@ -68,3 +68,32 @@ def test_deberta_flat_call_matches_padded_batch():
     want_b = deberta_forward(xb, lens.to(dev, torch.int32), w)
     want = torch.cat([want_b[b, :int(n)] for b, n in enumerate(lens)])
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("layers,max_rel", [(1, 512), (2, 128)])
+def test_deberta_v1_layers_match_oracle(layers, max_rel):
+    """DeBERTa v1 (deberta-base shapes: hidden 768, 12 heads, GELU 3072) with
+    linear relative positions: att_span = min(L, max_rel) = 512 uses the whole
+    relative table; max_rel 128 < L clamps at +-128. Valid rows only."""
+    import encoders.deberta as ed
+    from oracle import encoders as oe
+    B, L = 3, 512
+    g = torch.Generator().manual_seed(1013 + max_rel)
+    lens = torch.tensor([512, 300, 129], dtype=torch.int32)
+    x = torch.randn(B, L, 768, generator=g)
+    w = ed.random_weights_v1(num_layers=layers, max_relative_positions=max_rel, dtype=torch.bfloat16)
+    dev = torch.device("cuda:0")
+    got = ed.deberta_v1_forward(x.to(dev, torch.bfloat16), lens.to(dev), w.to(dev)).float().cpu()
+    want = x.to(torch.bfloat16).float()
+    for lw in w.layers:
+        want = oe.deberta_v1_layer(want, lens, w.rel_emb.float(),
+                                   ed.DebertaV1LayerWeights(*(getattr(lw, f).float() for f in
+                                                              ed.DebertaV1LayerWeights.__dataclass_fields__)),
+                                   12, max_rel, w.eps)
+    assert torch.isfinite(got).all()
+    for b in range(B):
+        n = int(lens[b])
+        err = (got[b, :n] - want[b, :n]).abs().max().item()
+        cs = cosine(got[b, :n], want[b, :n])
+        print(f"v1 layers {layers} max_rel {max_rel} row {b} (len {n}): max-abs {err:.3e} cosine {cs:.6f}")
+        assert err <= 6e-2 and cs >= 0.9999, (b, err, cs)

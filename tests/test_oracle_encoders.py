@@ -187,3 +187,59 @@ def test_deberta_oracle_padding_invariance():
     b = oe.deberta_encoder(y, lens, w, dtype=torch.float64)
     torch.testing.assert_close(a[0, :40], b[0, :40], rtol=0, atol=1e-12)
     torch.testing.assert_close(a[1, :21], b[1, :21], rtol=0, atol=1e-12)
+
+
+def _hf_deberta_v1(w):
+    from transformers import DebertaConfig
+    from transformers.models.deberta.modeling_deberta import DebertaEncoder
+    cfg = DebertaConfig(hidden_size=w.hidden, num_attention_heads=w.heads,
+                        intermediate_size=w.inter, num_hidden_layers=len(w.layers),
+                        relative_attention=True, max_relative_positions=w.max_relative_positions,
+                        pos_att_type=["c2p", "p2c"], layer_norm_eps=w.eps, hidden_act="gelu",
+                        hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0)
+    m = DebertaEncoder(cfg).double().eval()
+    sd = {"rel_embeddings.weight": w.rel_emb}
+    for i, lw in enumerate(w.layers):
+        p = f"layer.{i}."
+        sd.update({p + "attention.self.in_proj.weight": lw.in_proj,
+                   p + "attention.self.q_bias": lw.q_bias, p + "attention.self.v_bias": lw.v_bias,
+                   p + "attention.self.pos_proj.weight": lw.pos_proj,
+                   p + "attention.self.pos_q_proj.weight": lw.pos_q_proj,
+                   p + "attention.self.pos_q_proj.bias": lw.pos_q_bias,
+                   p + "attention.output.dense.weight": lw.wo, p + "attention.output.dense.bias": lw.bo,
+                   p + "attention.output.LayerNorm.weight": lw.ln1_w,
+                   p + "attention.output.LayerNorm.bias": lw.ln1_b,
+                   p + "intermediate.dense.weight": lw.wi, p + "intermediate.dense.bias": lw.bi,
+                   p + "output.dense.weight": lw.wo2, p + "output.dense.bias": lw.bo2,
+                   p + "output.LayerNorm.weight": lw.ln2_w, p + "output.LayerNorm.bias": lw.ln2_b})
+    m.load_state_dict(sd, strict=True)
+    return m
+
+
+@pytest.mark.parametrize("L,max_rel", [(80, 64), (40, 64)])
+def test_deberta_v1_oracle_matches_transformers(L, max_rel):
+    """transformers' DeBERTa v1 DebertaEncoder with the same weights: linear
+    positions, att_span = min(L, max_rel) (L = 80 > 64 clamps at +-S; L = 40
+    slices the middle of the relative table). Padded query rows are ignored
+    (transformers' 2-D mask hides every key of them, the flash path zeroes
+    them)."""
+    import encoders.deberta as ed
+    w = ed.random_weights_v1(num_layers=2, hidden=128, heads=2, inter=256,
+                             max_relative_positions=max_rel, seed=21, std=0.05,
+                             dtype=torch.float64)
+    lens = torch.tensor([L, L // 2 + 3, 17], dtype=torch.int32)
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(3, L, w.hidden, generator=g, dtype=torch.float64)
+    got = x
+    for lw in w.layers:
+        got = oe.deberta_v1_layer(got, lens, w.rel_emb, lw, w.heads, max_rel, w.eps, torch.float64)
+    m = _hf_deberta_v1(w)
+    mask = (torch.arange(L)[None, :] < lens[:, None].long()).long()
+    with torch.no_grad():
+        want = m(x, mask, output_hidden_states=False).last_hidden_state
+    for b in range(3):
+        n = int(lens[b])
+        # transformers' v1 DebertaLayerNorm normalises in float32 (.float())
+        # even in a float64 model, so outputs agree to ~1e-6; a missing c2p/p2c
+        # term, a wrong clamp or span slice differs by O(1e-2)
+        torch.testing.assert_close(got[b, :n], want[b, :n], rtol=0, atol=5e-6)

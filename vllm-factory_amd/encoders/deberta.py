@@ -1,4 +1,5 @@
-"""DeBERTa-v3 encoder forward (padded batch [B, L, hidden]) on the hot-path kernels.
+"""DeBERTa-v3 and DeBERTa v1 encoder forwards (padded batch [B, L, hidden]) on the
+hot-path kernels (v1: deberta_v1_layer_forward, linear relative positions).
 
 Follows models/deberta_v2/deberta_v2_encoder.py: the encoder (:734-819)
 LayerNorms the relative-position table once (get_rel_embedding, :770-774)
@@ -136,6 +137,119 @@ def deberta_forward(x: torch.Tensor, seq_lengths: torch.Tensor, w: DebertaWeight
     n = len(w.layers) if num_layers is None else num_layers
     for i in range(n):
         x = deberta_layer_forward(x, seq_lengths, rel, w.layers[i], w)
+    return x
+
+
+
+# ---------------------------------------------------------------------------
+# DeBERTa v1 (linear relative positions)
+# ---------------------------------------------------------------------------
+@dataclass
+class DebertaV1LayerWeights:
+    in_proj: torch.Tensor     # [3 * hidden, hidden], rows per head: q, k, v (no bias)
+    q_bias: torch.Tensor      # [hidden]
+    v_bias: torch.Tensor      # [hidden]
+    pos_proj: torch.Tensor    # [hidden, hidden] (c2p, no bias)
+    pos_q_proj: torch.Tensor  # [hidden, hidden] (p2c)
+    pos_q_bias: torch.Tensor  # [hidden]
+    wo: torch.Tensor
+    bo: torch.Tensor
+    ln1_w: torch.Tensor
+    ln1_b: torch.Tensor
+    wi: torch.Tensor
+    bi: torch.Tensor
+    wo2: torch.Tensor
+    bo2: torch.Tensor
+    ln2_w: torch.Tensor
+    ln2_b: torch.Tensor
+
+
+@dataclass
+class DebertaV1Weights:
+    hidden: int
+    heads: int
+    inter: int
+    rel_emb: torch.Tensor     # encoder.rel_embeddings.weight [2 * max_rel, hidden]
+    layers: List[DebertaV1LayerWeights] = field(default_factory=list)
+    max_relative_positions: int = 512
+    eps: float = 1e-7
+
+    def to(self, device=None, dtype=None) -> "DebertaV1Weights":
+        def mv(t):
+            return t.to(device=device, dtype=dtype)
+        return DebertaV1Weights(
+            self.hidden, self.heads, self.inter, mv(self.rel_emb),
+            [DebertaV1LayerWeights(*(mv(getattr(l, f))
+                                     for f in DebertaV1LayerWeights.__dataclass_fields__))
+             for l in self.layers],
+            self.max_relative_positions, self.eps)
+
+
+def random_weights_v1(num_layers: int = 12, hidden: int = 768, heads: int = 12, inter: int = 3072,
+                      max_relative_positions: int = 512, seed: int = 1013, std: float = 0.02,
+                      dtype=torch.bfloat16) -> DebertaV1Weights:
+    """DeBERTa-base (v1) shapes, random-init ~ N(0, std) (CPU, seeded);
+    LayerNorm weights 1 + N(0, std), biases N(0, std)."""
+    g = torch.Generator().manual_seed(seed)
+
+    def rnd(*shape):
+        return (torch.randn(*shape, generator=g) * std).to(dtype)
+
+    def ln():
+        return (1.0 + torch.randn(hidden, generator=g) * std).to(dtype), rnd(hidden)
+
+    layers = []
+    for _ in range(num_layers):
+        att = (rnd(3 * hidden, hidden), rnd(hidden), rnd(hidden), rnd(hidden, hidden),
+               rnd(hidden, hidden), rnd(hidden))
+        wo, bo = rnd(hidden, hidden), rnd(hidden)
+        ln1 = ln()
+        wi, bi = rnd(inter, hidden), rnd(inter)
+        wo2, bo2 = rnd(hidden, inter), rnd(hidden)
+        layers.append(DebertaV1LayerWeights(*att, wo, bo, *ln1, wi, bi, wo2, bo2, *ln()))
+    rel = rnd(2 * max_relative_positions, hidden)
+    return DebertaV1Weights(hidden, heads, inter, rel, layers, max_relative_positions)
+
+
+def deberta_v1_layer_forward(x: torch.Tensor, seq_lengths: torch.Tensor,
+                             lw: DebertaV1LayerWeights, w: DebertaV1Weights) -> torch.Tensor:
+    """One DeBERTa v1 DebertaLayer (models/deberta/deberta_encoder.py:528-548) on
+    x [B, L, hidden] with seq_lengths int32 [B] on the device: in_proj (rows
+    per head q, k, v) with q_bias / v_bias folded into the GEMM's bias, the
+    linear-position disentangled attention of :246-309 (att_span =
+    min(L, max_relative_positions), pos_proj / pos_q_proj applied to the
+    [2 span, hidden] slice of the relative table, projections computed in the
+    attention kernel), then the post-LN blocks (:445-526; DebertaLayerNorm,
+    eps inside the square root, as LayerNorm)."""
+    B, L, D = x.shape
+    H = w.heads
+    d = D // H
+    mr = w.max_relative_positions
+    span = min(L, mr)
+    zero = torch.zeros_like(lw.q_bias).view(H, 1, d)
+    b_in = torch.cat([lw.q_bias.view(H, 1, d), zero, lw.v_bias.view(H, 1, d)], 1).reshape(-1)
+    qkv = F.linear(x, lw.in_proj, b_in).view(B, L, H, 3, d)
+    q, k, v = (qkv[:, :, :, i].transpose(1, 2) for i in range(3))
+    rel = w.rel_emb[mr - span:mr + span]
+    key_rel = F.linear(rel, lw.pos_proj).view(2 * span, H, d).transpose(0, 1)
+    query_rel = F.linear(rel, lw.pos_q_proj, lw.pos_q_bias).view(2 * span, H, d).transpose(0, 1)
+    ctx = torch.empty(B, L, H, d, dtype=x.dtype, device=x.device)
+    flash_deberta_attention_fused(q, k, v, seq_lengths, key_rel, query_rel, 1.0 / math.sqrt(3 * d),
+                                  span, mr, False, out=ctx.transpose(1, 2))
+    h = fused_add_layernorm(F.linear(ctx.view(B, L, D), lw.wo, lw.bo), x, lw.ln1_w, lw.ln1_b,
+                            w.eps, return_sum=False)
+    inter = activation(F.linear(h, lw.wi, lw.bi), "gelu")
+    return fused_add_layernorm(F.linear(inter, lw.wo2, lw.bo2), h, lw.ln2_w, lw.ln2_b, w.eps,
+                               return_sum=False)
+
+
+def deberta_v1_forward(x: torch.Tensor, seq_lengths: torch.Tensor, w: DebertaV1Weights,
+                       num_layers: Optional[int] = None) -> torch.Tensor:
+    """DeBERTa v1 encoder stack (deberta_encoder.py:645-697) on embedding output
+    x [B, L, hidden] -> last hidden state."""
+    n = len(w.layers) if num_layers is None else num_layers
+    for i in range(n):
+        x = deberta_v1_layer_forward(x, seq_lengths, w.layers[i], w)
     return x
 
 
