@@ -269,6 +269,25 @@ def epilogue_bench(torch, args, c2):
     row = 1024 * 2
     bench("pad_rows", lambda: pad_packed(flat, cu3, 32, L3), (T3 + 32 * L3) * row)
     bench("unpad_rows", lambda: unpad_packed(padded, cu3, T3), 2 * T3 * row)
+    del hid, flat, padded
+    # ColBERT head at config 5 size: last residual add + final LayerNorm +
+    # projection 768 -> 128 + L2 norm, fused vs the unfused composition
+    # (LayerNorm kernel, hipBLASLt GEMM, torch normalize)
+    import torch.nn.functional as F
+    from kernels.colbert_head import colbert_head
+    from kernels.fused_layernorm import fused_add_layernorm
+    T5 = 163736
+    pend = torch.randn(T5, 768, generator=g).bfloat16().to(dev)
+    resid = torch.randn(T5, 768, generator=g).bfloat16().to(dev)
+    lnw = torch.ones(768, dtype=torch.bfloat16, device=dev)
+    proj = (torch.randn(128, 768, generator=g) * 0.03).bfloat16().to(dev)
+    hb = (2 * T5 * 768 + T5 * 128) * 2
+    bench("colbert_head", lambda: colbert_head(pend, proj, None, lnw, None, 1e-5, residual=resid), hb)
+
+    def unfused():
+        h, _ = fused_add_layernorm(pend, resid, lnw, None, 1e-5)
+        return F.normalize(F.linear(h, proj), dim=-1, eps=1e-8)
+    bench("colbert_head_unfused", unfused, hb)
     return res
 
 

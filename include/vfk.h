@@ -219,6 +219,26 @@ int vfk_unpad_rows(const void* src, int64_t row_bytes,
  * p < max_positions, f < 32. out: device fp32 [max_positions * 64]. */
 int vfk_rope_table(float theta, int32_t max_positions, float* out, void* stream);
 
+/* ColBERT output head (no counterpart kernel in the reference: it replaces
+ * the encoder's final LayerNorm, models/modernbert/modernbert_encoder.py:
+ * 412-415 and :478, followed by the PyLate Dense projection and the L2
+ * normalisation of plugins/moderncolbert/model.py:260-267).
+ *   x [T, D]: D a multiple of 256 up to 1024, rows contiguous and 8-byte
+ *     aligned; residual [T, D] or NULL (the LayerNorm input is x + residual)
+ *   ln_weight, ln_bias [D] or NULL; without ln_weight the rows are projected
+ *     as given (no LayerNorm)
+ *   weight [N, D] (nn.Linear layout; N = 32, 64, 96 or 128; rows 16-byte
+ *     aligned), bias [N] or NULL
+ *   hidden_out [T, D] or NULL: receives the LayerNorm output
+ *   out [T, N] = y / max(|y|, 1e-8) per row, y = LN(x + residual) W^T + bias
+ * x, weight and outputs share one 16-bit dtype; statistics, products and
+ * norms are fp32. */
+int vfk_colbert_head_fwd(const vfk_tensor* x, const vfk_tensor* residual,
+                         const vfk_tensor* ln_weight, const vfk_tensor* ln_bias,
+                         float eps, const vfk_tensor* weight,
+                         const vfk_tensor* bias, vfk_tensor* hidden_out,
+                         vfk_tensor* out, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Memory-bound epilogues                                                    */
 /* ------------------------------------------------------------------------ */

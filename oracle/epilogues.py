@@ -2,8 +2,9 @@
 
 Pinned by (tests/test_oracle_epilogues.py): torch.nn.functional.layer_norm,
 F.gelu(approximate='none'|'tanh'), F.silu, transformers' T5LayerNorm for
-RMSNorm, and the RoPE identities (position 0 is the identity, pair norms are
-preserved, <rope(q,p), rope(k,p')> depends only on p - p').
+RMSNorm, the RoPE identities (position 0 is the identity, pair norms are
+preserved, <rope(q,p), rope(k,p')> depends only on p - p'), and, for the
+ColBERT head, F.linear + F.normalize and unit row norms.
 """
 from __future__ import annotations
 
@@ -80,3 +81,33 @@ def rope_table(x, cos, sin, dtype=torch.float32):
 def residual_add(x, residual, dtype=torch.float32):
     """kernels/fused_dropout_residual.py:50-51 (inference): residual + x."""
     return residual.to(dtype) + x.to(dtype)
+
+
+def residual_dense(x, weight, bias=None, residual_weight=None, use_residual=False,
+                   dtype=torch.float32):
+    """plugins/moderncolbert/model.py:68-95 (_ResidualDense.forward): x W^T (+ b),
+    plus x (same width) or x R^T when use_residual."""
+    x = x.to(dtype)
+    y = x @ weight.to(dtype).t()
+    if bias is not None:
+        y = y + bias.to(dtype)
+    if use_residual:
+        y = y + (x if residual_weight is None else x @ residual_weight.to(dtype).t())
+    return y
+
+
+def colbert_head(hidden, layers, norm_weight=None, norm_bias=None, eps=1e-5, residual=None,
+                 layer_norm=True, dtype=torch.float32):
+    """The encoder's final LayerNorm (models/modernbert/modernbert_encoder.py:412-415,
+    :478; input hidden + residual when given) unless layer_norm is False, then
+    the ColBERT projection stack and L2 normalisation of
+    plugins/moderncolbert/model.py:260-267: projected / max(|projected|, 1e-8).
+    layers: (weight, bias, residual_weight, use_residual) per Dense module."""
+    x = hidden.to(dtype)
+    if residual is not None:
+        x = x + residual.to(dtype)
+    if layer_norm:
+        x = layernorm(x, norm_weight, norm_bias, eps, dtype)
+    for w, b, rw, use_res in layers:
+        x = residual_dense(x, w, b, rw, use_res, dtype)
+    return x / x.norm(dim=-1, keepdim=True).clamp(min=1e-8)

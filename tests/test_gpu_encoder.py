@@ -53,3 +53,22 @@ def test_modernbert_from_position_ids_matches_cu_path():
     got = em.modernbert_forward_positions(ids.to(dev)[None], pos.to(dev)[None], wd, num_layers=2)
     want = em.modernbert_forward(ids.to(dev), cu.to(dev), mx, wd, num_layers=2)
     assert torch.equal(got, want)
+
+
+def test_modernbert_colbert_head_matches_unfused():
+    """The ColBERT forward (final residual add + LayerNorm + projection + L2
+    norm fused) against the plain forward's last hidden state projected and
+    normalised in fp32: per-row cosine 0.9999, unit norms."""
+    import encoders.modernbert as em
+    w, ids, cu, mx = _case()
+    dev = torch.device("cuda:0")
+    wd = w.to(dev)
+    g = torch.Generator().manual_seed(1305)
+    proj = (torch.randn(128, 768, generator=g) * 0.03).bfloat16()
+    got = em.modernbert_colbert_forward(ids.to(dev), cu.to(dev), mx, wd, proj.to(dev),
+                                        num_layers=2).float().cpu()
+    hid = em.modernbert_forward(ids.to(dev), cu.to(dev), mx, wd, num_layers=2).float().cpu()
+    want = torch.nn.functional.normalize(hid @ proj.float().t(), dim=-1, eps=1e-8)
+    worst = min(cosine(got[i], want[i]) for i in range(0, got.shape[0], 7))
+    assert worst >= 0.9999, worst
+    torch.testing.assert_close(got.norm(dim=-1), torch.ones(got.shape[0]), atol=5e-3, rtol=0)

@@ -141,3 +141,67 @@ def test_rope_strided_qkv_view(dev):
     cos, sin = cos.bfloat16()[None], sin.bfloat16()[None]
     got = fused_rope_apply(qkv.to(dev)[:, :, 0], cos.to(dev), sin.to(dev))
     assert_elem_close(got, oe.rope_table(q, cos, sin), torch.bfloat16, "rope view")
+
+
+# ------------------------------------------------------------------ ColBERT head
+def _colbert_rows_close(got, want, what):
+    """Unit-norm embeddings of 16-bit LayerNorm outputs projected over D terms:
+    each row within cosine 0.9999 of the fp32 oracle and every entry within
+    4e-3 (entries are ~1/sqrt(N) ~ 0.09; one bf16 rounding of the normalised
+    hidden row, the product sum and the output each contribute < 1e-3)."""
+    from _tol import cosine
+    got = got.float().cpu()
+    assert torch.isfinite(got).all(), what
+    err = (got - want).abs().max().item()
+    worst = min(cosine(got[i], want[i]) for i in range(0, got.shape[0], max(1, got.shape[0] // 64)))
+    assert err <= 4e-3 and worst >= 0.9999, (what, err, worst)
+    torch.testing.assert_close(got.norm(dim=-1), torch.ones(got.shape[0]), atol=5e-3, rtol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,D,N", [(1000, 768, 128), (1, 768, 128), (33, 1024, 96), (64, 256, 32)])
+def test_colbert_head_with_final_layernorm(dev, dtype, T, D, N):
+    """ModernBERT final LayerNorm (weight, no bias, eps 1e-5) of x + residual,
+    projection [N, D] without bias, L2 normalisation; the LayerNorm output
+    that comes back equals the LayerNorm oracle."""
+    from kernels.colbert_head import colbert_head
+    x, r = _rand((T, D), dtype, 41), _rand((T, D), dtype, 42)
+    lw = (1 + 0.1 * _rand((D,), torch.float32, 43)).to(dtype)
+    w = _rand((N, D), dtype, 44, 0.05)
+    want = oe.colbert_head(x, [(w, None, None, False)], lw, None, 1e-5, residual=r)
+    got, h = colbert_head(x.to(dev), w.to(dev), None, lw.to(dev), None, 1e-5, residual=r.to(dev),
+                          return_hidden=True)
+    _colbert_rows_close(got, want, f"colbert {dtype} {T}x{D}->{N}")
+    assert_elem_close(h, oe.layernorm(x.float() + r.float(), lw, None, 1e-5), dtype,
+                      f"colbert hidden {dtype}")
+
+
+def test_colbert_head_projection_only_with_bias(dev):
+    """No LayerNorm (rows projected as given), a bias, and a strided input view."""
+    from kernels.colbert_head import colbert_head
+    base = _rand((300, 2 * 512), torch.bfloat16, 45)
+    x = base[:, 512:]  # row stride 1024
+    w = _rand((64, 512), torch.bfloat16, 46, 0.05)
+    b = _rand((64,), torch.bfloat16, 47, 0.1)
+    want = oe.colbert_head(x, [(w, b, None, False)], layer_norm=False)
+    got = colbert_head(x.to(dev), w.to(dev), b.to(dev))
+    _colbert_rows_close(got, want, "colbert projection only")
+
+
+def test_colbert_project_residual_stack(dev):
+    """A PyLate stack like the LateOn checkpoint's (768 -> 1536 + residual,
+    1536 -> 768 + residual, 768 -> 128): GEMMs, then the fused last layer."""
+    from kernels.colbert_head import colbert_project
+    g = lambda shape, seed: _rand(shape, torch.bfloat16, seed, 0.03)
+    layers = [(g((1536, 768), 51), None, g((1536, 768), 52), True),
+              (g((768, 1536), 53), None, g((768, 1536), 54), True),
+              (g((128, 768), 55), None, None, False)]
+    x = _rand((257, 768), torch.bfloat16, 56)
+    want = oe.colbert_head(x, layers, layer_norm=False)
+    got = colbert_project(x.to(dev), [tuple(None if t is None else (t.to(dev) if torch.is_tensor(t) else t)
+                                            for t in l) for l in layers])
+    from _tol import cosine
+    got = got.float().cpu()
+    # the intermediate GEMM outputs are rounded to bf16 twice per layer
+    assert min(cosine(got[i], want[i]) for i in range(257)) >= 0.9995
+    torch.testing.assert_close(got.norm(dim=-1), torch.ones(257), atol=5e-3, rtol=0)

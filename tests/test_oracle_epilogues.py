@@ -56,3 +56,49 @@ def test_rope_identities():
     for d in (0, 3, 11):
         vals = torch.stack([cq[p + d] @ ck[p] for p in range(0, 50 - d)])
         assert float(vals.max() - vals.min()) < 1e-4 * float(vals.abs().max() + 1)
+
+
+# ------------------------------------------------------------------ ColBERT head
+def test_colbert_head_matches_library_routines():
+    """LayerNorm -> Linear -> L2 normalise equals F.layer_norm, F.linear and
+    F.normalize (eps 1e-8 is the reference's clamp) composed."""
+    import torch.nn.functional as F
+    from oracle import epilogues as oep
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(50, 256, generator=g, dtype=torch.float64)
+    r = torch.randn(50, 256, generator=g, dtype=torch.float64)
+    lw = 1 + 0.1 * torch.randn(256, generator=g, dtype=torch.float64)
+    w = torch.randn(64, 256, generator=g, dtype=torch.float64) * 0.05
+    b = torch.randn(64, generator=g, dtype=torch.float64) * 0.01
+    got = oep.colbert_head(x, [(w, b, None, False)], lw, None, 1e-5, residual=r, dtype=torch.float64)
+    want = F.normalize(F.linear(F.layer_norm(x + r, (256,), lw, None, 1e-5), w, b), dim=-1, eps=1e-8)
+    torch.testing.assert_close(got, want, rtol=0, atol=1e-12)
+    torch.testing.assert_close(got.norm(dim=-1), torch.ones(50, dtype=torch.float64))
+
+
+def test_colbert_head_residual_stack_and_zero_rows():
+    """The PyLate residual Dense stack (widths 256 -> 512 -> 256 -> 64, residual
+    projections where widths differ, identity where equal), and an all-zero
+    projected row stays zero (the norm is clamped at 1e-8, not divided by 0)."""
+    import torch.nn.functional as F
+    from oracle import epilogues as oep
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(20, 256, generator=g, dtype=torch.float64)
+    w1, r1 = torch.randn(512, 256, generator=g, dtype=torch.float64) * 0.05, \
+        torch.randn(512, 256, generator=g, dtype=torch.float64) * 0.05
+    w2 = torch.randn(256, 512, generator=g, dtype=torch.float64) * 0.05
+    r2 = torch.randn(256, 512, generator=g, dtype=torch.float64) * 0.05
+    w3 = torch.randn(64, 256, generator=g, dtype=torch.float64) * 0.05
+    layers = [(w1, None, r1, True), (w2, None, r2, True), (w3, None, None, False)]
+    got = oep.colbert_head(x, layers, layer_norm=False, dtype=torch.float64)
+    h = F.linear(x, w1) + F.linear(x, r1)
+    h = F.linear(h, w2) + F.linear(h, r2)
+    want = F.normalize(F.linear(h, w3), dim=-1, eps=1e-8)
+    torch.testing.assert_close(got, want, rtol=0, atol=1e-12)
+    # same width: the residual is the input itself
+    sq = torch.randn(256, 256, generator=g, dtype=torch.float64) * 0.05
+    y = oep.residual_dense(x, sq, None, None, True, dtype=torch.float64)
+    torch.testing.assert_close(y, F.linear(x, sq) + x)
+    z = oep.colbert_head(torch.zeros(3, 256, dtype=torch.float64), [(w3, None, None, False)],
+                         layer_norm=False, dtype=torch.float64)
+    assert torch.equal(z, torch.zeros(3, 64, dtype=torch.float64))

@@ -24,6 +24,7 @@ from typing import List, Optional
 import torch
 import torch.nn.functional as F
 
+from kernels.colbert_head import colbert_head
 from kernels.fused_glu_mlp import fused_gelu_mul_dropout
 from kernels.fused_layernorm import fused_add_layernorm, fused_layernorm
 from kernels.varlen_attention import varlen_from_positions, varlen_rope_attention
@@ -85,9 +86,10 @@ def random_weights(num_layers: int = 22, hidden: int = 768, heads: int = 12, int
                              ones.clone())
 
 
-def modernbert_forward(ids: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,
-                       w: ModernBertWeights, num_layers: Optional[int] = None) -> torch.Tensor:
-    """ids [T] (device, int64), cu_seqlens int32 [n + 1] -> last hidden state [T, hidden]."""
+def _encode(ids: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int, w: ModernBertWeights,
+            num_layers: Optional[int]):
+    """Embeddings and layers; returns (pending MLP output or None, residual
+    stream) before the final LayerNorm."""
     T = ids.shape[0]
     d = w.hidden // w.heads
     key_valid = ids != MASK_TOKEN_ID
@@ -111,10 +113,29 @@ def modernbert_forward(ids: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: 
         y = F.linear(h, lw.wi)
         g = fused_gelu_mul_dropout(y[:, :w.inter], y[:, w.inter:], "gelu")
         pending = F.linear(g, lw.wo_mlp)
+    return pending, x
+
+
+def modernbert_forward(ids: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,
+                       w: ModernBertWeights, num_layers: Optional[int] = None) -> torch.Tensor:
+    """ids [T] (device, int64), cu_seqlens int32 [n + 1] -> last hidden state [T, hidden]."""
+    pending, x = _encode(ids, cu_seqlens, max_seqlen, w, num_layers)
     if pending is None:
         return fused_layernorm(x, w.hidden, w.final_norm, None, w.eps)
     out, _ = fused_add_layernorm(pending, x, w.final_norm, None, w.eps)
     return out
+
+
+def modernbert_colbert_forward(ids: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,
+                               w: ModernBertWeights, proj_weight: torch.Tensor,
+                               proj_bias: Optional[torch.Tensor] = None,
+                               num_layers: Optional[int] = None) -> torch.Tensor:
+    """ModernBERT + ColBERT head (plugins/moderncolbert/model.py:220-267 with a
+    single Dense layer): the last residual add, the final LayerNorm, the
+    projection [colbert_dim, hidden] and the L2 normalisation in one kernel
+    (kernels.colbert_head). Returns [T, colbert_dim] unit-norm embeddings."""
+    pending, x = _encode(ids, cu_seqlens, max_seqlen, w, num_layers)
+    return colbert_head(x, proj_weight, proj_bias, w.final_norm, None, w.eps, residual=pending)
 
 
 def modernbert_forward_positions(input_ids: torch.Tensor, position_ids: torch.Tensor,

@@ -1,0 +1,69 @@
+"""ColBERT output head: final LayerNorm, PyLate Dense projection and L2
+normalisation in one pass (vfk_colbert_head_fwd).
+
+No reference kernel exists for this step: the reference's ColBERT plugin runs
+the encoder's final LayerNorm (models/modernbert/modernbert_encoder.py:412-415,
+:478), then its projection stack and
+`projected / projected.norm(dim=-1, keepdim=True).clamp(min=1e-8)`
+(plugins/moderncolbert/model.py:260-267, _ResidualDense :68-95) as separate
+torch ops. Here the LayerNorm output is projected while it is still in LDS.
+"""
+from __future__ import annotations
+
+from typing import Optional, Sequence, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+
+def colbert_head(hidden: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                 norm_weight: Optional[torch.Tensor] = None,
+                 norm_bias: Optional[torch.Tensor] = None, eps: float = 1e-5,
+                 residual: Optional[torch.Tensor] = None,
+                 return_hidden: bool = False):
+    """hidden [T, D] (+ residual) -> LayerNorm (if norm_weight) -> @ weight^T
+    (+ bias) -> rows scaled to unit L2 norm (norm clamped at 1e-8).
+    weight [N, D] with N in {32, 64, 96, 128}, D a multiple of 256 up to 1024.
+    Returns the [T, N] embeddings, and the LayerNorm output if return_hidden."""
+    dev = _lib.require_gpu(hidden, weight, bias, norm_weight, norm_bias, residual)
+    if hidden.dim() != 2 or weight.dim() != 2 or weight.shape[1] != hidden.shape[1]:
+        raise ValueError("hidden must be [T, D] and weight [N, D]")
+    x = _lib.rows_aligned(hidden)
+    r = _lib.rows_aligned(residual) if residual is not None else None
+    wt = _lib.rows_aligned(weight)
+    T, N = x.shape[0], wt.shape[0]
+    out = torch.empty(T, N, dtype=x.dtype, device=dev)
+    h = torch.empty_like(x) if return_hidden else None
+    vec = lambda t: None if t is None else t.contiguous()
+    _lib.on_device(
+        "vfk_colbert_head_fwd", dev,
+        _lib.ref(_lib.desc(x)), _lib.ref(_lib.desc(r)), _lib.ref(_lib.desc(vec(norm_weight))),
+        _lib.ref(_lib.desc(vec(norm_bias))), float(eps), _lib.ref(_lib.desc(wt)),
+        _lib.ref(_lib.desc(vec(bias))), _lib.ref(_lib.desc(h)), _lib.ref(_lib.desc(out)))
+    return (out, h) if return_hidden else out
+
+
+ProjectionLayer = Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor], bool]
+
+
+def colbert_project(hidden_states: torch.Tensor, layers: Sequence[ProjectionLayer]) -> torch.Tensor:
+    """The PyLate Dense stack plus L2 normalisation of
+    plugins/moderncolbert/model.py:260-267 on [T, D] hidden states.
+    layers: (weight, bias, residual_weight, use_residual) per _ResidualDense
+    (:68-95): y = x W^T + b, plus x (same width) or x R^T when use_residual.
+    All layers but the last run as GEMMs; the last one (which must not use a
+    residual) runs fused with the normalisation."""
+    if not layers:
+        raise ValueError("at least one projection layer is needed")
+    x = hidden_states
+    for wt, b, rw, use_res in layers[:-1]:
+        y = F.linear(x, wt, b)
+        if use_res:
+            y = y + (x if rw is None else F.linear(x, rw))
+        x = y
+    wt, b, rw, use_res = layers[-1]
+    if use_res:
+        raise NotImplementedError("a residual branch on the last projection layer is not fused")
+    return colbert_head(x, wt, b)
