@@ -5,7 +5,7 @@ from .deberta import (DebertaLayerWeights, DebertaV1LayerWeights, DebertaV1Weigh
                       deberta_v1_forward, deberta_v1_layer_forward, random_weights_v1)
 from .modernbert import (ModernBertLayerWeights, ModernBertWeights, modernbert_colbert_forward,
                          modernbert_forward, modernbert_forward_positions, random_weights)
-from .mt5 import mt5_layer_forward
+from .mt5 import mt5_encoder_flat, mt5_layer_forward
 
 __all__ = ["DebertaLayerWeights", "DebertaV1LayerWeights", "DebertaV1Weights", "DebertaWeights",
            "deberta_forward", "deberta_forward_flat", "deberta_layer_forward",
@@ -13,4 +13,4 @@ __all__ = ["DebertaLayerWeights", "DebertaV1LayerWeights", "DebertaV1Weights", "
            "ModernBertLayerWeights", "ModernBertWeights", "modernbert_colbert_forward",
            "modernbert_forward",
            "modernbert_forward_positions", "random_weights",
-           "mt5_layer_forward"]
+           "mt5_encoder_flat", "mt5_layer_forward"]

@@ -255,7 +255,9 @@ def deberta_v1_forward(x: torch.Tensor, seq_lengths: torch.Tensor, w: DebertaV1W
 
 def deberta_forward_flat(x: torch.Tensor, positions: torch.Tensor, w: DebertaWeights,
                          num_layers: Optional[int] = None) -> torch.Tensor:
-    """The GLiNER plugins' flat call (plugins/deberta_gliner/model.py:166-202):
+    """The GLiNER plugins' flat call (plugins/deberta_gliner/model.py:166-202; the
+    GLiNER2 plugin, plugins/deberta_gliner2/model.py:124-137, runs the flat
+    stream as one sequence and gets per-sequence attention from this path):
     embedding output x [T, hidden] of a packed stream whose sequences start at
     position 0 -> last hidden state [T, hidden]. The re-padding and the
     concatenation of valid rows run on the device (kernels.packing); the

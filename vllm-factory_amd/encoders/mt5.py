@@ -34,3 +34,29 @@ def mt5_layer_forward(x: torch.Tensor, wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2
     h2, x1 = fused_add_rms_norm(o, x, ln2, eps)
     g = fused_gelu_mul_dropout(h2 @ wi0, h2 @ wi1, "gelu_new")
     return torch.addmm(x1.reshape(-1, D), g.reshape(-1, g.shape[-1]), wff_o).view(B, L, D)
+
+
+def mt5_encoder_flat(x: torch.Tensor, positions: torch.Tensor, layers, table: torch.Tensor,
+                     num_buckets: int = 32, max_distance: int = 128,
+                     eps: float = 1e-6) -> torch.Tensor:
+    """mT5 encoder layers on a flat vLLM stream routed per sequence.
+
+    The reference's mT5 GLiNER plugin (plugins/mt5_gliner/model.py:169-201)
+    runs the encoder on the flat [1, T] stream with an all-ones mask, so the
+    tokens of different requests attend to each other. Here the sequences are
+    found from the position ids on the device (a sequence starts at position
+    0, kernels.packing.seq_metadata rule "zero"), padded into [n, L, d_model]
+    once, run with the reference's additive key mask (1 - m) * finfo.min
+    (models/mt5/mt5_encoder.py:571-576), and the valid rows are concatenated
+    back; each sequence gets the attention it would get alone.
+    x: embedding output [T, d_model]; layers: (wq, wk, wv, wo, wi0, wi1, wff_o,
+    ln1, ln2) per layer as for mt5_layer_forward."""
+    from kernels.packing import pad_packed, read_metadata, seq_metadata, unpad_packed
+    cu, meta = seq_metadata(positions, "zero")
+    cu, n, max_len, _ = read_metadata(cu, meta)
+    xb, lens = pad_packed(x, cu, n, max_len)
+    valid = torch.arange(max_len, device=x.device)[None, :] < lens[:, None]
+    mask = ((~valid).to(x.dtype) * torch.finfo(x.dtype).min).view(n, 1, 1, max_len)
+    for lw in layers:
+        xb = mt5_layer_forward(xb, *lw, table, mask, num_buckets, max_distance, eps)
+    return unpad_packed(xb, cu, x.shape[0])
