@@ -123,3 +123,19 @@ def test_batch_from_flat_matches_gliner_loop(dev, lens):
     for a, b in zip(got[:3], want[:3]):
         assert torch.equal(a.cpu(), b)
     assert got[4].cpu().tolist() == want[3]
+
+
+def test_pad_unpad_zero_length_sequences(dev):
+    """Empty sequences get a padded block of fill only (their flat rows need
+    not exist, even at the end of the stream) and write nothing back."""
+    from kernels.packing import pad_packed, unpad_packed
+    lens = [0, 3, 0, 2, 0]
+    cu = workloads.cu_from_lengths(torch.tensor(lens))
+    x = _rows(5, (16,), torch.bfloat16, 9)
+    padded, slen = pad_packed(x.to(dev), cu.to(dev), 5, 4, -1.0)
+    want = torch.full((5, 4, 16), -1.0, dtype=torch.bfloat16)
+    want[1, :3] = x[:3]
+    want[3, :2] = x[3:5]
+    assert torch.equal(padded.cpu(), want)
+    assert slen.cpu().tolist() == lens
+    assert torch.equal(unpad_packed(padded, cu.to(dev), 5).cpu(), x)

@@ -133,3 +133,16 @@ def test_varlen_from_positions_drives_attention(dev):
     assert_attn_close(got, want, "varlen from positions")
     with pytest.raises(ValueError, match="count up from 0"):
         varlen_from_positions(torch.tensor([0, 1, 2, 5, 6], device=dev))
+
+
+@pytest.mark.parametrize("window", [-1, 64])
+def test_varlen_zero_length_sequences(dev, window):
+    """cu_seqlens with empty sequences (repeated offsets, also first and last):
+    their query tiles exit at once and the other sequences are unaffected."""
+    lengths = [0, 130, 0, 0, 65, 1, 0]
+    qkv, cu = _pack(lengths, torch.bfloat16, 21)
+    q, k, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
+    want = oa.varlen_attention(q, k, v, cu, window, 10000.0, None, 0.125)
+    qd = qkv.to(dev)
+    got = _vl()(qd[:, 0], qd[:, 1], qd[:, 2], cu.to(dev), max(lengths), window, 10000.0, 0.125)
+    assert_attn_close(got, want, f"zero-length sequences w={window}")
