@@ -288,6 +288,36 @@ def epilogue_bench(torch, args, c2):
         h, _ = fused_add_layernorm(pend, resid, lnw, None, 1e-5)
         return F.normalize(F.linear(h, proj), dim=-1, eps=1e-8)
     bench("colbert_head_unfused", unfused, hb)
+    del pend, resid
+    # GLiNER pooler front-end over 256 packed prompt + text requests of
+    # U{512..768} tokens, bf16 768: class-token compaction, first-subtoken
+    # word index, prompt rows and word rows. The whole call includes its one
+    # read-back; the word-row gather, which moves most of the bytes, is also
+    # timed alone.
+    from kernels import _lib
+    from kernels.gliner_pooler import gliner_reps_packed
+    gr = workloads.gliner_requests()
+    Tg = gr.ids.numel()
+    hg = torch.randn(Tg, 768, generator=g).bfloat16().to(dev)
+    ids_g, wm_g, cu_g = gr.ids.to(dev), gr.words_mask.to(dev), gr.cu_seqlens.to(dev)
+    pe, pe_cu, we, we_cu = gliner_reps_packed(hg, ids_g, wm_g, cu_g, gr.text_lengths,
+                                              gr.ent_token_id)
+    C, W = pe.shape[0], we.shape[0]
+    row = 768 * 2
+    bench("gliner_reps", lambda: gliner_reps_packed(hg, ids_g, wm_g, cu_g, gr.text_lengths,
+                                                     gr.ent_token_id),
+          16 * Tg + 2 * (C + W) * row)
+    wcu = we_cu.to(device=dev, dtype=torch.int32)
+    src = torch.zeros(W, dtype=torch.int32, device=dev)
+    _lib.on_device("vfk_gliner_word_index", dev, wm_g.data_ptr(), Tg, cu_g.data_ptr(),
+                   cu_g.numel() - 1, wcu.data_ptr(), src.data_ptr(), None)
+    bench("gliner_word_index", lambda: _lib.on_device(
+        "vfk_gliner_word_index", dev, wm_g.data_ptr(), Tg, cu_g.data_ptr(), cu_g.numel() - 1,
+        wcu.data_ptr(), src.data_ptr(), None), 8 * Tg + 4 * W)
+    bench("gliner_word_rows", lambda: _lib.on_device(
+        "vfk_gliner_word_rows", dev, hg.data_ptr(), row, Tg, src.data_ptr(), W, we.data_ptr()),
+        4 * W + 2 * W * row)
+    res["gliner_reps"].update(tokens=Tg, class_rows=C, word_rows=W)
     return res
 
 

@@ -212,6 +212,62 @@ int vfk_unpad_rows(const void* src, int64_t row_bytes,
                    const int32_t* cu_seqlens, int32_t num_seqs,
                    int32_t max_len, void* dst, void* stream);
 
+/* GLiNER span pooler front-end over a packed stream: the per-request
+ * gathers of _extract_gliner_reps (poolers/gliner.py:313-347), which the
+ * reference runs once per request after split_hidden_states
+ * (poolers/gliner.py:201, :219-255). Request s owns stream rows
+ * cu_seqlens[s] .. cu_seqlens[s + 1] - 1 (int32 [num_seqs + 1]). status
+ * (int32, may be NULL) is set to 1 where the reference raises IndexError and
+ * is never cleared by these calls.
+ *
+ * vfk_gliner_class_index: the class-token positions
+ * ((iid == ent_token_id).nonzero(), poolers/gliner.py:317) of every request
+ * at once. input_ids int64 [total_tokens]. Writes class_idx int32
+ * [total_tokens + 1] (stream indices of the class tokens in order, then
+ * total_tokens), class_cu int32 [num_seqs + 1] (request s owns
+ * class_idx[class_cu[s] .. class_cu[s + 1] - 1]) and meta int32 [4]
+ * (meta[0] = number of class tokens). shift is 1 when the model does not
+ * embed the class token itself (class_pos + 1, :318-319), else 0; a class
+ * token whose row + shift leaves its request sets status. workspace: at least
+ * vfk_gliner_class_workspace_bytes(total_tokens) bytes of device memory. */
+int64_t vfk_gliner_class_workspace_bytes(int64_t total_tokens);
+int vfk_gliner_class_index(const int64_t* input_ids, int64_t total_tokens,
+                           int64_t ent_token_id, int32_t shift,
+                           const int32_t* cu_seqlens, int32_t num_seqs,
+                           int32_t* class_idx, int32_t* class_cu, int32_t* meta,
+                           int32_t* status, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+
+/* Prompt rows, tok.index_select(0, class_pos) (poolers/gliner.py:321-324):
+ * pe[r] = tok[class_idx[r] + shift] for r < meta[0]. tok [total_tokens,
+ * row_bytes] and pe [max_rows, row_bytes], rows 16-byte aligned, row_bytes a
+ * multiple of 16; max_rows >= meta[0] (read back by the caller). */
+int vfk_gliner_prompt_rows(const void* tok, int64_t row_bytes,
+                           int64_t total_tokens, const int32_t* class_idx,
+                           const int32_t* meta, int32_t shift,
+                           int64_t max_rows, void* pe, void* stream);
+
+/* Word index with first-subtoken pooling (poolers/gliner.py:331-341): among
+ * the tokens of request s with words_mask > 0, the first token p of each run
+ * of equal word ids w gives word_src[word_cu[s] + w - 1] = p + 1.
+ * words_mask int64 [total_tokens]; word_cu int32 [num_seqs + 1] (request s
+ * owns text_lengths = word_cu[s + 1] - word_cu[s] words); word_src int32
+ * [word_cu[num_seqs]], zero-filled by the caller (0 = no token: a zero row,
+ * as in the reference's new_zeros). A word id past its request's text length
+ * sets status. Word ids that repeat after another word id in between give
+ * unordered duplicate writes, as the reference's indexed assignment does. */
+int vfk_gliner_word_index(const int64_t* words_mask, int64_t total_tokens,
+                          const int32_t* cu_seqlens, int32_t num_seqs,
+                          const int32_t* word_cu, int32_t* word_src,
+                          int32_t* status, void* stream);
+
+/* Word rows: we[j] = tok[word_src[j] - 1], or a zero row where
+ * word_src[j] == 0, for j < num_words. Same row rules as
+ * vfk_gliner_prompt_rows. */
+int vfk_gliner_word_rows(const void* tok, int64_t row_bytes,
+                         int64_t total_tokens, const int32_t* word_src,
+                         int64_t num_words, void* we, void* stream);
+
 /* RoPE cos/sin table of transformers' ModernBertRotaryEmbedding (default rope,
  * head_dim 64; the module the reference calls at
  * models/modernbert/modernbert_encoder.py:236-242): out[p][f] = (cos, sin) of

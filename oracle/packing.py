@@ -4,9 +4,13 @@ Restates how the reference finds sequences in vLLM's flat position ids and
 re-pads them for a padded encoder:
   * seq_metadata: models/modernbert/modernbert_encoder.py:505-513 (rule
     "reset") and plugins/deberta_gliner/model.py:166-170 (rule "zero");
-  * gliner_batch / gliner_unbatch: plugins/deberta_gliner/model.py:171-200.
+  * gliner_batch / gliner_unbatch: plugins/deberta_gliner/model.py:171-200;
+  * gliner_reps / gliner_reps_packed: the prompt and word gathers of the
+    GLiNER span pooler, poolers/gliner.py:313-347 (_extract_gliner_reps) per
+    request of the flat stream (poolers/gliner.py:201, :219-255).
 Pinned in tests/test_oracle_packing.py by construction (positions built from
-known lengths), hand cases, a pairwise brute force and round trips.
+known lengths; hidden rows that encode their own index), hand cases, a
+pairwise brute force and round trips.
 """
 from __future__ import annotations
 
@@ -64,3 +68,51 @@ def gliner_batch(input_ids: torch.Tensor, positions: torch.Tensor, pad_id: int =
 def gliner_unbatch(encoded: torch.Tensor, lengths):
     """torch.cat of the valid rows, plugins/deberta_gliner/model.py:197-200."""
     return torch.cat([encoded[row, :n] for row, n in enumerate(lengths)], dim=0)
+
+
+def gliner_reps(tok: torch.Tensor, iid: torch.Tensor, wmask: torch.Tensor, true_len: int,
+                ent_token_id: int, embed_ent_token: bool = True):
+    """_extract_gliner_reps of poolers/gliner.py:313-347 for one request.
+
+    pe: rows of tok at the class tokens (iid == ent_token_id), shifted by one
+    row when the class token itself is not embedded (:317-319); a shifted
+    index past the request raises IndexError like index_select. we [true_len,
+    H]: for the tokens with wmask > 0 in order, word id w = wmask - 1 takes the
+    token's row when w differs from the previous such token's (first-subtoken
+    pooling, :333-341); other rows stay zero. Returns (pe [C, H], we [true_len,
+    H]); the reference's leading batch dim of 1 and its all-ones masks are
+    left out."""
+    H = tok.shape[-1]
+    class_pos = [i for i, v in enumerate(iid.tolist()) if v == ent_token_id]
+    if not embed_ent_token:
+        class_pos = [i + 1 for i in class_pos]
+    if any(i >= tok.shape[0] for i in class_pos):
+        raise IndexError("class token position past the end of the request")
+    pe = tok[class_pos] if class_pos else tok.new_zeros(0, H)
+    we = tok.new_zeros(true_len, H)
+    prev = None
+    for p, w in enumerate(wmask.tolist()):
+        if w <= 0:
+            continue
+        if w - 1 != prev:
+            if w - 1 >= true_len:
+                raise IndexError(f"word id {w} past text length {true_len}")
+            we[w - 1] = tok[p]
+        prev = w - 1
+    return pe, we
+
+
+def gliner_reps_packed(hidden: torch.Tensor, input_ids: torch.Tensor, words_mask: torch.Tensor,
+                       cu_seqlens, text_lengths, ent_token_id: int, embed_ent_token: bool = True):
+    """gliner_reps over each request of a packed stream (split_hidden_states
+    at poolers/gliner.py:201, then the per-request loop :219-255). Returns
+    the lists of per-request pe and we."""
+    cu = [int(c) for c in cu_seqlens]
+    pes, wes = [], []
+    for s in range(len(cu) - 1):
+        a, b = cu[s], cu[s + 1]
+        pe, we = gliner_reps(hidden[a:b], input_ids[a:b], words_mask[a:b], int(text_lengths[s]),
+                             ent_token_id, embed_ent_token)
+        pes.append(pe)
+        wes.append(we)
+    return pes, wes

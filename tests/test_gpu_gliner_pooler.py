@@ -1,0 +1,88 @@
+"""GPU parity of the GLiNER pooler front-end gathers (kernels/gliner_pooler.py)
+against the oracle (oracle/packing.py gliner_reps_packed, the per-request
+_extract_gliner_reps of poolers/gliner.py:313-347). Row gathers: bit-exact."""
+import pytest
+import torch
+
+import workloads
+from oracle import packing as op
+
+pytestmark = pytest.mark.gpu
+
+E = 128001
+
+
+def _check(hidden, ids, wm, cu, tls, embed=True):
+    from kernels.gliner_pooler import extract_gliner_reps, gliner_reps_packed
+    print(f"gliner reps: T={hidden.shape[0]} H={hidden.shape[1]} {hidden.dtype} "
+          f"n={cu.numel() - 1} embed={embed}", flush=True)
+    want_pe, want_we = op.gliner_reps_packed(hidden, ids, wm, cu.tolist(), tls, E, embed)
+    dev = "cuda"
+    pe, pe_cu, we, we_cu = gliner_reps_packed(hidden.to(dev), ids.to(dev), wm.to(dev), cu.to(dev),
+                                              tls, E, embed)
+    torch.cuda.synchronize()
+    assert pe_cu.tolist() == [0] + torch.tensor([p.shape[0] for p in want_pe]).cumsum(0).tolist()
+    assert we_cu.tolist() == [0] + torch.tensor([int(t) for t in tls]).cumsum(0).tolist()
+    assert torch.equal(pe.cpu(), torch.cat(want_pe))
+    assert torch.equal(we.cpu(), torch.cat(want_we))
+    reps = extract_gliner_reps(hidden.to(dev), ids.to(dev), wm.to(dev), cu.to(dev), tls, E, embed)
+    assert len(reps) == len(want_pe)
+    for (p, pm, w, wmk), wp, ww in zip(reps, want_pe, want_we):
+        assert p.shape == (1,) + tuple(wp.shape) and w.shape == (1,) + tuple(ww.shape)
+        assert torch.equal(p[0].cpu(), wp) and torch.equal(w[0].cpu(), ww)
+        assert pm.shape == (1, wp.shape[0]) and bool((pm == 1).all())
+        assert wmk.shape == (1, ww.shape[0]) and bool((wmk == 1).all())
+
+
+@pytest.mark.parametrize("embed", [True, False])
+@pytest.mark.parametrize("dtype, H", [(torch.bfloat16, 768), (torch.float32, 1024),
+                                      (torch.float16, 8)])
+def test_gliner_reps_requests(embed, dtype, H):
+    r = workloads.gliner_requests(24, 120, 300)
+    g = torch.Generator().manual_seed(H)
+    hidden = torch.randn(r.ids.numel(), H, generator=g).to(dtype)
+    _check(hidden, r.ids, r.words_mask, r.cu_seqlens, r.text_lengths, embed)
+
+
+def test_gliner_reps_full_batch():
+    """256 requests of 512-768 tokens (the config-5 stream size), bf16 768."""
+    r = workloads.gliner_requests()
+    hidden = torch.randn(r.ids.numel(), 768, generator=torch.Generator().manual_seed(1)).bfloat16()
+    _check(hidden, r.ids, r.words_mask, r.cu_seqlens, r.text_lengths)
+
+
+def test_gliner_reps_edge_requests():
+    """No class tokens, no words, a zero gap inside a word run (the keep rule
+    looks past it), words that never appear (zero rows), more text length
+    than words, a one-token request, and a long prompt-free run (the
+    look-back crosses many 64-token steps)."""
+    reqs = [
+        ([5, 6, 7], [0, 0, 0], 0),
+        ([E, 9, 3, 11, 12, 13, 14], [0, 0, 0, 1, 0, 1, 2], 2),
+        ([E, 9, E, 8, 3, 11, 12], [0, 0, 0, 0, 0, 2, 2], 4),
+        ([E], [0], 0),
+        ([3] + [11] * 300, [0] * 150 + [1] * 50 + [0] * 100 + [1], 1),
+        ([E, 4, 3] + [11] * 130, [0, 0, 0] + [k // 2 + 1 for k in range(130)], 65),
+    ]
+    ids = torch.tensor(sum((q[0] for q in reqs), []))
+    wm = torch.tensor(sum((q[1] for q in reqs), []))
+    cu = torch.tensor([0] + torch.tensor([len(q[0]) for q in reqs]).cumsum(0).tolist(),
+                      dtype=torch.int32)
+    tls = [q[2] for q in reqs]
+    hidden = torch.randn(ids.numel(), 64, generator=torch.Generator().manual_seed(2)).bfloat16()
+    _check(hidden, ids, wm, cu, tls, embed=True)
+
+
+def test_gliner_reps_errors():
+    """IndexError where the reference's index_select / indexed write raise."""
+    from kernels.gliner_pooler import gliner_reps_packed
+    hidden = torch.randn(6, 64, device="cuda").bfloat16()
+    ids = torch.tensor([E, 3, 11, 3, 11, E], device="cuda")   # request 1 ends on a class token
+    cu = torch.tensor([0, 3, 6], dtype=torch.int32, device="cuda")
+    wm = torch.tensor([0, 0, 1, 0, 1, 0], device="cuda")
+    print("gliner reps: errors", flush=True)
+    gliner_reps_packed(hidden, ids, wm, cu, [1, 1], E, True)
+    with pytest.raises(IndexError, match="class token"):
+        gliner_reps_packed(hidden, ids, wm, cu, [1, 1], E, False)
+    with pytest.raises(IndexError, match="word id"):
+        gliner_reps_packed(hidden, ids, wm, cu, [1, 0], E, True)

@@ -32,7 +32,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     from kernels import _lib
-    assert _lib.load().vfk_abi_version() == 4
+    assert _lib.load().vfk_abi_version() == 5
 
 
 def _host_t5(rel, bidirectional, nb, md):
@@ -142,3 +142,41 @@ def test_packing_argument_checks():
         seq_metadata(torch.arange(5), "other")
     with pytest.raises(RuntimeError, match="GPU only"):
         pad_packed(torch.arange(5), torch.tensor([0, 5]), 1, 5)
+
+
+def test_gliner_front_end_argument_checks():
+    """Rejected before any HIP call, so these run without a GPU."""
+    from kernels import _lib
+    from kernels.gliner_pooler import gliner_reps_packed
+    lib = _lib.load()
+    assert lib.vfk_gliner_class_workspace_bytes(2048) == 8
+    fake = 1 << 20  # never dereferenced: every case below fails its host checks
+    cls = lambda *a: _lib.call("vfk_gliner_class_index", *a)
+    with pytest.raises(ValueError, match="NULL"):
+        cls(None, 10, 5, 0, fake, 1, fake, fake, fake, None, fake, 4, None)
+    with pytest.raises(ValueError, match="total_tokens"):
+        cls(fake, 0, 5, 0, fake, 1, fake, fake, fake, None, fake, 4, None)
+    with pytest.raises(ValueError, match="num_seqs"):
+        cls(fake, 10, 5, 0, fake, 0, fake, fake, fake, None, fake, 4, None)
+    with pytest.raises(ValueError, match="workspace"):
+        cls(fake, 5000, 5, 0, fake, 1, fake, fake, fake, None, fake, 8, None)
+    pr = lambda *a: _lib.call("vfk_gliner_prompt_rows", *a)
+    with pytest.raises(ValueError, match="multiple of 16"):
+        pr(fake, 24, 10, fake, fake, 0, 4, fake, None)
+    with pytest.raises(ValueError, match="aligned"):
+        pr(fake + 8, 32, 10, fake, fake, 0, 4, fake, None)
+    with pytest.raises(ValueError, match="sizes"):
+        pr(fake, 32, 0, fake, fake, 0, 4, fake, None)
+    wi = lambda *a: _lib.call("vfk_gliner_word_index", *a)
+    with pytest.raises(ValueError, match="NULL"):
+        wi(None, 10, fake, 1, fake, fake, None, None)
+    with pytest.raises(ValueError, match="sizes"):
+        wi(fake, 10, fake, 0, fake, fake, None, None)
+    wr = lambda *a: _lib.call("vfk_gliner_word_rows", *a)
+    with pytest.raises(ValueError, match="NULL"):
+        wr(fake, 32, 10, None, 4, fake, None)
+    with pytest.raises(ValueError, match="sizes"):
+        wr(fake, 32, 10, fake, -1, fake, None)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        gliner_reps_packed(torch.zeros(4, 8), torch.zeros(4), torch.zeros(4), torch.tensor([0, 4]),
+                           [1], 5)

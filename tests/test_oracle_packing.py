@@ -141,3 +141,81 @@ def test_gliner_batch_matches_known_lengths(lens):
     for b, L in enumerate(lens):
         hb[b, :L] = h[int(cu[b]):int(cu[b]) + L]
     assert torch.equal(op.gliner_unbatch(hb, got_lens), h)
+
+
+# ------------------------------------------------------- GLiNER prompt / word gathers
+E = 99  # class token id
+
+
+def _index_rows(T, H=4):
+    """Hidden rows that hold their own index: a gathered row names its source."""
+    return torch.arange(T, dtype=D64).unsqueeze(1).repeat(1, H)
+
+
+def _src(rows):
+    return rows[:, 0].long().tolist()
+
+
+@pytest.mark.parametrize("embed, pe_src", [(True, [1, 3]), (False, [2, 4])])
+def test_gliner_reps_hand_case(embed, pe_src):
+    """Prompt '<x> E a E b <sep>' then three subtokens of two words: word 0
+    spans tokens 6-7 (first subtoken 6, not the last one, 7) and word 1 is
+    token 8; the class rows move one token right when the class token itself
+    is not embedded."""
+    ids = torch.tensor([5, E, 7, E, 8, 3, 11, 12, 13])
+    wm = torch.tensor([0, 0, 0, 0, 0, 0, 1, 1, 2])
+    pe, we = op.gliner_reps(_index_rows(9), ids, wm, 2, E, embed)
+    assert _src(pe) == pe_src
+    assert _src(we) == [6, 8]
+
+
+def test_gliner_reps_keep_rule_skips_zero_gaps():
+    """The first-subtoken rule compares with the previous token whose mask is
+    positive, across zeros: mask [1, 0, 1, 2] keeps token 0 for word 0."""
+    _, we = op.gliner_reps(_index_rows(4), torch.zeros(4, dtype=torch.long),
+                           torch.tensor([1, 0, 1, 2]), 2, E)
+    assert _src(we) == [0, 3]
+
+
+def test_gliner_reps_unwritten_words_stay_zero():
+    h = _index_rows(5) + 1.0
+    _, we = op.gliner_reps(h, torch.zeros(5, dtype=torch.long), torch.tensor([0, 2, 2, 4, 0]), 5, E)
+    assert we[:, 0].tolist() == [0.0, 2.0, 0.0, 4.0, 0.0]
+
+
+def test_gliner_reps_errors():
+    """The reference's index_select / indexed write raise on these."""
+    with pytest.raises(IndexError):
+        op.gliner_reps(_index_rows(3), torch.tensor([0, 1, E]), torch.zeros(3, dtype=torch.long),
+                       0, E, embed_ent_token=False)
+    with pytest.raises(IndexError):
+        op.gliner_reps(_index_rows(3), torch.zeros(3, dtype=torch.long), torch.tensor([1, 2, 3]),
+                       2, E)
+
+
+def test_gliner_reps_by_construction():
+    """Requests built from word subtoken counts: word k's row must be the token
+    at prompt_len + (subtokens of words 0..k-1), the class rows the E positions,
+    in a packed stream of several requests."""
+    g = torch.Generator().manual_seed(3)
+    ids, wms, cu, tls, want_pe, want_we = [], [], [0], [], [], []
+    for r in range(6):
+        n_cls = int(torch.randint(0, 5, (1,), generator=g))
+        counts = torch.randint(1, 4, (int(torch.randint(0, 12, (1,), generator=g)),), generator=g)
+        prompt = []
+        for _ in range(n_cls):
+            want_pe.append(cu[-1] + len(prompt))
+            prompt += [E, 7]
+        prompt += [3]
+        start = cu[-1] + len(prompt)
+        firsts = (torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)[:-1]]) + start).tolist()
+        want_we += firsts
+        mask = [0] * len(prompt) + [k + 1 for k, c in enumerate(counts.tolist()) for _ in range(c)]
+        ids += prompt + [11] * int(counts.sum())
+        wms += mask
+        cu.append(cu[-1] + len(mask))
+        tls.append(len(counts))
+    h = _index_rows(cu[-1])
+    pes, wes = op.gliner_reps_packed(h, torch.tensor(ids), torch.tensor(wms), cu, tls, E)
+    assert sum((_src(p) for p in pes), []) == want_pe
+    assert sum((_src(w) for w in wes), []) == want_we

@@ -24,6 +24,12 @@
 // torch.cat of encoded[row, :length]). Sequence b's rows are contiguous in
 // both layouts, so workgroup row b copies len_b rows' bytes as one run and
 // fills the rest of its padded block; no per-element index arithmetic.
+//
+// The GLiNER pooler front-end gathers replace the per-request loop of
+// poolers/gliner.py:219-255 around _extract_gliner_reps (:313-347): the class
+// tokens of all requests are compacted with the same count / scan / write
+// passes, then one wave per row copies prompt rows and first-subtoken word
+// rows.
 #include <stdint.h>
 
 #include <algorithm>
@@ -223,6 +229,199 @@ __global__ __launch_bounds__(256) void unpad_rows_kernel(const U* __restrict__ s
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// GLiNER pooler front-end gathers over a packed stream
+// (poolers/gliner.py:312-345, _extract_gliner_reps, once per request there).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void class_count_kernel(const int64_t* __restrict__ ids, int64_t T,
+                                                          int64_t ent, int32_t* __restrict__ counts) {
+  __shared__ int red[4];
+  const int64_t base = (int64_t)blockIdx.x * kMetaBlock;
+  int c = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t i = base + u * 256 + threadIdx.x;
+    if (i < T && ids[i] == ent) ++c;
+  }
+  for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) counts[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+// Sequence of token p: the last s with cu[s] <= p (cu[0] = 0 <= p).
+__device__ inline int seq_of(const int32_t* cu, int n, int64_t p) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (cu[mid] <= p) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Indices of the class tokens, in stream order, at the scanned block offsets.
+// A class token whose row + shift leaves its request (the reference's
+// index_select on the per-request rows raises there) sets status[0] = 1.
+__global__ __launch_bounds__(256) void class_write_kernel(const int64_t* __restrict__ ids, int64_t T,
+                                                          int64_t ent,
+                                                          const int32_t* __restrict__ offsets,
+                                                          const int32_t* __restrict__ cu, int n,
+                                                          int shift, int32_t* __restrict__ idx,
+                                                          int32_t* __restrict__ status) {
+  __shared__ int red[4];
+  const int64_t base = (int64_t)blockIdx.x * kMetaBlock;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int off = offsets[blockIdx.x];
+  for (int u = 0; u < 4; ++u) {
+    const int64_t i = base + u * 256 + threadIdx.x;
+    const bool hit = i < T && ids[i] == ent;
+    const unsigned long long m = __builtin_amdgcn_ballot_w64(hit);
+    const int before_in_wave = __builtin_popcountll(m & ((1ull << lane) - 1ull));
+    if (lane == 0) red[w] = __builtin_popcountll(m);
+    __syncthreads();
+    int before = before_in_wave;
+    for (int j = 0; j < w; ++j) before += red[j];
+    if (hit) {
+      idx[off + before] = (int32_t)i;
+      const int sq = seq_of(cu, n, i);
+      const int64_t from = i + shift;
+      if (status && (from < cu[sq] || from >= cu[sq + 1])) status[0] = 1;
+    }
+    off += red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+  }
+}
+
+// out_cu[s] = number of class tokens before cu[s] (lower bound in idx).
+__global__ __launch_bounds__(256) void class_cu_kernel(const int32_t* __restrict__ idx,
+                                                       const int32_t* __restrict__ meta,
+                                                       const int32_t* __restrict__ cu, int n,
+                                                       int32_t* __restrict__ out_cu) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  if (s > n) return;
+  const int key = cu[s];
+  int lo = 0, hi = meta[0];
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (idx[mid] < key) lo = mid + 1;
+    else hi = mid;
+  }
+  out_cu[s] = lo;
+}
+
+// One wave per destination row, 16 bytes per lane and pass; all of a
+// lane's loads are issued before its stores. src == nullptr writes zeros.
+template <int MAXC>
+__device__ inline void copy_row(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                int chunks, int lane) {
+  const u32x4_t* sp = reinterpret_cast<const u32x4_t*>(src);
+  u32x4_t* dp = reinterpret_cast<u32x4_t*>(dst);
+  u32x4_t v[MAXC];
+  if (src) {  // clamped, unconditional loads: no per-lane branch around them
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) v[j] = sp[min(lane + 64 * j, chunks - 1)];
+  } else {
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) v[j] = u32x4_t{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int j = 0; j < MAXC; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) dp[c] = v[j];
+  }
+}
+
+// Rows of up to MAXC * 1 KiB (64 lanes x 16 bytes per pass); wider rows loop.
+template <int MAXC>
+__device__ inline void copy_row_any(const uint8_t* src, uint8_t* dst, int64_t row_bytes, int lane) {
+  const int64_t chunks = row_bytes / 16;
+  for (int64_t c0 = 0; c0 < chunks; c0 += 64 * MAXC) {
+    copy_row<MAXC>(src ? src + c0 * 16 : nullptr, dst + c0 * 16,
+                   (int)min<int64_t>(chunks - c0, 64 * MAXC), lane);
+  }
+}
+
+// pe[r] = tok[class_idx[r] + shift] for r < meta[0], the shifted row clamped
+// into the stream (an out-of-request row was flagged by the index pass).
+__global__ __launch_bounds__(256) void prompt_rows_kernel(const uint8_t* __restrict__ tok,
+                                                          int64_t row_bytes, int64_t T,
+                                                          const int32_t* __restrict__ idx,
+                                                          const int32_t* __restrict__ meta, int shift,
+                                                          uint8_t* __restrict__ pe) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= meta[0]) return;
+  const int64_t from = min<int64_t>(max<int64_t>((int64_t)idx[r] + shift, 0), T - 1);
+  copy_row_any<2>(tok + from * row_bytes, pe + r * row_bytes, row_bytes, threadIdx.x & 63);
+}
+
+// One thread per token. Token p with words_mask[p] = w > 0 is the first
+// subtoken of word w when no earlier token of its request has a positive
+// mask, or the nearest one that has holds another word (the reference's
+// keep[1:] = tgt[1:] != tgt[:-1] over the positive-mask tokens). Its index
+// goes to word_src[word_cu[s] + w - 1] as p + 1; a word id past the
+// request's word count sets status[0] = 1 instead (an IndexError in the
+// reference). The predecessor decides almost every token; lanes whose
+// predecessor has mask 0 (the first text token after the prompt, gaps) look
+// further back one at a time with the whole wave, 64 tokens per step.
+__global__ __launch_bounds__(256) void word_index_kernel(const int64_t* __restrict__ wm, int64_t T,
+                                                         const int32_t* __restrict__ cu, int n,
+                                                         const int32_t* __restrict__ word_cu,
+                                                         int32_t* __restrict__ word_src,
+                                                         int32_t* __restrict__ status) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const bool in = p < T;
+  const int64_t w = in ? wm[p] : 0;
+  const bool pos = w > 0;
+  int s = 0;
+  int64_t first = 0;
+  if (pos) {
+    s = seq_of(cu, n, p);
+    first = max<int64_t>(cu[s], 0);
+  }
+  int64_t prev = -1;  // mask of the nearest earlier positive token, 0 if none
+  if (pos) prev = p - 1 >= first ? wm[p - 1] : 0;
+  bool keep = pos && prev != w;
+  unsigned long long todo = __builtin_amdgcn_ballot_w64(pos && prev == 0 && p - 1 >= first);
+  while (todo) {
+    const int l = __builtin_ctzll(todo);
+    todo &= todo - 1;
+    const int64_t pl = __shfl(p, l, 64), fl = __shfl(first, l, 64);
+    int64_t found = 0;
+    for (int64_t hi = pl - 2; hi >= fl; hi -= 64) {
+      const int64_t q = hi - lane;
+      const int64_t v = q >= fl ? wm[q] : 0;
+      const unsigned long long m = __builtin_amdgcn_ballot_w64(v > 0);
+      if (m) {
+        found = __shfl(v, __builtin_ctzll(m), 64);
+        break;
+      }
+    }
+    if (lane == l) keep = found != w;
+  }
+  if (!keep) return;
+  const int64_t slot = w - 1;
+  if (slot >= (int64_t)(word_cu[s + 1] - word_cu[s])) {
+    if (status) status[0] = 1;
+    return;
+  }
+  word_src[word_cu[s] + slot] = (int32_t)(p + 1);
+}
+
+// we[j] = tok[word_src[j] - 1], or zeros where word_src[j] == 0.
+__global__ __launch_bounds__(256) void word_rows_kernel(const uint8_t* __restrict__ tok,
+                                                        int64_t row_bytes, int64_t T,
+                                                        const int32_t* __restrict__ word_src,
+                                                        int64_t W, uint8_t* __restrict__ we) {
+  const int64_t j = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (j >= W) return;
+  const int64_t p = (int64_t)word_src[j] - 1;
+  const uint8_t* src = (p >= 0 && p < T) ? tok + p * row_bytes : nullptr;
+  copy_row_any<2>(src, we + j * row_bytes, row_bytes, threadIdx.x & 63);
+}
+
 }  // namespace vfk
 
 using namespace vfk;
@@ -358,5 +557,91 @@ extern "C" int vfk_unpad_rows(const void* src, int64_t row_bytes, const int32_t*
     case 2: launch_unpad<uint16_t>(src, dst, cu_seqlens, num_seqs, max_len, row_bytes, st); break;
     default: launch_unpad<uint8_t>(src, dst, cu_seqlens, num_seqs, max_len, row_bytes, st); break;
   }
+  return launch_status(name);
+}
+
+extern "C" int64_t vfk_gliner_class_workspace_bytes(int64_t total_tokens) {
+  return vfk_varlen_meta_workspace_bytes(total_tokens);
+}
+
+extern "C" int vfk_gliner_class_index(const int64_t* input_ids, int64_t total_tokens,
+                                      int64_t ent_token_id, int32_t shift,
+                                      const int32_t* cu_seqlens, int32_t num_seqs,
+                                      int32_t* class_idx, int32_t* class_cu, int32_t* meta,
+                                      int32_t* status, void* workspace, int64_t workspace_bytes,
+                                      void* stream) {
+  const char* name = "vfk_gliner_class_index";
+  if (!input_ids || !cu_seqlens || !class_idx || !class_cu || !meta)
+    return set_error(VFK_ERR_INVALID, "%s: NULL pointer", name);
+  if (total_tokens <= 0 || total_tokens >= (1ll << 31) - 1)
+    return set_error(VFK_ERR_INVALID, "%s: total_tokens must be in [1, 2^31 - 2]", name);
+  if (num_seqs <= 0) return set_error(VFK_ERR_INVALID, "%s: num_seqs must be positive", name);
+  const int64_t need = vfk_varlen_meta_workspace_bytes(total_tokens);
+  if (!workspace || workspace_bytes < need)
+    return set_error(VFK_ERR_INVALID, "%s: needs a workspace of %lld bytes", name, (long long)need);
+  const int nblk = ceil_div(total_tokens, kMetaBlock);
+  int32_t* counts = reinterpret_cast<int32_t*>(workspace);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(class_count_kernel, dim3(nblk), dim3(256), 0, st, input_ids, total_tokens,
+                     ent_token_id, counts);
+  hipLaunchKernelGGL(meta_scan_kernel, dim3(1), dim3(1024), 0, st, counts, nblk, total_tokens,
+                     class_idx, meta);
+  hipLaunchKernelGGL(class_write_kernel, dim3(nblk), dim3(256), 0, st, input_ids, total_tokens,
+                     ent_token_id, counts, cu_seqlens, (int)num_seqs, (int)shift, class_idx, status);
+  hipLaunchKernelGGL(class_cu_kernel, dim3(ceil_div(num_seqs + 1, 256)), dim3(256), 0, st, class_idx,
+                     meta, cu_seqlens, num_seqs, class_cu);
+  return launch_status(name);
+}
+
+static int check_rows(const char* name, const void* a, const void* b, int64_t row_bytes) {
+  if (row_bytes <= 0 || row_bytes % 16)
+    return set_error(VFK_ERR_INVALID, "%s: row_bytes must be a positive multiple of 16", name);
+  if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15)
+    return set_error(VFK_ERR_INVALID, "%s: rows must be 16-byte aligned", name);
+  return VFK_OK;
+}
+
+extern "C" int vfk_gliner_prompt_rows(const void* tok, int64_t row_bytes, int64_t total_tokens,
+                                      const int32_t* class_idx, const int32_t* meta, int32_t shift,
+                                      int64_t max_rows, void* pe, void* stream) {
+  const char* name = "vfk_gliner_prompt_rows";
+  if (!tok || !class_idx || !meta || !pe) return set_error(VFK_ERR_INVALID, "%s: NULL pointer", name);
+  if (int rc = check_rows(name, tok, pe, row_bytes)) return rc;
+  if (total_tokens <= 0 || max_rows < 0 || max_rows >= (1ll << 31) - 1)
+    return set_error(VFK_ERR_INVALID, "%s: bad sizes", name);
+  if (max_rows == 0) return VFK_OK;
+  hipLaunchKernelGGL(prompt_rows_kernel, dim3((unsigned)ceil_div(max_rows, 4)), dim3(256), 0,
+                     (hipStream_t)stream, static_cast<const uint8_t*>(tok), row_bytes, total_tokens,
+                     class_idx, meta, (int)shift, static_cast<uint8_t*>(pe));
+  return launch_status(name);
+}
+
+extern "C" int vfk_gliner_word_index(const int64_t* words_mask, int64_t total_tokens,
+                                     const int32_t* cu_seqlens, int32_t num_seqs,
+                                     const int32_t* word_cu, int32_t* word_src, int32_t* status,
+                                     void* stream) {
+  const char* name = "vfk_gliner_word_index";
+  if (!words_mask || !cu_seqlens || !word_cu || !word_src)
+    return set_error(VFK_ERR_INVALID, "%s: NULL pointer", name);
+  if (total_tokens <= 0 || total_tokens >= (1ll << 31) - 1 || num_seqs <= 0)
+    return set_error(VFK_ERR_INVALID, "%s: bad sizes", name);
+  hipLaunchKernelGGL(word_index_kernel, dim3(ceil_div(total_tokens, 256)), dim3(256), 0,
+                     (hipStream_t)stream, words_mask, total_tokens, cu_seqlens, (int)num_seqs,
+                     word_cu, word_src, status);
+  return launch_status(name);
+}
+
+extern "C" int vfk_gliner_word_rows(const void* tok, int64_t row_bytes, int64_t total_tokens,
+                                    const int32_t* word_src, int64_t num_words, void* we,
+                                    void* stream) {
+  const char* name = "vfk_gliner_word_rows";
+  if (!tok || !word_src || !we) return set_error(VFK_ERR_INVALID, "%s: NULL pointer", name);
+  if (int rc = check_rows(name, tok, we, row_bytes)) return rc;
+  if (total_tokens <= 0 || num_words < 0 || num_words >= (1ll << 31) - 1)
+    return set_error(VFK_ERR_INVALID, "%s: bad sizes", name);
+  if (num_words == 0) return VFK_OK;
+  hipLaunchKernelGGL(word_rows_kernel, dim3((unsigned)ceil_div(num_words, 4)), dim3(256), 0,
+                     (hipStream_t)stream, static_cast<const uint8_t*>(tok), row_bytes, total_tokens,
+                     word_src, num_words, static_cast<uint8_t*>(we));
   return launch_status(name);
 }

@@ -17,6 +17,8 @@ with `vllm-factory_amd/` on sys.path gets the HIP implementation:
 plus ops with no reference kernel: varlen_attention.varlen_rope_attention
 (ModernBERT packed local/global attention), packing (sequence boundaries from
 flat position ids and flat <-> padded row copies, on the device),
-rms_norm.RMSNorm, flash_deberta_attention.flash_deberta_attention_fused, and
-colbert_head (final LayerNorm + ColBERT projection + L2 normalisation).
+rms_norm.RMSNorm, flash_deberta_attention.flash_deberta_attention_fused,
+colbert_head (final LayerNorm + ColBERT projection + L2 normalisation), and
+gliner_pooler (the GLiNER span pooler's prompt and word gathers for a whole
+packed batch).
 """

@@ -56,6 +56,12 @@ _SIGNATURES = {
     "vfk_pad_rows": [_vp, _i64, _vp, _i32, _i32, _i32, ctypes.c_uint64, _vp, _vp, _vp],
     "vfk_unpad_rows": [_vp, _i64, _vp, _i32, _i32, _vp, _vp],
     "vfk_varlen_meta_workspace_bytes": [_i64],
+    "vfk_gliner_class_workspace_bytes": [_i64],
+    "vfk_gliner_class_index": [_vp, _i64, _i64, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64,
+                               _vp],
+    "vfk_gliner_prompt_rows": [_vp, _i64, _i64, _vp, _vp, _i32, _i64, _vp, _vp],
+    "vfk_gliner_word_index": [_vp, _i64, _vp, _i32, _vp, _vp, _vp, _vp],
+    "vfk_gliner_word_rows": [_vp, _i64, _i64, _vp, _i64, _vp, _vp],
     "vfk_rope_fwd": [_P, _P, _P, _P, _vp],
     "vfk_layernorm_fwd": [_P, _P, _P, _P, _f32, _P, _P, _vp],
     "vfk_rmsnorm_fwd": [_P, _P, _P, _f32, _P, _P, _vp],
@@ -66,7 +72,8 @@ _SIGNATURES = {
 }
 
 _RESTYPES = {"vfk_varlen_attn_workspace_bytes": ctypes.c_int64,
-             "vfk_varlen_meta_workspace_bytes": ctypes.c_int64}
+             "vfk_varlen_meta_workspace_bytes": ctypes.c_int64,
+             "vfk_gliner_class_workspace_bytes": ctypes.c_int64}
 
 _lib: Optional[ctypes.CDLL] = None
 

@@ -220,3 +220,45 @@ def config5(num_seqs: int = 256, lo: int = 512, hi: int = 768, vocab: int = 5036
     T = int(lengths.sum())
     ids = torch.randint(0, vocab, (T,), generator=g, dtype=torch.int64)
     return EncoderCase(ids, cu_from_lengths(lengths), lengths, int(lengths.max()))
+
+
+# ---------------------------------------------------------------------------
+# GLiNER pooler input (the requests of configs 3 / 5 as GLiNER prompts)
+# ---------------------------------------------------------------------------
+@dataclass
+class GlinerRequests:
+    ids: torch.Tensor           # [T] int64
+    words_mask: torch.Tensor    # [T] int64, word id + 1 on text subtokens, else 0
+    cu_seqlens: torch.Tensor    # int32 [n + 1]
+    text_lengths: list          # words per request
+    ent_token_id: int
+
+
+def gliner_requests(num_seqs: int = 256, lo: int = 512, hi: int = 768, max_labels: int = 25,
+                    ent_token_id: int = 128001, seed: int = 7) -> GlinerRequests:
+    """Packed GLiNER requests in the prompt layout of poolers/gliner.py's
+    callers: per request, U{1..max_labels} labels, each a class token followed
+    by 1-3 label tokens, one separator, then words of 1-3 subtokens each until
+    the request's length U{lo..hi} is reached (the last word may be cut)."""
+    g = torch.Generator().manual_seed(1000 + seed)
+    lengths = _lengths(g, num_seqs, lo, hi)
+    ids, wm, tls = [], [], []
+    for n in lengths.tolist():
+        labels = int(torch.randint(1, max_labels + 1, (1,), generator=g))
+        lab_len = torch.randint(1, 4, (labels,), generator=g).tolist()
+        prompt = []
+        for k in lab_len:
+            prompt += [ent_token_id] + [500 + k] * k
+        prompt = (prompt + [3])[:n]
+        text = n - len(prompt)
+        sub = torch.randint(1, 4, (text + 1,), generator=g).tolist()
+        mask, w = [], 0
+        while len(mask) < text:
+            w += 1
+            mask += [w] * sub[w - 1]
+        mask = mask[:text]
+        ids += prompt + torch.randint(1000, 120000, (text,), generator=g).tolist()
+        wm += [0] * len(prompt) + mask
+        tls.append(w)
+    return GlinerRequests(torch.tensor(ids, dtype=torch.int64), torch.tensor(wm, dtype=torch.int64),
+                          cu_from_lengths(lengths), tls, ent_token_id)
