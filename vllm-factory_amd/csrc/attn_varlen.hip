@@ -55,10 +55,14 @@ __global__ __launch_bounds__(256) void rope_table_kernel(RopeTableArgs a) {
 constexpr int kPenOff = 192;
 constexpr int kPenLen = 2 * kPenOff;
 
-// K rotation pre-pass: block (s, kt) rotates rows [64 kt, 64 kt + 64) of
-// sequence s for every head; thread t handles row t >> 2 and d chunks
-// cp = t & 3 and cp + 4 (the rotate-half partners d and d + 32), loading the
-// row's cos/sin once for all heads.
+// K rotation pre-pass: block (s, kt, g) rotates rows [64 kt, 64 kt + 64) of
+// sequence s for heads [kPackHeads g, kPackHeads g + kPackHeads); thread t
+// handles row t >> 2 and d chunks cp = t & 3 and cp + 4 (the rotate-half
+// partners d and d + 32), loading the row's cos/sin once for its heads. All
+// of a thread's loads are issued before any store, with head indices clamped
+// so that the loads are unconditional; one pass per block, no head loop.
+constexpr int kPackHeads = 6;
+
 template <typename E>
 __global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int nkt) {
   const int kt = blockIdx.x % nkt;
@@ -68,31 +72,27 @@ __global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int nkt)
   const int row = kt * 64 + (threadIdx.x >> 2);
   if (row >= n) return;
   const int cp = threadIdx.x & 3;
+  const int h0 = blockIdx.y * kPackHeads;
   RopeK rk;
   rope_k_fetch(rk, a.rope, row, true);
   const uint16_t* src = reinterpret_cast<const uint16_t*>(a.k) + (int64_t)(tok0 + row) * a.ks[0] + 8 * cp;
   uint16_t* dst = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(a.kr)) +
                   (int64_t)(tok0 + row) * 64 + 8 * cp;
   const int64_t hs = (int64_t)a.T * 64;
-  constexpr int kU = 4;  // heads in flight per thread
-  for (int h0 = 0; h0 < a.H; h0 += kU) {
-    u32x4_t k0[kU], k1[kU];
+  u32x4_t k0[kPackHeads], k1[kPackHeads];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      if (h0 + u < a.H) {
-        const uint16_t* p = src + (int64_t)(h0 + u) * a.ks[1];
-        k0[u] = *reinterpret_cast<const u32x4_t*>(p);
-        k1[u] = *reinterpret_cast<const u32x4_t*>(p + 32);
-      }
-    }
+  for (int u = 0; u < kPackHeads; ++u) {
+    const uint16_t* p = src + (int64_t)min(h0 + u, a.H - 1) * a.ks[1];
+    k0[u] = *reinterpret_cast<const u32x4_t*>(p);
+    k1[u] = *reinterpret_cast<const u32x4_t*>(p + 32);
+  }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      if (h0 + u < a.H) {
-        rope_k_apply<E>(k0[u], k1[u], rk);
-        uint16_t* q = dst + (h0 + u) * hs;
-        *reinterpret_cast<u32x4_t*>(q) = k0[u];
-        *reinterpret_cast<u32x4_t*>(q + 32) = k1[u];
-      }
+  for (int u = 0; u < kPackHeads; ++u) {
+    if (h0 + u < a.H) {
+      rope_k_apply<E>(k0[u], k1[u], rk);
+      uint16_t* q = dst + (h0 + u) * hs;
+      *reinterpret_cast<u32x4_t*>(q) = k0[u];
+      *reinterpret_cast<u32x4_t*>(q + 32) = k1[u];
     }
   }
 }
@@ -394,10 +394,11 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
     const int64_t pblocks = (int64_t)num_seqs * nkt;
     if (pblocks >= (1ll << 31))
       return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: grid too large");
+    const dim3 pgrid((unsigned)pblocks, (unsigned)ceil_div(H, kPackHeads));
     if (dt == VFK_BF16)
-      hipLaunchKernelGGL(rope_k_pack_kernel<BF16>, dim3((unsigned)pblocks), dim3(256), 0, st, a, nkt);
+      hipLaunchKernelGGL(rope_k_pack_kernel<BF16>, pgrid, dim3(256), 0, st, a, nkt);
     else
-      hipLaunchKernelGGL(rope_k_pack_kernel<F16>, dim3((unsigned)pblocks), dim3(256), 0, st, a, nkt);
+      hipLaunchKernelGGL(rope_k_pack_kernel<F16>, pgrid, dim3(256), 0, st, a, nkt);
   }
   if (a.window >= 0 && a.window >= max_seqlen) a.window = -1;  // window covers every pair
   if (a.window > kPenOff - kBM)
