@@ -148,3 +148,49 @@ def test_fused_strided_views_and_out(dev):
     for b, n in enumerate(lens.tolist()):
         assert_attn_close(got[b, :, :n], want[b, :, :n], f"strided b={b}")
         assert torch.all(buf[b, n:] == 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("log_bucket", [True, False])
+def test_gather_staged_vs_oracle(dev, dtype, log_bucket):
+    """Row-contiguous pos tensors with 2S >= 136 take the LDS-staged gather:
+    partial query and key tiles (L = 300), a short sequence, windows clamped at
+    both ends of the 2S columns (S = 128 < L)."""
+    q, k, v, kr, qr, lens = _case(2, 3, 300, 128, dtype, 6, lens=[300, 77])
+    pk, pq = oa.deberta_position_projections(q, k, kr, qr)
+    pk, pq = pk.to(dtype), pq.to(dtype)
+    want = oa.deberta_flash_attention(q, k, v, lens, pk, pq, SM, 128, 256, log_bucket)
+    print(f"deberta staged gather {dtype} log={log_bucket}", flush=True)
+    got = _k().flash_deberta_attention(q.to(dev), k.to(dev), v.to(dev), lens.to(dev), pk.to(dev),
+                                       pq.to(dev), False, SM, 128, 256, log_bucket)
+    assert_attn_close(got[0], want[0], f"staged {dtype} log={log_bucket} b=0")
+    assert_attn_close(got[1, :, :77], want[1, :, :77], f"staged {dtype} log={log_bucket} b=1")
+    assert torch.all(got[1, :, 77:] == 0)
+
+
+def test_gather_staged_equals_unstaged(dev):
+    """The staged and the per-score gather read the same bias values in the
+    same order: bit-equal outputs. Pos tensors viewed out of [.., 2S + 1]
+    buffers (row stride not a multiple of 8) take the per-score gather."""
+    q, k, v, kr, qr, lens = _case(3, 2, 384, 256, torch.bfloat16, 7, lens=[384, 200, 5])
+    pk, pq = oa.deberta_position_projections(q, k, kr, qr)
+    pk, pq = pk.bfloat16().to(dev), pq.bfloat16().to(dev)
+    wide = lambda t: torch.cat([t, t[..., :1]], -1)[..., :t.shape[-1]]
+    pk_w, pq_w = wide(pk), wide(pq)
+    assert pk_w.stride(2) % 8 != 0
+    args = (q.to(dev), k.to(dev), v.to(dev), lens.to(dev))
+    print("deberta staged vs unstaged", flush=True)
+    a = _k().flash_deberta_attention(*args, pk, pq, False, SM, 256, 512, True)
+    b = _k().flash_deberta_attention(*args, pk_w, pq_w, False, SM, 256, 512, True)
+    assert torch.equal(a, b)
+
+
+def test_gather_staged_causal(dev):
+    q, k, v, kr, qr, lens = _case(2, 2, 260, 96, torch.bfloat16, 8, lens=[260, 260])
+    pk, pq = oa.deberta_position_projections(q, k, kr, qr)
+    pk, pq = pk.bfloat16(), pq.bfloat16()
+    want = oa.deberta_flash_attention(q, k, v, None, pk, pq, SM, 96, 192, True, causal=True)
+    print("deberta staged causal", flush=True)
+    got = _k().flash_deberta_attention(q.to(dev), k.to(dev), v.to(dev), None, pk.to(dev),
+                                       pq.to(dev), True, SM, 96, 192, True)
+    assert_attn_close(got, want, "staged causal")

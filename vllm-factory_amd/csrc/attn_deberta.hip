@@ -133,6 +133,157 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_kernel(DebArgs a) {
   }
 }
 
+// Staged form of deberta_gather_kernel for row-contiguous pos tensors. The
+// gather above issues two 2-byte loads per score, spread over 32 rows per
+// instruction. Here each key tile first copies, with 16-byte loads, the
+// column windows it needs into LDS: c(i - j) is non-decreasing in i - j with
+// steps of at most 1, so the 64 keys of a tile meet at most 64 consecutive
+// pos_key columns of a query row, and the 128 query rows of the workgroup
+// meet at most 128 consecutive pos_query columns of a key row. Windows start
+// on an 8-column boundary (kPkW = 64 + 8, kPqW = 128 + 8) and are clamped
+// into [0, 2S). The scores then read their biases from LDS.
+constexpr int kPkW = kBN + 8;        // staged pos_key columns per query row
+constexpr int kPqW = kBM + 8;        // staged pos_query columns per key row
+constexpr int kPkChunks = kPkW / 8;  // 16-byte chunks per staged row
+constexpr int kPqChunks = kPqW / 8;
+
+__host__ __device__ constexpr size_t deb_staged_lds(int lut_len) {
+  return (size_t)(kKsElems + kVtElems + kBM * kPkW + kBN * kPqW) * 2 + (size_t)(kBM + kBN) * 4 +
+         (size_t)lut_len * 2;
+}
+
+template <typename E>
+__global__ __launch_bounds__(256, 2) void deberta_gather_staged_kernel(DebArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);
+  uint16_t* Vt = Ks + kKsElems;
+  uint16_t* PKs = Vt + kVtElems;                            // [kBM][kPkW]
+  uint16_t* PQs = PKs + kBM * kPkW;                         // [kBN][kPqW]
+  int* pko = reinterpret_cast<int*>(PQs + kBN * kPqW);      // [kBM] row * kPkW - window start
+  int* pqo = pko + kBM;                                     // [kBN] row * kPqW - window start
+  int16_t* lut = reinterpret_cast<int16_t*>(pqo + kBN);    // c(i - j)
+
+  const int nqt = (a.M + kBM - 1) / kBM;
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = work % nqt;
+  const int bh = work / nqt;
+  const int h = bh % a.H, b = bh / a.H;
+  const int q0 = qt * kBM;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, hl = lane >> 5;
+  const int len = a.seq_lengths ? min(max(a.seq_lengths[b], 0), a.N) : a.N;
+  const int qrow = q0 + w * 32 + (lane & 31);
+  const bool qstore = qrow < a.M;
+  const bool qvalid = qrow < min(len, a.M);
+  uint16_t* orow = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1] + (int64_t)qrow * a.os[2];
+
+  int kend = len;
+  if (a.causal) kend = min(kend, min(q0 + kBM, a.M) + (a.N - a.M));
+  const int kt_end = (max(kend, 0) + kBN - 1) / kBN;
+  if (q0 >= len || kt_end == 0) {
+    if (qstore) {
+      f32x16_t z = {};
+      store_out<E>(orow, z, z, 0.f);
+    }
+    return;
+  }
+
+  const int dmin = q0 - (kt_end * kBN - 1);
+  for (int e = t; e < a.lut_len; e += 256) lut[e] = (int16_t)deb_index(a, dmin + e);
+
+  const uint16_t* Qp = reinterpret_cast<const uint16_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const uint16_t* Kp = reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
+  const uint16_t* Vp = reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
+  const uint16_t* PKp = reinterpret_cast<const uint16_t*>(a.pk) + b * a.pks[0] + h * a.pks[1];
+  const uint16_t* PQp = reinterpret_cast<const uint16_t*>(a.pq) + b * a.pqs[0] + h * a.pqs[1];
+  const int span2 = 2 * a.span;
+
+  u32x4_t qf[4];
+  load_q(qf, Qp + (int64_t)qrow * a.qs[2], qvalid);
+  float m = -INFINITY, l = 0.f;
+  f32x16_t o0 = {}, o1 = {};
+  const int lut_lane = qrow - 4 * hl - dmin;
+  const int prow = w * 32 + (lane & 31);  // this lane's staged pos_key row
+
+  KVStage st;
+  kv_load(st, Kp, a.ks[2], Vp, a.vs[2], 0, kend);
+  __syncthreads();  // lut ready
+  for (int kt = 0; kt < kt_end; ++kt) {
+    const int key0 = kt * kBN;
+    // pos windows of this tile: global -> registers (clamped rows and
+    // chunks, so every load is unconditional; surplus chunks are not stored)
+    u32x4_t pkv[5], pqv[5];
+#pragma unroll
+    for (int u = 0; u < 5; ++u) {
+      const int c = min(t + 256 * u, kBM * kPkChunks - 1);
+      const int r = c / kPkChunks, j = c - r * kPkChunks;
+      const int cmin = lut[q0 + r - key0 - (kBN - 1) - dmin];
+      const int start = min(cmin & ~7, span2 - kPkW);
+      pkv[u] = *reinterpret_cast<const u32x4_t*>(PKp + (int64_t)min(q0 + r, a.M - 1) * a.pks[2] +
+                                                 start + 8 * j);
+    }
+#pragma unroll
+    for (int u = 0; u < 5; ++u) {
+      const int c = min(t + 256 * u, kBN * kPqChunks - 1);
+      const int r = c / kPqChunks, j = c - r * kPqChunks;
+      const int cmin = lut[q0 - key0 - r - dmin];
+      const int start = min(cmin & ~7, span2 - kPqW);
+      pqv[u] = *reinterpret_cast<const u32x4_t*>(PQp + (int64_t)min(key0 + r, a.N - 1) * a.pqs[2] +
+                                                 start + 8 * j);
+    }
+    kv_store(st, Ks, Vt);
+    if (t < kBM) {
+      const int cmin = lut[q0 + t - key0 - (kBN - 1) - dmin];
+      pko[t] = t * kPkW - min(cmin & ~7, span2 - kPkW);
+    } else if (t < kBM + kBN) {
+      const int r = t - kBM;
+      const int cmin = lut[q0 - key0 - r - dmin];
+      pqo[r] = r * kPqW - min(cmin & ~7, span2 - kPqW);
+    }
+    __syncthreads();
+    if (kt + 1 < kt_end) kv_load(st, Kp, a.ks[2], Vp, a.vs[2], (kt + 1) * kBN, kend);
+
+    f32x16_t s0, s1;
+    qk_tile<E>(Ks, qf, s0, s1);
+#pragma unroll
+    for (int u = 0; u < 5; ++u) {
+      const int c = t + 256 * u;
+      if (c < kBM * kPkChunks) {
+        const int r = c / kPkChunks, j = c - r * kPkChunks;
+        *reinterpret_cast<u32x4_t*>(PKs + r * kPkW + 8 * j) = pkv[u];
+      }
+      if (c < kBN * kPqChunks) {
+        const int r = c / kPqChunks, j = c - r * kPqChunks;
+        *reinterpret_cast<u32x4_t*>(PQs + r * kPqW + 8 * j) = pqv[u];
+      }
+    }
+    __syncthreads();
+
+    const int16_t* lp = lut + (lut_lane - key0);
+    const uint16_t* pkr = PKs + pko[prow];
+    map_scores(s0, s1, [&](int e, float v) {
+      const int xk = x_key(e, 0);  // key - key0 - 4*hl
+      const int kr = xk + 4 * hl;
+      const int key = key0 + kr;
+      const int c = lp[-xk];
+      v += E::to_f32(pkr[c]) + E::to_f32(PQs[pqo[kr] + c]);
+      return (key >= kend || (a.causal && key > qrow + (a.N - a.M))) ? -INFINITY : v;
+    });
+    u32x4_t p[4];
+    softmax_tile<E>(s0, s1, a.c2, m, l, o0, o1, p);
+    pv_tile<E>(Vt, p, o0, o1);
+    __syncthreads();
+  }
+  const float l_tot = half_swap_sum(l);
+  if (qstore) {
+    if (!qvalid) {
+      f32x16_t z = {};
+      store_out<E>(orow, z, z, 0.f);
+    } else {
+      store_out<E>(orow, o0, o1, l_tot);
+    }
+  }
+}
+
 // fp32: one thread per query row.
 __global__ __launch_bounds__(64) void deberta_gather_f32_kernel(DebArgs a) {
   __shared__ float Kt[64][kHD + 1];
@@ -601,6 +752,21 @@ extern "C" int vfk_flash_deberta_fwd(const vfk_tensor* q, const vfk_tensor* k, c
   if (lds > 160 * 1024) return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_deberta_fwd: N too large");
   const int nqt = ceil_div(a.M, kBM);
   dim3 grid((unsigned)(nqt * a.B * a.H));
+  // staged form: both pos tensors with contiguous, 16-byte aligned rows, a
+  // span whose 2S columns hold the widest window, and LDS within 64 KB
+  auto rows16 = [](const void* p, const int64_t* s) {
+    return s[3] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 &&
+           (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+  };
+  const size_t slds = deb_staged_lds(a.lut_len);
+  if (a.pk && a.pq && rows16(a.pk, a.pks) && rows16(a.pq, a.pqs) && a.span % 4 == 0 &&
+      2 * a.span >= kPqW && slds <= 64 * 1024) {
+    if (q->dtype == VFK_BF16)
+      hipLaunchKernelGGL(deberta_gather_staged_kernel<BF16>, grid, dim3(256), slds, st, a);
+    else
+      hipLaunchKernelGGL(deberta_gather_staged_kernel<F16>, grid, dim3(256), slds, st, a);
+    return launch_status("vfk_flash_deberta_fwd");
+  }
   if (q->dtype == VFK_BF16)
     hipLaunchKernelGGL(deberta_gather_kernel<BF16>, grid, dim3(256), lds, st, a);
   else
