@@ -86,3 +86,19 @@ def test_gliner_reps_errors():
         gliner_reps_packed(hidden, ids, wm, cu, [1, 1], E, False)
     with pytest.raises(IndexError, match="word id"):
         gliner_reps_packed(hidden, ids, wm, cu, [1, 0], E, True)
+
+
+def test_gliner_reps_list_and_int32_inputs():
+    """input_ids / words_mask as host lists or int32 tensors, as the
+    reference's _to_tensor accepts them: same rows as int64 device tensors."""
+    from kernels.gliner_pooler import gliner_reps_packed
+    r = workloads.gliner_requests(6, 120, 200)
+    hidden = torch.randn(r.ids.numel(), 64, generator=torch.Generator().manual_seed(4)).bfloat16()
+    h, cu = hidden.to("cuda"), r.cu_seqlens.to("cuda")
+    print("gliner reps: list / int32 inputs", flush=True)
+    base = gliner_reps_packed(h, r.ids.to("cuda"), r.words_mask.to("cuda"), cu, r.text_lengths, E)
+    for ids, wm in ((r.ids.tolist(), r.words_mask.tolist()),
+                    (r.ids.int(), r.words_mask.int().to("cuda"))):
+        got = gliner_reps_packed(h, ids, wm, cu, r.text_lengths, E)
+        assert torch.equal(got[0], base[0]) and torch.equal(got[2], base[2])
+        assert torch.equal(got[1], base[1]) and torch.equal(got[3], base[3])

@@ -24,8 +24,10 @@ import torch
 from . import _lib
 
 
-def _stream_i64(x: torch.Tensor, dev, T: int, name: str) -> torch.Tensor:
-    x = x.reshape(-1)
+def _stream_i64(x, dev, T: int, name: str) -> torch.Tensor:
+    """A tensor or list of ids as contiguous int64 on the device (the
+    reference's _to_tensor(..., dtype=torch.long), poolers/gliner.py:349-357)."""
+    x = torch.as_tensor(x).reshape(-1)
     if x.numel() != T:
         raise ValueError(f"{name} has {x.numel()} entries, the hidden stream {T} rows")
     return x.to(device=dev, dtype=torch.int64).contiguous()
@@ -37,7 +39,8 @@ def gliner_reps_packed(hidden: torch.Tensor, input_ids: torch.Tensor, words_mask
     """Prompt and word representations of every request of a packed stream.
 
     hidden [T, H] (any dtype, H * itemsize a multiple of 16), input_ids and
-    words_mask [T] (cast to int64 as the reference's _to_tensor does),
+    words_mask [T] (tensors of any integer dtype, on any device, or lists;
+    cast to int64 as the reference's _to_tensor does),
     cu_seqlens int32 [n + 1] on the device (request s owns rows cu[s] ..
     cu[s + 1] - 1), text_lengths: n word counts (the reference's
     text_lengths). Returns (pe [C, H], pe_cu int64 [n + 1] on the host, we
