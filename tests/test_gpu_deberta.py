@@ -168,9 +168,11 @@ def test_gather_staged_vs_oracle(dev, dtype, log_bucket):
     assert torch.all(got[1, :, 77:] == 0)
 
 
-def test_gather_staged_equals_unstaged(dev):
+@pytest.mark.parametrize("which", ["both", "c2p", "p2c"])
+def test_gather_staged_equals_unstaged(dev, which):
     """The staged and the per-score gather read the same bias values in the
-    same order: bit-equal outputs. Pos tensors viewed out of [.., 2S + 1]
+    same order: bit-equal outputs, with both pos tensors or only one of them
+    (pos_att_type c2p or p2c alone). Pos tensors viewed out of [.., 2S + 1]
     buffers (row stride not a multiple of 8) take the per-score gather."""
     q, k, v, kr, qr, lens = _case(3, 2, 384, 256, torch.bfloat16, 7, lens=[384, 200, 5])
     pk, pq = oa.deberta_position_projections(q, k, kr, qr)
@@ -179,7 +181,11 @@ def test_gather_staged_equals_unstaged(dev):
     pk_w, pq_w = wide(pk), wide(pq)
     assert pk_w.stride(2) % 8 != 0
     args = (q.to(dev), k.to(dev), v.to(dev), lens.to(dev))
-    print("deberta staged vs unstaged", flush=True)
+    if which == "c2p":
+        pq = pq_w = None
+    if which == "p2c":
+        pk = pk_w = None
+    print(f"deberta staged vs unstaged ({which})", flush=True)
     a = _k().flash_deberta_attention(*args, pk, pq, False, SM, 256, 512, True)
     b = _k().flash_deberta_attention(*args, pk_w, pq_w, False, SM, 256, 512, True)
     assert torch.equal(a, b)
@@ -194,3 +200,15 @@ def test_gather_staged_causal(dev):
     got = _k().flash_deberta_attention(q.to(dev), k.to(dev), v.to(dev), None, pk.to(dev),
                                        pq.to(dev), True, SM, 96, 192, True)
     assert_attn_close(got, want, "staged causal")
+
+
+def test_gather_staged_c2p_only_vs_oracle(dev):
+    q, k, v, kr, qr, lens = _case(2, 2, 200, 128, torch.bfloat16, 9, lens=[200, 131])
+    pk, _ = oa.deberta_position_projections(q, k, kr, qr)
+    pk = pk.bfloat16()
+    want = oa.deberta_flash_attention(q, k, v, lens, pk, None, SM, 128, 256, True)
+    print("deberta staged c2p only", flush=True)
+    got = _k().flash_deberta_attention(q.to(dev), k.to(dev), v.to(dev), lens.to(dev), pk.to(dev),
+                                       None, False, SM, 128, 256, True)
+    assert_attn_close(got[0], want[0], "staged c2p-only b=0")
+    assert_attn_close(got[1, :, :131], want[1, :, :131], "staged c2p-only b=1")

@@ -152,7 +152,7 @@ __host__ __device__ constexpr size_t deb_staged_lds(int lut_len) {
          (size_t)lut_len * 2;
 }
 
-template <typename E>
+template <typename E, bool PK, bool PQ>
 __global__ __launch_bounds__(256, 2) void deberta_gather_staged_kernel(DebArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);
@@ -193,8 +193,8 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_staged_kernel(DebArgs a
   const uint16_t* Qp = reinterpret_cast<const uint16_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
   const uint16_t* Kp = reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
   const uint16_t* Vp = reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
-  const uint16_t* PKp = reinterpret_cast<const uint16_t*>(a.pk) + b * a.pks[0] + h * a.pks[1];
-  const uint16_t* PQp = reinterpret_cast<const uint16_t*>(a.pq) + b * a.pqs[0] + h * a.pqs[1];
+  const uint16_t* PKp = PK ? reinterpret_cast<const uint16_t*>(a.pk) + b * a.pks[0] + h * a.pks[1] : nullptr;
+  const uint16_t* PQp = PQ ? reinterpret_cast<const uint16_t*>(a.pq) + b * a.pqs[0] + h * a.pqs[1] : nullptr;
   const int span2 = 2 * a.span;
 
   u32x4_t qf[4];
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_staged_kernel(DebArgs a
     // chunks, so every load is unconditional; surplus chunks are not stored)
     u32x4_t pkv[5], pqv[5];
 #pragma unroll
-    for (int u = 0; u < 5; ++u) {
+    for (int u = 0; u < 5 && PK; ++u) {
       const int c = min(t + 256 * u, kBM * kPkChunks - 1);
       const int r = c / kPkChunks, j = c - r * kPkChunks;
       const int cmin = lut[q0 + r - key0 - (kBN - 1) - dmin];
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_staged_kernel(DebArgs a
                                                  start + 8 * j);
     }
 #pragma unroll
-    for (int u = 0; u < 5; ++u) {
+    for (int u = 0; u < 5 && PQ; ++u) {
       const int c = min(t + 256 * u, kBN * kPqChunks - 1);
       const int r = c / kPqChunks, j = c - r * kPqChunks;
       const int cmin = lut[q0 - key0 - r - dmin];
@@ -231,10 +231,10 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_staged_kernel(DebArgs a
                                                  start + 8 * j);
     }
     kv_store(st, Ks, Vt);
-    if (t < kBM) {
+    if (PK && t < kBM) {
       const int cmin = lut[q0 + t - key0 - (kBN - 1) - dmin];
       pko[t] = t * kPkW - min(cmin & ~7, span2 - kPkW);
-    } else if (t < kBM + kBN) {
+    } else if (PQ && t >= kBM && t < kBM + kBN) {
       const int r = t - kBM;
       const int cmin = lut[q0 - key0 - r - dmin];
       pqo[r] = r * kPqW - min(cmin & ~7, span2 - kPqW);
@@ -247,11 +247,11 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_staged_kernel(DebArgs a
 #pragma unroll
     for (int u = 0; u < 5; ++u) {
       const int c = t + 256 * u;
-      if (c < kBM * kPkChunks) {
+      if (PK && c < kBM * kPkChunks) {
         const int r = c / kPkChunks, j = c - r * kPkChunks;
         *reinterpret_cast<u32x4_t*>(PKs + r * kPkW + 8 * j) = pkv[u];
       }
-      if (c < kBN * kPqChunks) {
+      if (PQ && c < kBN * kPqChunks) {
         const int r = c / kPqChunks, j = c - r * kPqChunks;
         *reinterpret_cast<u32x4_t*>(PQs + r * kPqW + 8 * j) = pqv[u];
       }
@@ -259,13 +259,16 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_staged_kernel(DebArgs a
     __syncthreads();
 
     const int16_t* lp = lut + (lut_lane - key0);
-    const uint16_t* pkr = PKs + pko[prow];
+    const uint16_t* pkr = PKs + (PK ? pko[prow] : 0);
     map_scores(s0, s1, [&](int e, float v) {
       const int xk = x_key(e, 0);  // key - key0 - 4*hl
       const int kr = xk + 4 * hl;
       const int key = key0 + kr;
       const int c = lp[-xk];
-      v += E::to_f32(pkr[c]) + E::to_f32(PQs[pqo[kr] + c]);
+      float bias = 0.f;  // summed as the per-score gather does: bit-equal
+      if (PK) bias += E::to_f32(pkr[c]);
+      if (PQ) bias += E::to_f32(PQs[pqo[kr] + c]);
+      v += bias;
       return (key >= kend || (a.causal && key > qrow + (a.N - a.M))) ? -INFINITY : v;
     });
     u32x4_t p[4];
@@ -759,12 +762,21 @@ extern "C" int vfk_flash_deberta_fwd(const vfk_tensor* q, const vfk_tensor* k, c
            (reinterpret_cast<uintptr_t>(p) & 15) == 0;
   };
   const size_t slds = deb_staged_lds(a.lut_len);
-  if (a.pk && a.pq && rows16(a.pk, a.pks) && rows16(a.pq, a.pqs) && a.span % 4 == 0 &&
-      2 * a.span >= kPqW && slds <= 64 * 1024) {
-    if (q->dtype == VFK_BF16)
-      hipLaunchKernelGGL(deberta_gather_staged_kernel<BF16>, grid, dim3(256), slds, st, a);
-    else
-      hipLaunchKernelGGL(deberta_gather_staged_kernel<F16>, grid, dim3(256), slds, st, a);
+  if ((a.pk || a.pq) && (!a.pk || rows16(a.pk, a.pks)) && (!a.pq || rows16(a.pq, a.pqs)) &&
+      a.span % 4 == 0 && 2 * a.span >= kPqW && slds <= 64 * 1024) {
+#define VFK_DEB_STAGED(E)                                                                         \
+  if (a.pk && a.pq)                                                                               \
+    hipLaunchKernelGGL((deberta_gather_staged_kernel<E, true, true>), grid, dim3(256), slds, st, a); \
+  else if (a.pk)                                                                                  \
+    hipLaunchKernelGGL((deberta_gather_staged_kernel<E, true, false>), grid, dim3(256), slds, st, a); \
+  else                                                                                            \
+    hipLaunchKernelGGL((deberta_gather_staged_kernel<E, false, true>), grid, dim3(256), slds, st, a);
+    if (q->dtype == VFK_BF16) {
+      VFK_DEB_STAGED(BF16)
+    } else {
+      VFK_DEB_STAGED(F16)
+    }
+#undef VFK_DEB_STAGED
     return launch_status("vfk_flash_deberta_fwd");
   }
   if (q->dtype == VFK_BF16)
