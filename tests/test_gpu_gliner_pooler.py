@@ -86,6 +86,9 @@ def test_gliner_reps_errors():
         gliner_reps_packed(hidden, ids, wm, cu, [1, 1], E, False)
     with pytest.raises(IndexError, match="word id"):
         gliner_reps_packed(hidden, ids, wm, cu, [1, 0], E, True)
+    with pytest.raises(ValueError, match="cu_seqlens"):
+        gliner_reps_packed(hidden, ids, wm, torch.tensor([0, 3, 5], dtype=torch.int32,
+                                                         device="cuda"), [1, 1], E, True)
 
 
 def test_gliner_reps_list_and_int32_inputs():

@@ -77,8 +77,9 @@ def gliner_reps_packed(hidden: torch.Tensor, input_ids: torch.Tensor, words_mask
     # first subtoken of every word; both flag the reference's IndexErrors in
     # aux[n + 1:], read back with the class offsets in one copy.
     class_idx = torch.empty(T + 1, dtype=torch.int32, device=dev)
-    aux = torch.zeros(n + 3, dtype=torch.int32, device=dev)
-    class_cu, status = aux[:n + 1], aux[n + 1:]
+    aux = torch.zeros(n + 5, dtype=torch.int32, device=dev)
+    class_cu, status = aux[:n + 1], aux[n + 1:n + 3]
+    aux[n + 3:] = cu[[0, n]]  # endpoints, checked with the same read-back
     meta = torch.empty(4, dtype=torch.int32, device=dev)
     ws_bytes = int(lib.vfk_gliner_class_workspace_bytes(T))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
@@ -92,6 +93,9 @@ def gliner_reps_packed(hidden: torch.Tensor, input_ids: torch.Tensor, words_mask
         _lib.on_device("vfk_gliner_word_index", dev, wm.data_ptr(), T, cu.data_ptr(), n,
                        wcu.data_ptr(), word_src.data_ptr(), status.data_ptr() + 4)
     host = aux.cpu()
+    if int(host[n + 3]) != 0 or int(host[n + 4]) != T:
+        raise ValueError(f"cu_seqlens must run from 0 to the {T} hidden rows, got "
+                         f"{int(host[n + 3])} .. {int(host[n + 4])}")
     if host[n + 1]:
         raise IndexError("index out of range: a shifted class token lies past its request")
     if host[n + 2]:
