@@ -318,6 +318,23 @@ def epilogue_bench(torch, args, c2):
         "vfk_gliner_word_rows", dev, hg.data_ptr(), row, Tg, src.data_ptr(), W, we.data_ptr()),
         4 * W + 2 * W * row)
     res["gliner_reps"].update(tokens=Tg, class_rows=C, word_rows=W)
+    # SpanMarkerV0 pair rows for the same 256 requests: default spans of
+    # width 12 over each request's word rows, relu(cat(start[i], end[j]))
+    # written as [S, 1536] bf16 (the projections are random rows here)
+    from kernels.gliner_pooler import default_spans, gliner_span_rows
+    lens_w = [int(t) for t in gr.text_lengths]
+    sp = [default_spans(n, n, 12) for n in lens_w]
+    s_idx = torch.cat([x[0] for x in sp]).to(dev)
+    s_mask = torch.cat([x[1] for x in sp]).to(dev)
+    row_cu = we_cu.to(device=dev, dtype=torch.int32)
+    span_cu = torch.tensor([0] + torch.tensor([x[0].shape[0] for x in sp]).cumsum(0).tolist(),
+                           dtype=torch.int32, device=dev)
+    S = int(span_cu[-1])
+    st_rep = torch.randn(W, 768, generator=g).bfloat16().to(dev)
+    en_rep = torch.randn(W, 768, generator=g).bfloat16().to(dev)
+    bench("gliner_span_rows", lambda: gliner_span_rows(st_rep, en_rep, row_cu, s_idx, s_mask, span_cu),
+          S * (2 * row + 24) + 2 * W * row)
+    res["gliner_span_rows"].update(spans=S)
     return res
 
 

@@ -268,6 +268,24 @@ int vfk_gliner_word_rows(const void* tok, int64_t row_bytes,
                          int64_t total_tokens, const int32_t* word_src,
                          int64_t num_words, void* we, void* stream);
 
+/* Span pair rows of the GLiNER span marker (SpanMarkerV0.forward with
+ * extract_elements, poolers/gliner.py:40-45, :131-145; called at :286-287):
+ * for span s of request r (span_cu[r] <= s < span_cu[r + 1]) over r's
+ * L = row_cu[r + 1] - row_cu[r] rows of start_rep / end_rep,
+ * out[s] = relu(cat(start_rep[row_cu[r] + i], end_rep[row_cu[r] + j])) with
+ * i, j = span_idx[s][0 / 1] * (span_mask[s] != 0) clamped to [0, L - 1].
+ * start_rep, end_rep [num_rows = row_cu[num_requests], row_bytes] and out [num_spans,
+ * 2 * row_bytes] of dtype VFK_BF16 / VFK_F16 / VFK_F32, rows 16-byte aligned,
+ * row_bytes a multiple of 16; span_idx int64 [num_spans, 2], span_mask int64
+ * [num_spans], row_cu / span_cu int32 [num_requests + 1]. ReLU maps negative
+ * values to +0 and keeps NaN. A request with L == 0 gives zero rows. */
+int vfk_gliner_span_rows(const void* start_rep, const void* end_rep,
+                         int64_t row_bytes, int64_t num_rows, int32_t dtype,
+                         const int32_t* row_cu,
+                         int32_t num_requests, const int64_t* span_idx,
+                         const int64_t* span_mask, const int32_t* span_cu,
+                         int64_t num_spans, void* out, void* stream);
+
 /* RoPE cos/sin table of transformers' ModernBertRotaryEmbedding (default rope,
  * head_dim 64; the module the reference calls at
  * models/modernbert/modernbert_encoder.py:236-242): out[p][f] = (cos, sin) of

@@ -7,7 +7,10 @@ re-pads them for a padded encoder:
   * gliner_batch / gliner_unbatch: plugins/deberta_gliner/model.py:171-200;
   * gliner_reps / gliner_reps_packed: the prompt and word gathers of the
     GLiNER span pooler, poolers/gliner.py:313-347 (_extract_gliner_reps) per
-    request of the flat stream (poolers/gliner.py:201, :219-255).
+    request of the flat stream (poolers/gliner.py:201, :219-255);
+  * gliner_default_spans / gliner_span_rows: the pooler's default span list
+    (poolers/gliner.py:270-283) and SpanMarkerV0's start/end pair rows
+    (:131-145 with extract_elements :40-45).
 Pinned in tests/test_oracle_packing.py by construction (positions built from
 known lengths; hidden rows that encode their own index), hand cases, a
 pairwise brute force and round trips.
@@ -116,3 +119,32 @@ def gliner_reps_packed(hidden: torch.Tensor, input_ids: torch.Tensor, words_mask
         pes.append(pe)
         wes.append(we)
     return pes, wes
+
+
+def gliner_span_rows(start_rep: torch.Tensor, end_rep: torch.Tensor, span_idx: torch.Tensor,
+                     span_mask: torch.Tensor) -> torch.Tensor:
+    """SpanMarkerV0's pair rows for one request (poolers/gliner.py:131-145,
+    extract_elements :40-45, indices masked at :285): span s takes start row
+    i and end row j, i, j = span_idx[s] * span_mask[s] clamped to [0, L - 1],
+    written as an explicit loop; out[s] = relu(cat(start[i], end[j]))."""
+    L = start_rep.shape[0]
+    rows = []
+    for (a, b), m in zip(span_idx.tolist(), span_mask.tolist()):
+        a, b = (a, b) if m else (0, 0)
+        i, j = min(max(a, 0), L - 1), min(max(b, 0), L - 1)
+        rows.append(torch.cat([start_rep[i], end_rep[j]]))
+    if not rows:
+        return start_rep.new_zeros(0, 2 * start_rep.shape[1])
+    return torch.relu(torch.stack(rows))
+
+
+def gliner_default_spans(block_len: int, true_len: int, max_width: int):
+    """The pooler's default spans (poolers/gliner.py:270-283) as a loop: for
+    every start word i < block_len and width k < max_width, span (i, i + k),
+    valid when both ends are < true_len."""
+    idx, mask = [], []
+    for i in range(block_len):
+        for k in range(max_width):
+            idx.append([i, i + k])
+            mask.append(int(i < true_len and i + k < true_len))
+    return torch.tensor(idx, dtype=torch.int64).reshape(-1, 2), torch.tensor(mask, dtype=torch.int64)

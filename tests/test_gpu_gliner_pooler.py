@@ -105,3 +105,57 @@ def test_gliner_reps_list_and_int32_inputs():
         got = gliner_reps_packed(h, ids, wm, cu, r.text_lengths, E)
         assert torch.equal(got[0], base[0]) and torch.equal(got[2], base[2])
         assert torch.equal(got[1], base[1]) and torch.equal(got[3], base[3])
+
+
+def _span_batch(dtype, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    lens = [int(x) for x in torch.randint(1, 40, (7,), generator=g)]
+    W = sum(lens)
+    start = torch.randn(W, D, generator=g).to(dtype)
+    end = torch.randn(W, D, generator=g).to(dtype)
+    idxs, masks, counts = [], [], []
+    for r, L in enumerate(lens):
+        if r % 2 == 0:   # the pooler's default spans, text shorter than the block
+            i, m = op.gliner_default_spans(L, max(L - 3, 0), 12)
+        else:            # caller-given spans: out-of-range indices, random masks
+            S = int(torch.randint(0, 60, (1,), generator=g))
+            i = torch.randint(-5, L + 5, (S, 2), generator=g)
+            m = torch.randint(0, 2, (S,), generator=g)
+        idxs.append(i)
+        masks.append(m)
+        counts.append(i.shape[0])
+    cu = lambda c: torch.tensor([0] + torch.tensor(c).cumsum(0).tolist(), dtype=torch.int32)
+    return start, end, lens, idxs, masks, cu(lens), cu(counts)
+
+
+@pytest.mark.parametrize("dtype, D", [(torch.bfloat16, 768), (torch.float32, 1024),
+                                      (torch.float16, 8)])
+def test_gliner_span_rows(dtype, D):
+    from kernels.gliner_pooler import gliner_span_rows
+    start, end, lens, idxs, masks, row_cu, span_cu = _span_batch(dtype, D, D)
+    print(f"gliner span rows {dtype} D={D} spans={int(span_cu[-1])}", flush=True)
+    got = gliner_span_rows(start.cuda(), end.cuda(), row_cu.cuda(), torch.cat(idxs).cuda(),
+                           torch.cat(masks).cuda(), span_cu.cuda()).cpu()
+    for r in range(len(lens)):
+        a, b = int(row_cu[r]), int(row_cu[r + 1])
+        want = op.gliner_span_rows(start[a:b], end[a:b], idxs[r], masks[r])
+        assert torch.equal(got[int(span_cu[r]):int(span_cu[r + 1])], want), f"request {r}"
+
+
+def test_gliner_span_rows_special_values():
+    """ReLU on the bits: negatives (-0 and -inf included) become +0, NaN and
+    +inf pass; an empty request gives zero rows."""
+    from kernels.gliner_pooler import gliner_span_rows
+    vals = torch.tensor([float("nan"), -0.0, float("-inf"), float("inf"), -2.5, 3.0, 0.0, -1e-30])
+    start = vals.repeat(1, 1).bfloat16()
+    end = (-vals).repeat(1, 1).bfloat16()
+    print("gliner span rows special values", flush=True)
+    out = gliner_span_rows(start.cuda(), end.cuda(), torch.tensor([0, 1, 1]), torch.tensor([[0, 0], [0, 0]]),
+                           torch.tensor([1, 1]), torch.tensor([0, 1, 2])).cpu()
+    want = torch.tensor([float("nan"), 0.0, 0.0, float("inf"), 0.0, 3.0, 0.0, 0.0,
+                         float("nan"), 0.0, float("inf"), 0.0, 2.5, 0.0, 0.0, 1e-30]).bfloat16()
+    got0 = out[0].float()
+    assert torch.isnan(got0[0]) and torch.isnan(got0[8])
+    assert torch.equal(out[0, 1:8].view(torch.int16), want[1:8].view(torch.int16))
+    assert torch.equal(out[0, 9:].view(torch.int16), want[9:].view(torch.int16))
+    assert torch.all(out[1] == 0) and not torch.any(torch.signbit(out[1].float()))

@@ -219,3 +219,32 @@ def test_gliner_reps_by_construction():
     pes, wes = op.gliner_reps_packed(h, torch.tensor(ids), torch.tensor(wms), cu, tls, E)
     assert sum((_src(p) for p in pes), []) == want_pe
     assert sum((_src(w) for w in wes), []) == want_we
+
+
+def test_gliner_default_spans_hand_case():
+    idx, mask = op.gliner_default_spans(3, 2, 2)
+    assert idx.tolist() == [[0, 0], [0, 1], [1, 1], [1, 2], [2, 2], [2, 3]]
+    assert mask.tolist() == [1, 1, 1, 0, 0, 0]
+
+
+def test_gliner_default_spans_mirror():
+    """The device-side helper's torch construction equals the loop."""
+    from kernels.gliner_pooler import default_spans
+    for L, T, K in [(5, 3, 4), (1, 1, 12), (7, 7, 3), (4, 0, 2), (0, 0, 3)]:
+        a, b = default_spans(L, T, K), op.gliner_default_spans(L, T, K)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_gliner_span_rows_sources_and_relu():
+    """Start rows hold i + 1 and end rows 100 + j, so each output names its
+    sources: a masked span takes rows (0, 0), indices clamp into [0, L - 1],
+    and negative values leave the ReLU as zeros."""
+    L = 4
+    start = (torch.arange(L, dtype=D64) + 1).unsqueeze(1).repeat(1, 2)
+    end = (torch.arange(L, dtype=D64) + 100).unsqueeze(1).repeat(1, 2)
+    idx = torch.tensor([[1, 2], [3, 3], [2, 3], [-3, 99]])
+    out = op.gliner_span_rows(start, end, idx, torch.tensor([1, 1, 0, 1]))
+    assert out[:, 0].tolist() == [2.0, 4.0, 1.0, 1.0]
+    assert out[:, 2].tolist() == [102.0, 103.0, 100.0, 103.0]
+    neg = op.gliner_span_rows(-start, end, idx[:1], torch.tensor([1]))
+    assert neg[0].tolist() == [0.0, 0.0, 102.0, 102.0]

@@ -422,6 +422,102 @@ __global__ __launch_bounds__(256) void word_rows_kernel(const uint8_t* __restric
   copy_row_any<2>(src, we + j * row_bytes, row_bytes, threadIdx.x & 63);
 }
 
+// ReLU on the raw bits of a 16-byte chunk: a negative value (sign set, not
+// NaN) becomes +0, everything else (NaN included) passes, as torch.relu's
+// NaN-propagating maximum does. EB: element bytes (2 = bf16, 3 = fp16, 4 = fp32;
+// bf16 and fp16 differ only in where NaN starts).
+template <int EB>
+__device__ inline u32x4_t relu_bits(u32x4_t v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t w = v[i];
+    if (EB == 4) {
+      if ((w & 0x80000000u) && (w & 0x7fffffffu) <= 0x7f800000u) w = 0u;
+    } else {
+      constexpr uint32_t kInf = EB == 2 ? 0x7f80u : 0x7c00u;
+      const uint32_t lo = w & 0xffffu, hi = w >> 16;
+      const uint32_t lo2 = ((lo & 0x8000u) && (lo & 0x7fffu) <= kInf) ? 0u : lo;
+      const uint32_t hi2 = ((hi & 0x8000u) && (hi & 0x7fffu) <= kInf) ? 0u : hi;
+      w = lo2 | (hi2 << 16);
+    }
+    v[i] = w;
+  }
+  return v;
+}
+
+// Span pair rows of SpanMarkerV0 (poolers/gliner.py:131-145 with
+// extract_elements :40-45), for span s of request r (span_cu[r] <= s <
+// span_cu[r + 1]) over r's L = row_cu[r + 1] - row_cu[r] word rows:
+// i = clamp(span_idx[s][0] * m, 0, L - 1), j = clamp(span_idx[s][1] * m, 0,
+// L - 1) with m = (span_mask[s] != 0) (the reference multiplies the indices by
+// the mask), out[s] = relu(cat(start[row_cu[r] + i], end[row_cu[r] + j])).
+// L == 0 gives a zero row. Each wave writes kSpansPerWave consecutive spans:
+// lanes 0.. resolve their span's source rows in parallel, then every lane
+// issues all of its 16-byte loads (addresses selected per lane, rows clamped
+// so that no load is conditional) before its stores.
+constexpr int kSpansPerWave = 4;
+constexpr int kSpanPass = 3;  // 16-byte chunks per lane and span in one pass
+
+template <int EB>
+__global__ __launch_bounds__(256) void span_rows_kernel(const uint8_t* __restrict__ start,
+                                                        const uint8_t* __restrict__ end,
+                                                        int64_t row_bytes, int64_t W,
+                                                        const int32_t* __restrict__ row_cu,
+                                                        const int64_t* __restrict__ idx,
+                                                        const int64_t* __restrict__ mask,
+                                                        const int32_t* __restrict__ span_cu, int n,
+                                                        int64_t S, uint8_t* __restrict__ out) {
+  const int64_t s0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kSpansPerWave;
+  const int lane = threadIdx.x & 63;
+  if (s0 >= S) return;
+  const int chunks = (int)(row_bytes / 16), total = 2 * chunks;
+  const u32x4_t zero = {0u, 0u, 0u, 0u};
+  if (W <= 0) {  // no rows at all: every span is a zero row
+    for (int64_t sp = s0; sp < min(S, s0 + kSpansPerWave); ++sp)
+      for (int c = lane; c < total; c += 64)
+        reinterpret_cast<u32x4_t*>(out + sp * 2 * row_bytes)[c] = zero;
+    return;
+  }
+  int64_t ra = -1, rb = -1;  // source rows of span s0 + lane (-1: zero row)
+  if (lane < kSpansPerWave && s0 + lane < S) {
+    const int64_t sp = s0 + lane;
+    const int r = seq_of(span_cu, n, sp);
+    const int64_t base = row_cu[r], L = (int64_t)row_cu[r + 1] - base;
+    if (L > 0) {
+      const bool m = mask[sp] != 0;
+      const int64_t i = m ? idx[2 * sp] : 0, j = m ? idx[2 * sp + 1] : 0;
+      ra = base + min(max(i, (int64_t)0), L - 1);
+      rb = base + min(max(j, (int64_t)0), L - 1);
+    }
+  }
+  for (int c0 = 0; c0 < total; c0 += 64 * kSpanPass) {
+    u32x4_t v[kSpansPerWave][kSpanPass];
+#pragma unroll
+    for (int u = 0; u < kSpansPerWave; ++u) {
+      const int64_t a = __shfl(ra, u, 64), b = __shfl(rb, u, 64);
+#pragma unroll
+      for (int k = 0; k < kSpanPass; ++k) {
+        const int c = min(c0 + lane + 64 * k, total - 1);
+        const bool first = c < chunks;
+        const int64_t row = min(max(first ? a : b, (int64_t)0), W - 1);
+        const uint8_t* src = (first ? start : end) + row * row_bytes + (int64_t)(first ? c : c - chunks) * 16;
+        const u32x4_t x = *reinterpret_cast<const u32x4_t*>(src);
+        v[u][k] = a >= 0 ? relu_bits<EB>(x) : zero;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSpansPerWave; ++u) {
+      if (s0 + u >= S) break;
+      u32x4_t* dst = reinterpret_cast<u32x4_t*>(out + (s0 + u) * 2 * row_bytes);
+#pragma unroll
+      for (int k = 0; k < kSpanPass; ++k) {
+        const int c = c0 + lane + 64 * k;
+        if (c < total) dst[c] = v[u][k];
+      }
+    }
+  }
+}
+
 }  // namespace vfk
 
 using namespace vfk;
@@ -643,5 +739,37 @@ extern "C" int vfk_gliner_word_rows(const void* tok, int64_t row_bytes, int64_t 
   hipLaunchKernelGGL(word_rows_kernel, dim3((unsigned)ceil_div(num_words, 4)), dim3(256), 0,
                      (hipStream_t)stream, static_cast<const uint8_t*>(tok), row_bytes, total_tokens,
                      word_src, num_words, static_cast<uint8_t*>(we));
+  return launch_status(name);
+}
+
+extern "C" int vfk_gliner_span_rows(const void* start_rep, const void* end_rep, int64_t row_bytes,
+                                    int64_t num_rows, int32_t dtype, const int32_t* row_cu, int32_t num_requests,
+                                    const int64_t* span_idx, const int64_t* span_mask,
+                                    const int32_t* span_cu, int64_t num_spans, void* out,
+                                    void* stream) {
+  const char* name = "vfk_gliner_span_rows";
+  if (!start_rep || !end_rep || !row_cu || !span_idx || !span_mask || !span_cu || !out)
+    return set_error(VFK_ERR_INVALID, "%s: NULL pointer", name);
+  if (int rc = check_rows(name, start_rep, out, row_bytes)) return rc;
+  if (int rc = check_rows(name, end_rep, out, row_bytes)) return rc;
+  if (num_requests <= 0 || num_rows < 0 || num_spans < 0 || num_spans >= (1ll << 31) - 1)
+    return set_error(VFK_ERR_INVALID, "%s: bad sizes", name);
+  if (num_spans == 0) return VFK_OK;
+  const dim3 grid((unsigned)ceil_div(num_spans, 4 * kSpansPerWave));
+  hipStream_t st = (hipStream_t)stream;
+  const uint8_t* sp = static_cast<const uint8_t*>(start_rep);
+  const uint8_t* ep = static_cast<const uint8_t*>(end_rep);
+  uint8_t* op = static_cast<uint8_t*>(out);
+  if (dtype == VFK_BF16)
+    hipLaunchKernelGGL(span_rows_kernel<2>, grid, dim3(256), 0, st, sp, ep, row_bytes, num_rows, row_cu, span_idx,
+                       span_mask, span_cu, (int)num_requests, num_spans, op);
+  else if (dtype == VFK_F16)
+    hipLaunchKernelGGL(span_rows_kernel<3>, grid, dim3(256), 0, st, sp, ep, row_bytes, num_rows, row_cu, span_idx,
+                       span_mask, span_cu, (int)num_requests, num_spans, op);
+  else if (dtype == VFK_F32)
+    hipLaunchKernelGGL(span_rows_kernel<4>, grid, dim3(256), 0, st, sp, ep, row_bytes, num_rows, row_cu, span_idx,
+                       span_mask, span_cu, (int)num_requests, num_spans, op);
+  else
+    return set_error(VFK_ERR_INVALID, "%s: dtype must be bf16, fp16 or fp32", name);
   return launch_status(name);
 }

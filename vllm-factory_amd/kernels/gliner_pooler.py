@@ -134,3 +134,63 @@ def extract_gliner_reps(hidden: torch.Tensor, input_ids: torch.Tensor, words_mas
         out.append((pe[a:b].unsqueeze(0), torch.ones(1, b - a, dtype=torch.long, device=dev),
                     we[c:d].unsqueeze(0), torch.ones(1, d - c, dtype=torch.long, device=dev)))
     return out
+
+
+def default_spans(block_len: int, true_len: int, max_width: int):
+    """The pooler's default span list for one request (poolers/gliner.py:
+    270-283): span (i, i + k) for every start i < block_len and width
+    k < max_width, valid where both ends are < true_len. Returns (span_idx
+    int64 [block_len * max_width, 2], span_mask int64 [block_len * max_width])
+    on the CPU."""
+    starts = torch.arange(block_len).repeat_interleave(max_width)
+    widths = torch.arange(max_width).repeat(block_len)
+    idx = torch.stack([starts, starts + widths], dim=-1)
+    mask = ((idx[:, 0] < true_len) & (idx[:, 1] < true_len)).to(torch.int64)
+    return idx, mask
+
+
+def gliner_span_rows(start_rep: torch.Tensor, end_rep: torch.Tensor, row_cu: torch.Tensor,
+                     span_idx: torch.Tensor, span_mask: torch.Tensor,
+                     span_cu: torch.Tensor) -> torch.Tensor:
+    """SpanMarkerV0's pair rows for every request of a packed batch at once:
+    relu(cat(start_rep[i], end_rep[j])) per span (poolers/gliner.py:131-145,
+    extract_elements :40-45, the masked indices of :285).
+
+    start_rep / end_rep [W, D] (bf16, fp16 or fp32; the project_start /
+    project_end outputs over the requests' word rows, request r owning rows
+    row_cu[r] .. row_cu[r + 1] - 1), span_idx [S, 2] request-local word
+    indices and span_mask [S] (any integer or bool dtype), span_cu [n + 1]
+    (request r owns spans span_cu[r] .. span_cu[r + 1] - 1). Returns
+    [S, 2 * D]; for request r it equals the reference's cat(...).relu()
+    rows before out_project."""
+    dev = _lib.require_gpu(start_rep, end_rep)
+    if start_rep.dim() != 2 or start_rep.shape != end_rep.shape or start_rep.dtype != end_rep.dtype:
+        raise ValueError("start_rep and end_rep must be [W, D] of one dtype")
+    codes = {torch.bfloat16: 1, torch.float16: 2, torch.float32: 0}
+    if start_rep.dtype not in codes:
+        raise ValueError("start_rep must be bf16, fp16 or fp32")
+
+    def rows(t):
+        t = t.contiguous()
+        return t if t.data_ptr() % 16 == 0 else t.clone()
+    sr, er = rows(start_rep), rows(end_rep)
+    W, D = sr.shape
+    row_bytes = D * sr.element_size()
+    if row_bytes % 16:
+        raise ValueError("row size must be a multiple of 16 bytes")
+    idx = torch.as_tensor(span_idx).to(device=dev, dtype=torch.int64).reshape(-1, 2).contiguous()
+    S = idx.shape[0]
+    mask = torch.as_tensor(span_mask).to(device=dev, dtype=torch.int64).reshape(-1).contiguous()
+    if mask.numel() != S:
+        raise ValueError("span_mask must have one entry per span")
+    rcu = torch.as_tensor(row_cu).to(device=dev, dtype=torch.int32).contiguous()
+    scu = torch.as_tensor(span_cu).to(device=dev, dtype=torch.int32).contiguous()
+    n = rcu.numel() - 1
+    if n < 1 or scu.numel() != n + 1:
+        raise ValueError("row_cu and span_cu need one entry per request plus one")
+    out = torch.empty(S, 2 * D, dtype=sr.dtype, device=dev)
+    if S:
+        _lib.on_device("vfk_gliner_span_rows", dev, sr.data_ptr(), er.data_ptr(), row_bytes, W,
+                       codes[sr.dtype], rcu.data_ptr(), n, idx.data_ptr(), mask.data_ptr(),
+                       scu.data_ptr(), S, out.data_ptr())
+    return out
