@@ -72,6 +72,18 @@ int vfk_t5_bucket(const int64_t* rel, int32_t* out, int64_t n,
 int vfk_deberta_bucket(const int64_t* rel, int32_t* out, int64_t n,
                        int32_t bucket_size, int32_t max_position);
 
+/* 1 when the clamped DeBERTa index c(d) = clamp(bucket(d) + att_span, 0,
+ * 2 att_span - 1) changes by at most 1 per unit of d for |d| <= max_len, else
+ * 0 (or a negative VFK_ERR code). The bucket formula of
+ * models/deberta_v2/deberta_v2_encoder.py:70-89 jumps by 2 or more when
+ * max_relative_positions is small against position_buckets (e.g. 256 / 256).
+ * The staged vfk_flash_deberta_fwd kernel and vfk_deberta_fused_fwd need unit
+ * steps: otherwise the former takes its per-score gather and the latter
+ * returns VFK_ERR_UNSUPPORTED. Span and bucket arguments are derived as in
+ * kernels/flash_deberta_attention.py:323, :366-368. Host only. */
+int vfk_deberta_unit_steps(int32_t position_buckets, int32_t max_relative_distance,
+                           int32_t use_log_bucket, int32_t max_len);
+
 /* ------------------------------------------------------------------------ */
 /* Attention                                                                 */
 /* ------------------------------------------------------------------------ */
@@ -324,6 +336,19 @@ int vfk_colbert_head_fwd(const vfk_tensor* x, const vfk_tensor* residual,
  *          = x[d] cos[d] + x[d-D/2] sin[d]        (d >= D/2)            */
 int vfk_rope_fwd(const vfk_tensor* x, const vfk_tensor* cos,
                  const vfk_tensor* sin, vfk_tensor* out, void* stream);
+
+/* RoPE of q and k in one launch. Replaces kernels/fused_rope_global.py:145-166
+ * (fused_rope_global_apply, one _fused_rope_kernel launch per tensor) and
+ * kernels/fused_rope_local.py:11-76. Same formula as vfk_rope_fwd.
+ *   q, q_out [B,S,Hq,D]; k, k_out [B,S,Hk,D] or both NULL (q only); last dim
+ *   contiguous, 16-byte aligned rows, D a multiple of 16 (16-bit) or 8 (fp32)
+ *   cos, sin [B|1,S,D] in q's dtype or fp32 (then used at fp32, as the
+ *   reference's kernel promotes mixed operands), 16-byte aligned rows.
+ * Each cos/sin chunk is loaded once per thread and applied to several heads
+ * of q and k; the result is rounded once to q's dtype. */
+int vfk_rope_qk_fwd(const vfk_tensor* q, const vfk_tensor* k,
+                    const vfk_tensor* cos, const vfk_tensor* sin,
+                    vfk_tensor* q_out, vfk_tensor* k_out, void* stream);
 
 /* LayerNorm over the last dim. Replaces kernels/fused_layernorm.py:19-274.
  *   x, out [rows, n] (row stride, unit column stride); weight/bias [n] or

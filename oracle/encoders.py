@@ -13,8 +13,9 @@ attention inside each sequence; the others use theta 10000 and |i - j| <= 64
 (:456-460). Everything is computed per sequence in fp32 (the packed dense
 masks of :491-550 are equivalent and infeasible at benchmark sizes).
 
-mt5_layer follows the reference's T5EncoderLayer (models/mt5/mt5_encoder.py
-:476-491): h = x + SelfAttention(RMSNorm1(x)); h + FF(RMSNorm2(h)), with the
+mt5_encoder is the stack with the final RMSNorm (models/mt5/mt5_encoder.py
+:524-599); mt5_layer follows the reference's T5EncoderLayer (:476-491):
+h = x + SelfAttention(RMSNorm1(x)); h + FF(RMSNorm2(h)), with the
 relative-position-bias attention of :234-320 (bidirectional buckets, bias
 table [buckets, heads] shared from layer 0, no 1/sqrt(d) scaling, additive
 key mask (1 - m) * finfo.min, :571-576) and the gated FFN of :411-447
@@ -131,6 +132,17 @@ def mt5_layer(x: torch.Tensor, wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2, table,
     x = x + att.transpose(1, 2).reshape(B, L, D) @ wo.to(dtype)
     h = rmsnorm(x, ln2, eps, dtype)
     return x + (gelu_tanh(h @ wi0.to(dtype)) * (h @ wi1.to(dtype))) @ wff_o.to(dtype)
+
+
+def mt5_encoder(x: torch.Tensor, layers, table, final_ln, mask: Optional[torch.Tensor],
+                num_buckets: int = 32, max_distance: int = 128, eps: float = 1e-6,
+                dtype=torch.float32) -> torch.Tensor:
+    """models/mt5/mt5_encoder.py:524-599 (MT5Encoder.forward) after the
+    embeddings: every layer with layer 0's table, then the final RMSNorm (:591).
+    layers: (wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2) per layer."""
+    for lw in layers:
+        x = mt5_layer(x, *lw, table, mask, num_buckets, max_distance, eps, dtype)
+    return rmsnorm(x, final_ln, eps, dtype)
 
 
 def deberta_layer(x: torch.Tensor, seq_lengths: torch.Tensor, rel: torch.Tensor, lw, heads: int,

@@ -2,9 +2,12 @@
 
 Pinned by (tests/test_oracle_epilogues.py): torch.nn.functional.layer_norm,
 F.gelu(approximate='none'|'tanh'), F.silu, transformers' T5LayerNorm for
-RMSNorm, the RoPE identities (position 0 is the identity, pair norms are
-preserved, <rope(q,p), rope(k,p')> depends only on p - p'), and, for the
-ColBERT head, F.linear + F.normalize and unit row norms.
+RMSNorm; rope_table by RoPE's closed form (each (x[f], x[f+32]) pair as a
+complex number times e^{i angle}), transformers' ModernBERT
+apply_rotary_pos_emb and the brute-force-pinned oracle.attention.apply_rope,
+with a negative control (a sign-flipped rotate_half fails all three while it
+passes the RoPE identities); residual_add by torch.add; and, for the ColBERT
+head, F.linear + F.normalize and unit row norms.
 """
 from __future__ import annotations
 

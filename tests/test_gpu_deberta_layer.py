@@ -34,6 +34,29 @@ def test_deberta_layers_match_oracle(batch, layers):
         assert err <= 6e-2 and cs >= 0.9999, (b, err, cs)
 
 
+def test_deberta_layer_wide_bucket_steps_match_oracle():
+    """position_buckets 256 with max_relative_positions 256: the log bucket
+    moves by 2 per unit of distance in places, so the layer takes the
+    reference interface (materialised pos_key / pos_query, per-score gather)
+    instead of the fused kernel; the output still matches the oracle."""
+    from encoders.deberta import deberta_forward, random_weights
+    from kernels.flash_deberta_attention import unit_steps
+    from oracle import encoders as oe
+    assert not unit_steps(256, 256, True, 512)
+    hidden, lens = workloads.config3_hidden(2)
+    w = random_weights(num_layers=1, dtype=torch.bfloat16)
+    w.max_relative_positions = 256
+    dev = torch.device("cuda:0")
+    got = deberta_forward(hidden.to(dev, torch.bfloat16), lens.to(dev), w.to(dev)).float().cpu()
+    want = oe.deberta_encoder(hidden.to(torch.bfloat16).float(), lens, w)
+    for b in range(2):
+        n = int(lens[b])
+        err = (got[b, :n] - want[b, :n]).abs().max().item()
+        cs = cosine(got[b, :n], want[b, :n])
+        print(f"wide steps row {b} (len {n}): max-abs {err:.3e} cosine {cs:.6f}")
+        assert err <= 6e-2 and cs >= 0.9999, (b, err, cs)
+
+
 def test_activation_gelu_matches_oracle():
     """vfk_act_fwd on a strided [rows, n] view (DeBERTa's intermediate GELU)."""
     from kernels.activation import activation

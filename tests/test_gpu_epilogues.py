@@ -131,6 +131,46 @@ def test_rope_table(dev, dtype, cos_rank):
         assert_elem_close(gk, oe.rope_table(k, cos, sin), dtype, "rope k")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_fp32_tables_used_at_fp32(dev, dtype):
+    """16-bit q/k with fp32 cos/sin (the reference's Triton kernel promotes
+    the mixed product to fp32): the tables are not rounded to q's dtype first,
+    so the result is the fp32 rotation rounded once. Different head counts for
+    q and k put both tensors into one head group of the launch."""
+    from kernels.fused_rope_global import fused_rope_global_apply
+    from oracle.attention import rope_cos_sin
+    B, S, D = 2, 333, 64
+    q = _rand((B, S, 7, D), dtype, 21)
+    k = _rand((B, S, 5, D), dtype, 22)
+    cos, sin = rope_cos_sin(torch.arange(S) * 7 + 3, 160000.0, D)   # fp32, large angles
+    gq, gk = fused_rope_global_apply(q.to(dev), k.to(dev), cos.to(dev), sin.to(dev))
+    for got, x, name in ((gq, q, "q"), (gk, k, "k")):
+        want = oe.rope_table(x, cos[None], sin[None])                  # fp32 tables, fp32 math
+        assert got.dtype == dtype
+        assert_elem_close(got, want, dtype, f"rope fp32-table {name}")
+        # the output is the fp32 result rounded once: it equals the oracle
+        # rounded to q's dtype except at rare rounding ties; tables rounded to
+        # q's dtype first would change many more elements
+        got_c = got.cpu()
+        exact = (got_c == want.to(dtype)).float().mean().item()
+        lossy = oe.rope_table(x, cos[None].to(dtype), sin[None].to(dtype)).to(dtype)
+        lossy_exact = (lossy == want.to(dtype)).float().mean().item()
+        print(f"rope {dtype} {name}: {exact:.5f} of elements equal the rounded fp32 result "
+              f"(tables rounded first: {lossy_exact:.5f})")
+        assert exact >= 0.99 and exact > lossy_exact + 0.02, (exact, lossy_exact)
+
+
+def test_rope_fp32(dev):
+    from kernels.fused_rope_global import fused_rope_global_apply
+    from oracle.attention import rope_cos_sin
+    q = _rand((1, 257, 12, 64), torch.float32, 23)
+    k = _rand((1, 257, 12, 64), torch.float32, 24)
+    cos, sin = rope_cos_sin(torch.arange(257), 10000.0, 64)
+    gq, gk = fused_rope_global_apply(q.to(dev), k.to(dev), cos.to(dev), sin.to(dev))
+    assert_elem_close(gq, oe.rope_table(q, cos[None], sin[None]), torch.float32, "rope f32 q")
+    assert_elem_close(gk, oe.rope_table(k, cos[None], sin[None]), torch.float32, "rope f32 k")
+
+
 def test_rope_strided_qkv_view(dev):
     """q/k as strided views of a fused [B,S,3,H,D] projection (no copies)."""
     from kernels.fused_rope_global import fused_rope_apply

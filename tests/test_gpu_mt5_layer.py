@@ -30,6 +30,36 @@ def test_mt5_layer_matches_oracle():
         assert err <= 6e-2 and cs >= 0.9999, (b, err, cs)
 
 
+def test_mt5_encoder_stack_matches_oracle():
+    """mt5_encoder_forward (models/mt5/mt5_encoder.py:524-599): two layers with
+    their own weights, the layer-0 bias table shared, the reference's key mask
+    built from an attention_mask of ones and zeros, then the final RMSNorm, on
+    two config-4 batch rows. The final RMSNorm rescales rows to unit RMS
+    (values up to ~5), so the bound is the per-layer one: max-abs 6e-2,
+    cosine 0.9999 on valid rows."""
+    from encoders.mt5 import mt5_encoder_forward
+    from oracle import encoders as oe
+    c = workloads.config4(batch=2)
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1404)
+    base = (c.wq, c.wk, c.wv, c.wo, c.wi0, c.wi1, c.wff_o, c.ln1, c.ln2)
+    second = tuple((w.float() + 0.01 * torch.randn(w.shape, generator=g)).to(w.dtype) for w in base)
+    layers = [base, second]
+    lnf = (1.0 + 0.1 * torch.randn(1024, generator=g)).bfloat16()
+    L = c.hidden.shape[1]
+    keep = (torch.arange(L)[None, :] < c.lengths[:, None]).long()
+    got = mt5_encoder_forward(None, keep.to(dev), [tuple(w.to(dev) for w in lw) for lw in layers],
+                              c.table.to(dev), lnf.to(dev), inputs_embeds=c.hidden.to(dev))
+    want = oe.mt5_encoder(c.hidden, layers, c.table, lnf, c.mask)
+    got = got.float().cpu()
+    for b in range(2):
+        n = int(c.lengths[b])
+        err = (got[b, :n] - want[b, :n]).abs().max().item()
+        cs = cosine(got[b, :n], want[b, :n])
+        print(f"2 layers + final RMSNorm, row {b} (len {n}): max-abs {err:.3e} cosine {cs:.6f}")
+        assert err <= 6e-2 and cs >= 0.9999, (b, err, cs)
+
+
 def test_mt5_flat_stream_routed_per_sequence():
     """The GLiNER flat call (plugins/mt5_gliner/model.py:169-201) routed per
     sequence: two layers on the packed valid rows of three config-4 rows equal

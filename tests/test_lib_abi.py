@@ -32,7 +32,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     from kernels import _lib
-    assert _lib.load().vfk_abi_version() == 6
+    assert _lib.load().vfk_abi_version() == 7
 
 
 def _host_t5(rel, bidirectional, nb, md):
@@ -70,6 +70,23 @@ def test_deberta_host_bucket_matches_oracle(bs, mp):
     rel = (np.arange(L)[:, None] - np.arange(L)[None, :]).astype(np.int64)
     got = _host_deb(rel, bs, mp)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("pb,mrp", [(256, 512), (256, 1024), (128, 512), (64, 128), (256, 256),
+                                    (256, 300), (128, 128), (64, 64)])
+def test_deberta_unit_steps_matches_oracle(pb, mrp):
+    """vfk_deberta_unit_steps reports whether the clamped index
+    clamp(bucket(d) + S, 0, 2S - 1) moves by at most 1 per unit of d, as the
+    oracle's bucket matrix shows it (256/256, 256/300 and 128/128 jump by 2)."""
+    from kernels import _lib
+    L = 1100
+    S = pb
+    c = torch.clamp(ob.build_relative_position_v2(L, L, pb, mrp)[0][0] + S, 0, 2 * S - 1)
+    want = int((c[:-1] - c[1:]).abs().max() <= 1)  # row 0: d = -j, consecutive keys
+    assert _lib.load().vfk_deberta_unit_steps(pb, mrp, 1, L) == want
+    assert _lib.load().vfk_deberta_unit_steps(pb, mrp, 0, L) == 1   # linear positions
+    if (pb, mrp) in ((256, 256), (256, 300), (128, 128)):
+        assert want == 0
 
 
 def test_invalid_arguments_raise():

@@ -115,6 +115,50 @@ def test_mt5_layer_oracle_matches_transformers():
     torch.testing.assert_close(got, want, rtol=0, atol=1e-5)
 
 
+def test_mt5_encoder_stack_oracle_matches_transformers():
+    """Two MT5EncoderModel blocks (layer 1 reuses layer 0's relative-attention
+    bias, as the reference passes one table to every layer) and the final
+    RMSNorm against oracle.encoders.mt5_encoder with the same weights."""
+    from transformers import MT5Config, MT5EncoderModel
+    g = torch.Generator().manual_seed(12)
+    B, L, D, H, F = 2, 36, 128, 2, 192
+    cfg = MT5Config(vocab_size=64, d_model=D, d_kv=64, d_ff=F, num_layers=2, num_heads=H,
+                    relative_attention_num_buckets=32, relative_attention_max_distance=128,
+                    feed_forward_proj="gated-gelu", layer_norm_epsilon=1e-6, dropout_rate=0.0)
+    m = MT5EncoderModel(cfg).eval().double()
+    r = lambda *s: torch.randn(*s, generator=g, dtype=torch.float64)
+    table = r(32, H) * 0.5
+    layers = []
+    for i in range(2):
+        wq, wk, wv, wo = (r(D, D) * 0.08 for _ in range(4))
+        wi0, wi1, wff = r(D, F) * 0.08, r(D, F) * 0.08, r(F, D) * 0.08
+        ln1, ln2 = 1 + 0.1 * r(D), 1 + 0.1 * r(D)
+        layers.append((wq, wk, wv, wo, wi0, wi1, wff, ln1, ln2))
+        sa, ff = m.encoder.block[i].layer[0], m.encoder.block[i].layer[1]
+        with torch.no_grad():
+            sa.SelfAttention.q.weight.copy_(wq.t()); sa.SelfAttention.k.weight.copy_(wk.t())
+            sa.SelfAttention.v.weight.copy_(wv.t()); sa.SelfAttention.o.weight.copy_(wo.t())
+            if i == 0:
+                sa.SelfAttention.relative_attention_bias.weight.copy_(table)
+            sa.layer_norm.weight.copy_(ln1)
+            ff.DenseReluDense.wi_0.weight.copy_(wi0.t()); ff.DenseReluDense.wi_1.weight.copy_(wi1.t())
+            ff.DenseReluDense.wo.weight.copy_(wff.t()); ff.layer_norm.weight.copy_(ln2)
+    assert not m.encoder.block[1].layer[0].SelfAttention.has_relative_attention_bias
+    lnf = 1 + 0.1 * r(D)
+    with torch.no_grad():
+        m.encoder.final_layer_norm.weight.copy_(lnf)
+    x = r(B, L, D)
+    keep = torch.ones(B, L, dtype=torch.float64)
+    keep[0, 30:] = 0
+    with torch.no_grad():
+        want = m(inputs_embeds=x, attention_mask=keep).last_hidden_state
+    mask = ((1.0 - keep) * torch.finfo(torch.float64).min)[:, None, None, :]
+    got = oe.mt5_encoder(x, layers, table, lnf, mask, dtype=torch.float64)
+    torch.testing.assert_close(got, want, rtol=0, atol=1e-5)
+    # dropping the final RMSNorm or the second layer is far outside that bound
+    assert (oe.mt5_encoder(x, layers[:1], table, lnf, mask, dtype=torch.float64) - want).abs().max() > 1e-2
+
+
 def _deberta_small(seed=11):
     import encoders.deberta as ed
     return ed.random_weights(num_layers=3, hidden=128, heads=2, inter=256, position_buckets=16,

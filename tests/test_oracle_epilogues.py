@@ -58,6 +58,69 @@ def test_rope_identities():
         assert float(vals.max() - vals.min()) < 1e-4 * float(vals.abs().max() + 1)
 
 
+def _rope_sign_flipped(x, cos, sin, dtype=torch.float64):
+    """A plausible mistake: rotate_half with the wrong sign (a rotation by -theta)."""
+    x, cos, sin = x.to(dtype), cos.to(dtype), sin.to(dtype)
+    h = x.shape[-1] // 2
+    rot = torch.cat((x[..., h:], -x[..., :h]), dim=-1)
+    return x * cos.unsqueeze(2) + rot * sin.unsqueeze(2)
+
+
+def _rope_checks(fn):
+    """Checks that pin a RoPE implementation f(x [B,S,H,64], cos, sin [B,S,64]):
+    (1) the closed form: the pair (x[f], x[f + 32]) read as the complex number
+    x[f] + i x[f + 32] is multiplied by e^{i pos inv_freq[f]} (RoPE's
+    definition, non-interleaved halves); (2) transformers' ModernBERT
+    apply_rotary_pos_emb; (3) the brute-force-pinned oracle.attention.apply_rope."""
+    from transformers.models.modernbert.modeling_modernbert import apply_rotary_pos_emb
+    g = torch.Generator().manual_seed(11)
+    B, S, H = 2, 37, 3
+    x = torch.randn(B, S, H, 64, generator=g, dtype=D64)
+    pos = torch.randint(0, 4000, (B, S), generator=g)
+    inv = 1.0 / (160000.0 ** (torch.arange(0, 64, 2, dtype=torch.int64).float() / 64))
+    ang = (pos.float()[..., None] * inv).double()          # fp32 angles, as HF forms them
+    cos = torch.cat((ang.cos(), ang.cos()), -1)
+    sin = torch.cat((ang.sin(), ang.sin()), -1)
+    got = fn(x, cos, sin)
+    z = torch.complex(x[..., :32], x[..., 32:]) * torch.polar(torch.ones_like(ang), ang)[:, :, None]
+    want = torch.cat((z.real, z.imag), -1)
+    ok = [torch.allclose(got, want, rtol=0, atol=1e-12)]
+    qh, _ = apply_rotary_pos_emb(x.float(), x.float(), cos.float(), sin.float(), unsqueeze_dim=2)
+    ok.append(torch.allclose(got.float(), qh, rtol=0, atol=1e-5))
+    ok.append(torch.allclose(got, oa.apply_rope(x, cos, sin), rtol=0, atol=1e-12))
+    return ok
+
+
+def test_rope_table_pinned_by_closed_form_and_transformers():
+    assert _rope_checks(lambda x, c, s: oe.rope_table(x, c, s, dtype=D64)) == [True, True, True]
+    # the [B, 1, S, D] table layout the reference also accepts
+    x = _r(2, 9, 2, 64, seed=12)
+    c, s = _r(2, 9, 64, seed=13), _r(2, 9, 64, seed=14)
+    torch.testing.assert_close(oe.rope_table(x, c[:, None], s[:, None], dtype=D64),
+                               oe.rope_table(x, c, s, dtype=D64))
+
+
+def test_rope_checks_reject_sign_flip():
+    """Negative control: the sign-flipped rotation passes the identities of
+    test_rope_identities (norms, position 0, relative dependence) but fails
+    every check that pins rope_table."""
+    assert _rope_checks(_rope_sign_flipped) == [False, False, False]
+    x = _r(1, 50, 3, 64, seed=8)
+    cos, sin = oa.rope_cos_sin(torch.arange(50), 10000.0)
+    y = _rope_sign_flipped(x, cos[None].double(), sin[None].double())
+    torch.testing.assert_close(y[:, 0], x[:, 0])
+    torch.testing.assert_close(x[..., :32] ** 2 + x[..., 32:] ** 2, y[..., :32] ** 2 + y[..., 32:] ** 2)
+
+
+def test_residual_add_equals_torch_add():
+    """kernels/fused_dropout_residual.py:50-51 (inference): residual + input,
+    in the oracle's dtype, element for element."""
+    x, r = _r(30, 768, seed=15), _r(30, 768, seed=16)
+    assert torch.equal(oe.residual_add(x, r, dtype=D64), torch.add(r, x))
+    xb, rb = x.to(torch.bfloat16), r.to(torch.bfloat16)
+    assert torch.equal(oe.residual_add(xb, rb), torch.add(rb.float(), xb.float()))
+
+
 # ------------------------------------------------------------------ ColBERT head
 def test_colbert_head_matches_library_routines():
     """LayerNorm -> Linear -> L2 normalise equals F.layer_norm, F.linear and

@@ -31,6 +31,7 @@ struct DebArgs {
   const void* kr; int64_t krs[2];   // fused: key_rel [H, 2S, 64] (c2p) or null
   const void* qr; int64_t qrs[2];   // fused: query_rel [H, 2S, 64] (p2c) or null
   StepFn step;                      // |bucket| as a function of |d| (log mode)
+  int unit;                         // c(d) moves by at most 1 per unit of d
 };
 
 __device__ inline int deb_index(const DebArgs& a, int d) {
@@ -706,9 +707,11 @@ static int setup_common(DebArgs& a, const vfk_tensor* q, const vfk_tensor* k, co
   const int maxd = max_relative_distance > 0 ? max_relative_distance : 512;
   a.log_bucket = use_log_bucket ? 1 : 0;
   if (a.span <= 0) return set_error(VFK_ERR_INVALID, "%s: att_span must be > 0", name);
+  a.unit = 1;
   if (a.log_bucket) {
     const int max_abs = (int)(M > N ? M : N);
     if ((rc = build_deberta_step(nb, maxd, max_abs, a.span, &a.step))) return rc;
+    a.unit = step_is_unit(a.step) ? 1 : 0;
   }
   return VFK_OK;
 }
@@ -762,7 +765,7 @@ extern "C" int vfk_flash_deberta_fwd(const vfk_tensor* q, const vfk_tensor* k, c
            (reinterpret_cast<uintptr_t>(p) & 15) == 0;
   };
   const size_t slds = deb_staged_lds(a.lut_len);
-  if ((a.pk || a.pq) && (!a.pk || rows16(a.pk, a.pks)) && (!a.pq || rows16(a.pq, a.pqs)) &&
+  if (a.unit && (a.pk || a.pq) && (!a.pk || rows16(a.pk, a.pks)) && (!a.pq || rows16(a.pq, a.pqs)) &&
       a.span % 4 == 0 && 2 * a.span >= kPqW && slds <= 64 * 1024) {
 #define VFK_DEB_STAGED(E)                                                                         \
   if (a.pk && a.pq)                                                                               \
@@ -797,6 +800,13 @@ extern "C" int vfk_deberta_fused_fwd(const vfk_tensor* q, const vfk_tensor* k, c
   if (rc) return rc;
   if (a.M != a.N)
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_deberta_fused_fwd: self-attention only (M == N)");
+  // the per-tile index windows (at most 3 C and 6 P^T blocks of 32) hold
+  // only for indices that move by at most 1 per unit of distance
+  if (!a.unit)
+    return set_error(VFK_ERR_UNSUPPORTED,
+                     "vfk_deberta_fused_fwd: position_buckets=%d / max_relative_positions=%d give "
+                     "bucket steps above 1 (use flash_deberta_attention)",
+                     position_buckets, max_relative_distance);
   const vfk_tensor* rel[2] = {key_rel, query_rel};
   const char* names[2] = {"key_rel", "query_rel"};
   for (int i = 0; i < 2; ++i) {

@@ -144,6 +144,15 @@ int build_deberta_step(int bucket_size, int max_position, int max_abs,
   return fill_steps(out, mid + 1, deb_abs_fn, args, max_abs, f_cap);
 }
 
+bool step_is_unit(const StepFn& s) {
+  if (s.f0 < s.a0 - 1 || s.f0 > s.a0) return false;
+  for (int i = 0; i < s.nthr; ++i) {
+    const int prev = i ? s.thr[i - 1] : s.a0;
+    if (s.thr[i] <= prev) return false;
+  }
+  return true;
+}
+
 }  // namespace vfk
 
 // ---------------------------------------------------------------------------
@@ -196,4 +205,20 @@ extern "C" int vfk_deberta_bucket(const int64_t* rel, int32_t* out, int64_t n,
     out[i] = r < 0 ? -v : v;
   }
   return VFK_OK;
+}
+
+extern "C" int vfk_deberta_unit_steps(int32_t position_buckets, int32_t max_relative_distance,
+                                      int32_t use_log_bucket, int32_t max_len) {
+  // Same span / bucket derivation as the attention entry points
+  // (kernels/flash_deberta_attention.py:323, :366-368).
+  const int span = position_buckets > 0 ? position_buckets : max_relative_distance;
+  if (span <= 0 || max_len < 0)
+    return vfk::set_error(VFK_ERR_INVALID, "vfk_deberta_unit_steps: bad arguments");
+  if (!use_log_bucket) return 1;  // c = clamp(d + S): unit steps
+  const int nb = position_buckets > 0 ? position_buckets : max_relative_distance * 2;
+  const int maxd = max_relative_distance > 0 ? max_relative_distance : 512;
+  vfk::StepFn s;
+  int rc = vfk::build_deberta_step(nb, maxd, max_len, span, &s);
+  if (rc) return rc;
+  return vfk::step_is_unit(s) ? 1 : 0;
 }

@@ -763,6 +763,85 @@ __global__ __launch_bounds__(256) void rope_scalar_kernel(RopeArgs p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// RoPE of q and k in one launch (kernels/fused_rope_global.py:108-166 makes
+// one launch per tensor). Thread = (row (b, s), chunk pair cp): it loads the
+// cos / sin values of d in chunk cp and of d + D/2 once, in the table's own
+// dtype (fp32 or the element type), and applies them to kRopeHG heads of the
+// concatenated head list (q heads, then k heads), all loads of those heads in
+// flight before the first use. Grid y = head groups.
+// ---------------------------------------------------------------------------
+struct RopeQKArgs {
+  const void* x[2]; int64_t xs[2][3];  // q, k: strides of B, S, H (D contiguous)
+  void* y[2]; int64_t ys[2][3];
+  int nh[2];                           // heads of q, k (k: 0 when absent)
+  const void* c; int64_t cs[2];        // cos: strides of B (0: shared), S
+  const void* s; int64_t ss[2];
+  int half;                            // D / 2
+  uint32_t rows;                       // B * S
+};
+
+constexpr int kRopeHG = 6;
+
+// VEC table values at element i as fp32 (VEC = the x chunk's element count).
+template <int CT, int VEC>
+__device__ inline void load_tab(const void* base, int64_t i, float* f) {
+  if constexpr (CT == VFK_F32) {
+#pragma unroll
+    for (int j = 0; j < VEC / 4; ++j) Elt<VFK_F32>::load(base, i + 4 * j, f + 4 * j);
+  } else {
+    static_assert(VEC == Elt<CT>::VEC, "16-bit table with a 16-bit element type");
+    Elt<CT>::load(base, i, f);
+  }
+}
+
+template <int DT, int CT>
+__global__ __launch_bounds__(256) void rope_qk_kernel(RopeQKArgs p, Magic gcp, Magic gs) {
+  using L = Elt<DT>;
+  constexpr int VEC = L::VEC;
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t row = magic_div(t, gcp);
+  if (row >= p.rows) return;
+  const int d0 = (int)(t - row * gcp.d) * VEC;
+  const uint32_t b = magic_div(row, gs);
+  const uint32_t sq = row - b * gs.d;
+  float c1[VEC], c2[VEC], s1[VEC], s2[VEC];
+  const int64_t co = (int64_t)b * p.cs[0] + (int64_t)sq * p.cs[1] + d0;
+  const int64_t so = (int64_t)b * p.ss[0] + (int64_t)sq * p.ss[1] + d0;
+  load_tab<CT, VEC>(p.c, co, c1);
+  load_tab<CT, VEC>(p.c, co + p.half, c2);
+  load_tab<CT, VEC>(p.s, so, s1);
+  load_tab<CT, VEC>(p.s, so + p.half, s2);
+  const int nh = p.nh[0] + p.nh[1];
+  const int h0 = blockIdx.y * kRopeHG;
+  float x1[kRopeHG][VEC], x2[kRopeHG][VEC];
+  int64_t yo[kRopeHG];
+#pragma unroll
+  for (int u = 0; u < kRopeHG; ++u) {
+    // head index uniform over the grid row: the tensor choice is scalar
+    const int hh = min(h0 + u, nh - 1);
+    const int ti = hh >= p.nh[0] ? 1 : 0;
+    const int h = hh - ti * p.nh[0];
+    const int64_t xo = (int64_t)b * p.xs[ti][0] + (int64_t)sq * p.xs[ti][1] + (int64_t)h * p.xs[ti][2] + d0;
+    yo[u] = (int64_t)b * p.ys[ti][0] + (int64_t)sq * p.ys[ti][1] + (int64_t)h * p.ys[ti][2] + d0;
+    L::load(p.x[ti], xo, x1[u]);
+    L::load(p.x[ti], xo + p.half, x2[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < kRopeHG; ++u) {
+    if (h0 + u >= nh) break;
+    const int ti = h0 + u >= p.nh[0] ? 1 : 0;
+    float y1[VEC], y2[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      y1[i] = x1[u][i] * c1[i] - x2[u][i] * s1[i];
+      y2[i] = x2[u][i] * c2[i] + x1[u][i] * s2[i];
+    }
+    L::store(p.y[ti], yo[u], y1);
+    L::store(p.y[ti], yo[u] + p.half, y2);
+  }
+}
+
 }  // namespace vfk
 
 using namespace vfk;
@@ -867,4 +946,85 @@ extern "C" int vfk_rope_fwd(const vfk_tensor* x, const vfk_tensor* cos,
   }
 #undef VFK_ROPE
   return launch_status("vfk_rope_fwd");
+}
+
+static int rope_x_ok(const vfk_tensor* t, const char* name, int dt) {
+  int rc = check_tensor(t, name, 4);
+  if (rc) return rc;
+  if (t->dtype != dt) return set_error(VFK_ERR_INVALID, "vfk_rope_qk_fwd: %s dtype differs from q", name);
+  const int vec = 16 / elem_size(dt);
+  if (t->stride[3] != 1 || !aligned16(t->data) || t->stride[0] % vec || t->stride[1] % vec ||
+      t->stride[2] % vec)
+    return set_error(VFK_ERR_INVALID, "vfk_rope_qk_fwd: %s needs a contiguous last dim and "
+                     "16-byte aligned rows", name);
+  return VFK_OK;
+}
+
+extern "C" int vfk_rope_qk_fwd(const vfk_tensor* q, const vfk_tensor* k, const vfk_tensor* cos,
+                               const vfk_tensor* sin, vfk_tensor* q_out, vfk_tensor* k_out,
+                               void* stream) {
+  int rc;
+  if ((rc = check_tensor(q, "q", 4))) return rc;
+  const int dt = q->dtype;
+  const bool has_k = present(k);
+  if (has_k != present(k_out))
+    return set_error(VFK_ERR_INVALID, "vfk_rope_qk_fwd: k and k_out go together");
+  if ((rc = rope_x_ok(q, "q", dt)) || (rc = rope_x_ok(q_out, "q_out", dt))) return rc;
+  if (has_k && ((rc = rope_x_ok(k, "k", dt)) || (rc = rope_x_ok(k_out, "k_out", dt)))) return rc;
+  const int64_t B = q->size[0], S = q->size[1], D = q->size[3];
+  for (int i = 0; i < 4; ++i)
+    if (q_out->size[i] != q->size[i] || (has_k && k_out->size[i] != k->size[i]))
+      return set_error(VFK_ERR_INVALID, "vfk_rope_qk_fwd: out shape mismatch");
+  if (has_k && (k->size[0] != B || k->size[1] != S || k->size[3] != D))
+    return set_error(VFK_ERR_INVALID, "vfk_rope_qk_fwd: q and k must share B, S and D");
+  const int vec = 16 / elem_size(dt);
+  if (D <= 0 || D % (2 * vec))
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_rope_qk_fwd: head_dim %lld is not a multiple of %d",
+                     (long long)D, 2 * vec);
+  const vfk_tensor* cs[2] = {cos, sin};
+  for (int i = 0; i < 2; ++i) {
+    const vfk_tensor* t = cs[i];
+    if ((rc = check_tensor(t, i ? "sin" : "cos", 3))) return rc;
+    if ((t->size[0] != B && t->size[0] != 1) || t->size[1] != S || t->size[2] != D)
+      return set_error(VFK_ERR_INVALID, "vfk_rope_qk_fwd: cos/sin must be [B|1, S, D]");
+    if (t->dtype != dt && t->dtype != VFK_F32)
+      return set_error(VFK_ERR_INVALID, "vfk_rope_qk_fwd: cos/sin dtype must be q's or fp32");
+    const int tv = 16 / elem_size(t->dtype);
+    if (t->stride[2] != 1 || !aligned16(t->data) || t->stride[1] % tv ||
+        (t->size[0] != 1 && t->stride[0] % tv))
+      return set_error(VFK_ERR_INVALID, "vfk_rope_qk_fwd: cos/sin need 16-byte aligned rows");
+  }
+  if (cos->dtype != sin->dtype)
+    return set_error(VFK_ERR_INVALID, "vfk_rope_qk_fwd: cos and sin dtypes differ");
+  const int64_t rows = B * S;
+  const int64_t cpr = D / 2 / vec;
+  if (rows * cpr >= (1ll << 32) - 256)
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_rope_qk_fwd: too many rows");
+  const int nh = (int)q->size[2] + (has_k ? (int)k->size[2] : 0);
+  if (rows == 0 || nh == 0) return VFK_OK;
+  RopeQKArgs p = {};
+  p.x[0] = q->data; p.y[0] = q_out->data; p.nh[0] = (int)q->size[2];
+  p.x[1] = has_k ? k->data : q->data; p.y[1] = has_k ? k_out->data : q_out->data;
+  p.nh[1] = has_k ? (int)k->size[2] : 0;
+  for (int i = 0; i < 3; ++i) {
+    p.xs[0][i] = q->stride[i]; p.ys[0][i] = q_out->stride[i];
+    p.xs[1][i] = has_k ? k->stride[i] : 0; p.ys[1][i] = has_k ? k_out->stride[i] : 0;
+  }
+  p.c = cos->data; p.cs[0] = cos->size[0] == 1 ? 0 : cos->stride[0]; p.cs[1] = cos->stride[1];
+  p.s = sin->data; p.ss[0] = sin->size[0] == 1 ? 0 : sin->stride[0]; p.ss[1] = sin->stride[1];
+  p.half = (int)(D / 2);
+  p.rows = (uint32_t)rows;
+  const Magic gcp = magic_for((uint32_t)cpr);
+  const Magic gs = magic_for((uint32_t)std::max<int64_t>(1, S));
+  const dim3 grid((unsigned)((rows * cpr + 255) / 256), (unsigned)((nh + kRopeHG - 1) / kRopeHG));
+  hipStream_t st = (hipStream_t)stream;
+  const bool f32t = cos->dtype == VFK_F32;
+#define VFK_RQK(DT, CT) hipLaunchKernelGGL((rope_qk_kernel<DT, CT>), grid, dim3(256), 0, st, p, gcp, gs)
+  switch (dt) {
+    case VFK_F32: VFK_RQK(VFK_F32, VFK_F32); break;
+    case VFK_BF16: if (f32t) VFK_RQK(VFK_BF16, VFK_F32); else VFK_RQK(VFK_BF16, VFK_BF16); break;
+    case VFK_F16: if (f32t) VFK_RQK(VFK_F16, VFK_F32); else VFK_RQK(VFK_F16, VFK_F16); break;
+  }
+#undef VFK_RQK
+  return launch_status("vfk_rope_qk_fwd");
 }

@@ -56,4 +56,10 @@ int deberta_bucket_host(int64_t rel, int bucket_size, int max_position);
 int build_deberta_step(int bucket_size, int max_position, int max_abs,
                        int f_cap, StepFn* out);
 
+// True when f(a) - f(a - 1) is 0 or 1 for every a >= 1: f0 is a0 - 1 or a0
+// and the thresholds strictly increase. The staged and fused DeBERTa kernels
+// size their LDS windows on this (a key tile of 64 keys meets at most 64
+// consecutive indices of a query row).
+bool step_is_unit(const StepFn& s);
+
 }  // namespace vfk

@@ -30,7 +30,8 @@ import torch
 import torch.nn.functional as F
 
 from kernels.activation import activation
-from kernels.flash_deberta_attention import flash_deberta_attention_fused
+from kernels.flash_deberta_attention import (flash_deberta_attention,
+                                             flash_deberta_attention_fused, unit_steps)
 from kernels.fused_layernorm import fused_add_layernorm, fused_layernorm
 from kernels.packing import pad_packed, read_metadata, seq_metadata, unpad_packed
 
@@ -119,10 +120,19 @@ def deberta_layer_forward(x: torch.Tensor, seq_lengths: torch.Tensor, rel: torch
     pr = F.linear(rel[:2 * span], lw.wqkv[:2 * D], lw.bqkv[:2 * D]).view(2 * span, 2, H, d)
     query_rel, key_rel = pr[:, 0].transpose(0, 1), pr[:, 1].transpose(0, 1)
     ctx = torch.empty(B, L, H, d, dtype=x.dtype, device=x.device)
-    flash_deberta_attention_fused(q, k, v, seq_lengths, key_rel, query_rel, 1.0 / math.sqrt(3 * d),
-                                  w.position_buckets if w.position_buckets > 0 else span,
-                                  w.max_relative_positions, w.position_buckets > 0,
-                                  out=ctx.transpose(1, 2))
+    pb = w.position_buckets if w.position_buckets > 0 else span
+    log = w.position_buckets > 0
+    sm = 1.0 / math.sqrt(3 * d)
+    if unit_steps(pb, w.max_relative_positions, log, L):
+        flash_deberta_attention_fused(q, k, v, seq_lengths, key_rel, query_rel, sm, pb,
+                                      w.max_relative_positions, log, out=ctx.transpose(1, 2))
+    else:
+        # bucket steps above 1: the reference interface with materialised
+        # pos_key = q key_rel^T, pos_query = k query_rel^T (:275-286)
+        pos_key = torch.matmul(q, key_rel.transpose(-1, -2).contiguous().unsqueeze(0))
+        pos_query = torch.matmul(k, query_rel.transpose(-1, -2).contiguous().unsqueeze(0))
+        ctx.copy_(flash_deberta_attention(q, k, v, seq_lengths, pos_key, pos_query, False, sm, pb,
+                                          w.max_relative_positions, log).transpose(1, 2))
     h = fused_add_layernorm(F.linear(ctx.view(B, L, D), lw.wo, lw.bo), x, lw.ln1_w, lw.ln1_b,
                             w.eps, return_sum=False)
     inter = activation(F.linear(h, lw.wi, lw.bi), "gelu")

@@ -1,5 +1,10 @@
-"""mT5 encoder layer forward (config 4 shapes: d_model 1024, 16 heads of 64,
+"""mT5 encoder forward (config 4 shapes: d_model 1024, 16 heads of 64,
 gated-GELU d_ff 2816) on the hot-path kernels.
+
+mt5_encoder_forward follows models/mt5/mt5_encoder.py:524-599
+(MT5Encoder.forward): token embeddings (or inputs_embeds), the [B, 1, 1, L]
+additive key mask (1 - m) * finfo.min, every layer with the layer-0 bias table
+[buckets, heads], then the final RMSNorm (:591).
 
 Follows models/mt5/mt5_encoder.py:476-491 (T5EncoderLayer):
     h = x + o_proj(RPB-attention(q, k, v of RMSNorm1(x)))
@@ -10,6 +15,8 @@ residual add is fused into the second RMSNorm and the second into the wo GEMM
 (beta = 1).
 """
 from __future__ import annotations
+
+from typing import Optional
 
 import torch
 
@@ -34,6 +41,29 @@ def mt5_layer_forward(x: torch.Tensor, wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2
     h2, x1 = fused_add_rms_norm(o, x, ln2, eps)
     g = fused_gelu_mul_dropout(h2 @ wi0, h2 @ wi1, "gelu_new")
     return torch.addmm(x1.reshape(-1, D), g.reshape(-1, g.shape[-1]), wff_o).view(B, L, D)
+
+
+def mt5_encoder_forward(input_ids: Optional[torch.Tensor], attention_mask: Optional[torch.Tensor],
+                        layers, table: torch.Tensor, final_ln: torch.Tensor,
+                        embed: Optional[torch.Tensor] = None,
+                        inputs_embeds: Optional[torch.Tensor] = None, num_buckets: int = 32,
+                        max_distance: int = 128, eps: float = 1e-6) -> torch.Tensor:
+    """Padded-batch encoder: input_ids [B, L] (or [L]) with embed [vocab, d_model],
+    or inputs_embeds [B, L, d_model]; attention_mask [B, L] of 1 (keep) / 0
+    (pad) or None; layers: (wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2) per
+    layer as for mt5_layer_forward; table: layer 0's [buckets, heads]."""
+    x = embed[input_ids] if inputs_embeds is None else inputs_embeds
+    squeeze = x.dim() == 2
+    if squeeze:
+        x = x.unsqueeze(0)
+    mask = None
+    if attention_mask is not None:
+        m = attention_mask.reshape(x.shape[0], -1)[:, None, None, :].to(x.dtype)
+        mask = (1.0 - m) * torch.finfo(x.dtype).min
+    for lw in layers:
+        x = mt5_layer_forward(x, *lw, table, mask, num_buckets, max_distance, eps)
+    x = rms_norm(x, final_ln, eps)
+    return x.squeeze(0) if squeeze else x
 
 
 def mt5_encoder_flat(x: torch.Tensor, positions: torch.Tensor, layers, table: torch.Tensor,

@@ -45,6 +45,7 @@ _SIGNATURES = {
     "vfk_abi_version": [],
     "vfk_t5_bucket": [_vp, _vp, ctypes.c_int64, _i32, _i32, _i32],
     "vfk_deberta_bucket": [_vp, _vp, ctypes.c_int64, _i32, _i32],
+    "vfk_deberta_unit_steps": [_i32, _i32, _i32, _i32],
     "vfk_flash_rpb_fwd": [_P, _P, _P, _P, _i32, _i32, _i32, _P, _f32, _P, _vp],
     "vfk_flash_deberta_fwd": [_P, _P, _P, _vp, _P, _P, _i32, _f32, _i32, _i32, _i32, _P, _vp],
     "vfk_deberta_fused_fwd": [_P, _P, _P, _vp, _P, _P, _f32, _i32, _i32, _i32, _P, _vp],
@@ -64,6 +65,7 @@ _SIGNATURES = {
     "vfk_gliner_word_rows": [_vp, _i64, _i64, _vp, _i64, _vp, _vp],
     "vfk_gliner_span_rows": [_vp, _vp, _i64, _i64, _i32, _vp, _i32, _vp, _vp, _vp, _i64, _vp, _vp],
     "vfk_rope_fwd": [_P, _P, _P, _P, _vp],
+    "vfk_rope_qk_fwd": [_P, _P, _P, _P, _P, _P, _vp],
     "vfk_layernorm_fwd": [_P, _P, _P, _P, _f32, _P, _P, _vp],
     "vfk_rmsnorm_fwd": [_P, _P, _P, _f32, _P, _P, _vp],
     "vfk_glu_fwd": [_i32, _P, _P, _P, _vp],

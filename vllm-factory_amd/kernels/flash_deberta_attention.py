@@ -17,6 +17,7 @@ pos_query tensors the reference materialises with two batched matmuls
 """
 from __future__ import annotations
 
+import functools
 import math
 from typing import Optional
 
@@ -32,6 +33,21 @@ HAS_TRITON = False
 def clear_config_cache() -> None:
     """Kept for API compatibility: tile shapes are fixed at build time."""
     return None
+
+
+@functools.lru_cache(maxsize=64)
+def unit_steps(position_buckets: int, max_relative_distance: int, use_log_bucket: bool,
+               max_len: int) -> bool:
+    """Whether c(d) = clamp(bucket(d) + att_span, 0, 2 att_span - 1) moves by at
+    most 1 per unit of distance for |d| <= max_len. The fused kernel needs it;
+    the log bucket of deberta_v2_encoder.py:70-89 breaks it when
+    max_relative_positions is small against position_buckets (e.g. 256 / 256)."""
+    rc = _lib.load().vfk_deberta_unit_steps(int(position_buckets), int(max_relative_distance),
+                                            int(bool(use_log_bucket)), int(max_len))
+    if rc < 0:
+        _lib.call("vfk_deberta_unit_steps", int(position_buckets), int(max_relative_distance),
+                  int(bool(use_log_bucket)), int(max_len))
+    return rc == 1
 
 
 def _seq_lengths(seq_lengths: Optional[torch.Tensor], B: int, dev) -> Optional[torch.Tensor]:
@@ -98,7 +114,9 @@ def flash_deberta_attention_fused(
 
     key_rel, query_rel: [H, 2*ATT_SPAN, D] per-head projections of the
     relative-position embeddings. Equivalent to flash_deberta_attention with
-    pos_key = q @ key_rel^T and pos_query = k @ query_rel^T. `out` may be a
+    pos_key = q @ key_rel^T and pos_query = k @ query_rel^T. Raises
+    NotImplementedError where `unit_steps` is False (flash_deberta_attention
+    covers those bucket settings). `out` may be a
     strided [B, H, M, D] view (e.g. of a [B, M, H, D] buffer) with contiguous
     16-byte-aligned rows; it is written in place and returned.
     """
@@ -124,4 +142,5 @@ def flash_deberta_attention_fused(
     return out
 
 
-__all__ = ["flash_deberta_attention", "flash_deberta_attention_fused", "clear_config_cache", "HAS_TRITON"]
+__all__ = ["flash_deberta_attention", "flash_deberta_attention_fused", "unit_steps",
+           "clear_config_cache", "HAS_TRITON"]

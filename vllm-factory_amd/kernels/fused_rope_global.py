@@ -3,9 +3,12 @@
 Drop-in for kernels/fused_rope_global.py:108-166: `fused_rope_apply(x, cos, sin)`
 and `fused_rope_global_apply(q, k, cos, sin)`, non-interleaved halves:
 out[d] = x[d] cos[d] - x[d+D/2] sin[d] (d < D/2), x[d] cos[d] + x[d-D/2] sin[d]
-otherwise. Inputs [B,S,H,D] with any strides (no contiguous copy is made when
-the last dim is contiguous); cos/sin [B,S,D] or [B,1,S,D]. Returns new
-contiguous tensors.
+otherwise. Inputs [B,S,H,D] (no copy when the last dim is contiguous with
+16-byte aligned rows); cos/sin [B,S,D], [B,1,S,D] or [S,D], in the input's
+dtype or fp32 (used at fp32, as the reference's kernel promotes mixed
+operands; other dtypes are widened to fp32 exactly). Returns new contiguous
+tensors of the input's dtype. q and k are rotated in one launch that loads
+each cos/sin value once per thread for several heads.
 """
 from __future__ import annotations
 
@@ -19,26 +22,38 @@ def _cos_sin(t: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
         t = t.squeeze(1)
     if t.dim() == 2:  # [S, D]
         t = t.unsqueeze(0)
-    if t.dtype != x.dtype:
-        t = t.to(x.dtype)
+    if t.dtype not in (x.dtype, torch.float32):
+        t = t.float()
     return _lib.rows_aligned(t)
+
+
+def _rope(q: torch.Tensor, k, cos: torch.Tensor, sin: torch.Tensor):
+    dev = _lib.require_gpu(q, k, cos, sin)
+    for t in (q, k):
+        if t is not None and t.dim() != 4:
+            raise ValueError("q/k must be [B, S, H, D]")
+    c = _cos_sin(cos, q)
+    s = _cos_sin(sin, q)
+    if c.dtype != s.dtype:
+        c, s = c.float(), s.float()
+    qq = _lib.rows_aligned(q)
+    qo = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    kk = _lib.rows_aligned(k) if k is not None else None
+    ko = torch.empty(k.shape, dtype=k.dtype, device=k.device) if k is not None else None
+    _lib.on_device("vfk_rope_qk_fwd", dev, _lib.ref(_lib.desc(qq)), _lib.ref(_lib.desc(kk)),
+                   _lib.ref(_lib.desc(c)), _lib.ref(_lib.desc(s)), _lib.ref(_lib.desc(qo)),
+                   _lib.ref(_lib.desc(ko)))
+    return qo, ko
 
 
 def fused_rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     """Apply RoPE to a single [B, S, H, D] tensor."""
-    dev = _lib.require_gpu(x, cos, sin)
-    if x.dim() != 4:
-        raise ValueError("x must be [B, S, H, D]")
-    c = _cos_sin(cos, x)
-    s = _cos_sin(sin, x)
-    xx = x if x.stride(-1) == 1 else x.contiguous()
-    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    _lib.on_device("vfk_rope_fwd", dev, _lib.ref(_lib.desc(xx)), _lib.ref(_lib.desc(c)),
-                   _lib.ref(_lib.desc(s)), _lib.ref(_lib.desc(out)))
-    return out
+    return _rope(x, None, cos, sin)[0]
 
 
 def fused_rope_global_apply(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,
                             sin: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Apply RoPE (global) to query and key tensors."""
-    return fused_rope_apply(q, cos, sin), fused_rope_apply(k, cos, sin)
+    """Apply RoPE (global) to query and key tensors, both in one launch."""
+    if k.dtype != q.dtype:
+        raise ValueError("q and k must share a dtype")
+    return _rope(q, k, cos, sin)
