@@ -243,21 +243,24 @@ def epilogue_bench(torch, args, c2):
     emb = torch.cat([fr, fr], -1)
     cos, sin = emb.cos().bfloat16()[None], emb.sin().bfloat16()[None]
     bench("rope_qk", lambda: fused_rope_global_apply(q, k, cos, sin), 4 * T * 768 * 2 + 2 * T * 64 * 2)
+    res["rope_qk"]["launches"] = 1
     # LayerNorm [T, 768] bf16, no bias (ModernBERT)
     g = torch.Generator().manual_seed(1002)
     x = torch.randn(T, 768, generator=g).bfloat16().to(dev)
     w = torch.ones(768, dtype=torch.bfloat16, device=dev)
     bench("layernorm", lambda: fused_layernorm(x, 768, w, None, 1e-5), 2 * T * 768 * 2)
-    # mT5 RMSNorm and gated-GELU at config 4 shapes (valid tokens only counted)
+    # mT5 RMSNorm and gated-GELU at config 4 sizes on the packed valid rows
+    # (20 280 of the 24 576 padded rows), as the packed mT5 layer runs them
     c4 = workloads.config4(device=dev)
     tv = int(c4.lengths.sum())
-    h = c4.hidden.reshape(-1, 1024)
-    bench("rmsnorm", lambda: rms_norm(h, c4.ln1, 1e-6), 2 * h.shape[0] * 1024 * 2)
-    res["rmsnorm"]["valid_token_mb"] = 2 * tv * 1024 * 2 / 1e6
-    gate = torch.randn(32 * 768, 2816, generator=g).bfloat16().to(dev)
-    up = torch.randn(32 * 768, 2816, generator=g).bfloat16().to(dev)
-    bench("gated_gelu", lambda: ffg(gate, up, "gelu_new"), 3 * gate.numel() * 2)
-    del c4, gate, up
+    keep = (torch.arange(c4.hidden.shape[1], device=dev)[None, :] < c4.lengths.to(dev)[:, None])
+    h = c4.hidden[keep].contiguous()
+    bench("rmsnorm", lambda: rms_norm(h, c4.ln1, 1e-6), 2 * tv * 1024 * 2)
+    gate = torch.randn(tv, 2816, generator=g).bfloat16().to(dev)
+    up = torch.randn(tv, 2816, generator=g).bfloat16().to(dev)
+    bench("gated_gelu", lambda: ffg(gate, up, "gelu_new"), 3 * tv * 2816 * 2)
+    res["rmsnorm"]["rows"] = res["gated_gelu"]["rows"] = tv
+    del c4, gate, up, h
     # flat <-> padded rows of the DeBERTa-v3-large GLiNER flat call at config 3
     # sizes: 32 sequences U{256..512} of 1024 bf16 hidden values
     from kernels.packing import pad_packed, unpad_packed
@@ -444,8 +447,18 @@ def cpu_baseline(torch, c2, min_seconds=10.0):
     import workloads
     from oracle import attention as oa
 
-    threads = min(os.cpu_count() or 1, 16)
+    # every core this process may run on (the host's CPUs minus any affinity
+    # restriction the box places on the job)
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     torch.set_num_threads(threads)
+    model = ""
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     qkv = c2.qkv.float().cpu()
     cu = c2.cu_seqlens.cpu().tolist()
     lens = c2.lengths.tolist()
@@ -464,6 +477,7 @@ def cpu_baseline(torch, c2, min_seconds=10.0):
         done += 1
     dt = time.perf_counter() - t0
     return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                host_cpus=os.cpu_count(), cpu_model=model, dtype="fp32",
                 sample=f"{done} sequence-layer pairs cycling over the {len(lens)} config-2 sequences "
                        f"(global + local layer each), fp32 oracle, per-sequence dense softmax, "
                        f"{dt:.1f} s")
