@@ -14,7 +14,11 @@ the memory-bound epilogues in GB/s, the end-to-end tokens/s of the full
 22-layer ModernBERT-base encoder over 256 packed sequences, and the CPU
 oracle timed on the host.
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--only headline|traffic]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
+                       [--only headline|traffic|SECTION[,SECTION...]]
+SECTION names the extra figures to run after the headline (rpb, deberta,
+epilogues, mt5_layer, deberta_layer, deberta_v1_layer, encoder); the default
+runs all of them.
 """
 from __future__ import annotations
 
@@ -61,9 +65,13 @@ class KernelTimer:
 def traffic_workload(torch):
     """Workload of the FETCH_SIZE / WRITE_SIZE counter runs (--only traffic):
     three plain copies of a 512 MiB bf16 tensor (calibration: known bytes,
-    larger than the last-level cache), then the config-2 global and local
-    attention calls three times each."""
+    larger than the last-level cache), then three calls each of the config-2
+    global and local attention, the config-4 RPB attention, the config-3 fused
+    DeBERTa attention and the config-5 ColBERT head."""
     import workloads
+    from kernels.colbert_head import colbert_head
+    from kernels.flash_attention_rpb import flash_attention_rpb_final
+    from kernels.flash_deberta_attention import flash_deberta_attention_fused
     from kernels.varlen_attention import varlen_rope_attention
 
     dev = torch.device("cuda:0")
@@ -79,6 +87,26 @@ def traffic_workload(torch):
     for _ in range(3):
         varlen_rope_attention(q, k, v, c.cu_seqlens, c.max_seqlen, -1, 160000.0, 0.125, out=out)
         varlen_rope_attention(q, k, v, c.cu_seqlens, c.max_seqlen, 64, 10000.0, 0.125, out=out)
+    del c, q, k, v, out
+    c4 = workloads.config4(device=dev)
+    B, L = c4.hidden.shape[:2]
+    g = torch.Generator().manual_seed(1004)
+    q4, k4, v4 = ((torch.randn(B, 16, L, 64, generator=g) * 0.64).bfloat16().to(dev) for _ in range(3))
+    for _ in range(3):
+        flash_attention_rpb_final(q4, k4, v4, c4.table, 32, 128, False, padding_mask=c4.mask)
+    del c4, q4, k4, v4
+    c3 = workloads.config3(device=dev)
+    for _ in range(3):
+        flash_deberta_attention_fused(c3.q, c3.k, c3.v, c3.lengths, c3.key_rel, c3.query_rel,
+                                      c3.sm_scale, 256, 512, True)
+    del c3
+    T5 = 163736
+    pend = torch.randn(T5, 768, generator=g).bfloat16().to(dev)
+    resid = torch.randn(T5, 768, generator=g).bfloat16().to(dev)
+    lnw = torch.ones(768, dtype=torch.bfloat16, device=dev)
+    proj = (torch.randn(128, 768, generator=g) * 0.03).bfloat16().to(dev)
+    for _ in range(3):
+        colbert_head(pend, proj, None, lnw, None, 1e-5, residual=resid)
     torch.cuda.synchronize()
     print("traffic workload done", file=sys.stderr)
 
@@ -494,7 +522,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="'headline' to skip the extra figures; 'traffic' "
-                    "runs only the workload of the HBM-traffic counter runs")
+                    "runs only the workload of the HBM-traffic counter runs; a comma list of "
+                    "sections runs the headline and those")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path is "
@@ -512,14 +541,22 @@ def main():
     head, c2 = headline(torch, args)
     _progress("headline")
     extra = {}
-    if args.only != "headline":
-        for key, fn in (("rpb_mt5_large_config4", lambda: rpb_config4(torch, args)),
-                        ("deberta_v3_large_config3", lambda: deberta_config3(torch, args)),
-                        ("epilogues", lambda: epilogue_bench(torch, args, c2)),
-                        ("mt5_large_layer_config4", lambda: mt5_layer_config4(torch, args)),
-                        ("deberta_v3_large_layer_config3", lambda: deberta_layer_config3(torch, args)),
-                        ("deberta_v1_base_layer_config3", lambda: deberta_v1_layer_config3(torch, args)),
-                        ("modernbert_encoder_config5", lambda: encoder_config5(torch, args))):
+    sections = (("rpb", "rpb_mt5_large_config4", lambda: rpb_config4(torch, args)),
+                ("deberta", "deberta_v3_large_config3", lambda: deberta_config3(torch, args)),
+                ("epilogues", "epilogues", lambda: epilogue_bench(torch, args, c2)),
+                ("mt5_layer", "mt5_large_layer_config4", lambda: mt5_layer_config4(torch, args)),
+                ("deberta_layer", "deberta_v3_large_layer_config3",
+                 lambda: deberta_layer_config3(torch, args)),
+                ("deberta_v1_layer", "deberta_v1_base_layer_config3",
+                 lambda: deberta_v1_layer_config3(torch, args)),
+                ("encoder", "modernbert_encoder_config5", lambda: encoder_config5(torch, args)))
+    wanted = None if not args.only else set(args.only.split(","))
+    unknown = (wanted or set()) - {s[0] for s in sections} - {"headline"}
+    if unknown:
+        print(f"unknown sections {sorted(unknown)}", file=sys.stderr)
+        sys.exit(2)
+    for short, key, fn in sections:
+        if wanted is None or short in wanted:
             extra[key] = fn()
             _progress(key)
     line = {

@@ -162,11 +162,15 @@ int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
                         void* workspace, int64_t workspace_bytes,
                         vfk_tensor* out, void* stream);
 
-/* Workspace size of vfk_varlen_attn_fwd for total_tokens rows (q->size[0]) and
- * num_heads heads: total_tokens * num_heads * 64 * 2 bytes for 16-bit dtypes
- * with RoPE (the rotated K, head-major), else 0. */
+/* Workspace size of vfk_varlen_attn_fwd for total_tokens rows (q->size[0]),
+ * num_heads heads, num_seqs sequences and max_seqlen: for 16-bit dtypes with
+ * RoPE, the rotated and scaled K (head-major, total_tokens * num_heads * 64 * 2
+ * bytes rounded up to 256) plus one fp32 row-norm maximum per (head,
+ * sequence, 64-key tile) (num_heads * num_seqs * ceil(max_seqlen / 64) * 4
+ * bytes); else 0. */
 int64_t vfk_varlen_attn_workspace_bytes(int32_t dtype, int64_t total_tokens,
-                                        int32_t num_heads, int32_t rope);
+                                        int32_t num_heads, int32_t rope,
+                                        int32_t num_seqs, int32_t max_seqlen);
 
 /* Packed-sequence metadata from vLLM's flat position ids, on the device
  * (no counterpart kernel in the reference: it replaces the boundary detection

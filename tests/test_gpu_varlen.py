@@ -146,3 +146,31 @@ def test_varlen_zero_length_sequences(dev, window):
     qd = qkv.to(dev)
     got = _vl()(qd[:, 0], qd[:, 1], qd[:, 2], cu.to(dev), max(lengths), window, 10000.0, 0.125)
     assert_attn_close(got, want, f"zero-length sequences w={window}")
+
+
+@pytest.mark.parametrize("window", [-1, 64])
+def test_varlen_bound_fallback_and_fast_waves(dev, window):
+    """Both softmax paths in one workgroup. With RoPE every wave bounds its
+    scores by |q| * max|k| over its key tiles before the loop: within
+    log2(kPMax) it takes p = exp2(score) directly, otherwise the online
+    softmax with a running max. Sequence 0 holds one key with 100x the norm of
+    the others (masked by key_valid, so it cannot change any output but it
+    sets the bound), which sends its normal rows to the running-max path,
+    while its rows 32..63 (q scaled by 1e-3) stay under the bound; sequence 1
+    is ordinary."""
+    lengths = [300, 200]
+    g = torch.Generator().manual_seed(12)
+    T = sum(lengths)
+    q = torch.randn(T, 12, 64, generator=g) * 0.8
+    k = torch.randn(T, 12, 64, generator=g) * 0.8
+    v = torch.randn(T, 12, 64, generator=g)
+    q[32:64] *= 1e-3
+    k[5] *= 100.0
+    key_valid = torch.ones(T, dtype=torch.bool)
+    key_valid[5] = False
+    cu = workloads.cu_from_lengths(torch.tensor(lengths))
+    q, k, v = (t.bfloat16() for t in (q, k, v))
+    want = oa.varlen_attention(q, k, v, cu, window, 160000.0, key_valid, 0.125)
+    got = _vl()(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), max(lengths), window, 160000.0, 0.125,
+                key_valid=key_valid.to(dev))
+    assert_attn_close(got, want, f"bound fallback w={window}")

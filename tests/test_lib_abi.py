@@ -32,7 +32,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     from kernels import _lib
-    assert _lib.load().vfk_abi_version() == 7
+    assert _lib.load().vfk_abi_version() == 8
 
 
 def _host_t5(rel, bidirectional, nb, md):
@@ -113,10 +113,12 @@ def test_product_rejects_cpu_tensors():
 def test_varlen_workspace_bytes():
     from kernels import _lib
     lib = _lib.load()
-    assert lib.vfk_varlen_attn_workspace_bytes(_lib.BF16, 40265, 12, 1) == 40265 * 12 * 64 * 2
-    assert lib.vfk_varlen_attn_workspace_bytes(_lib.F16, 7, 3, 1) == 7 * 3 * 64 * 2
-    assert lib.vfk_varlen_attn_workspace_bytes(_lib.BF16, 40265, 12, 0) == 0
-    assert lib.vfk_varlen_attn_workspace_bytes(_lib.F32, 40265, 12, 1) == 0
+    # rotated K rounded up to 256 bytes, then one fp32 norm per (head, sequence, key tile)
+    kr = (40265 * 12 * 64 * 2 + 255) // 256 * 256
+    assert lib.vfk_varlen_attn_workspace_bytes(_lib.BF16, 40265, 12, 1, 64, 768) == kr + 12 * 64 * 12 * 4
+    assert lib.vfk_varlen_attn_workspace_bytes(_lib.F16, 7, 3, 1, 2, 5) == 7 * 3 * 128 + 256 - 7 * 3 * 128 % 256 + 3 * 2 * 1 * 4
+    assert lib.vfk_varlen_attn_workspace_bytes(_lib.BF16, 40265, 12, 0, 64, 768) == 0
+    assert lib.vfk_varlen_attn_workspace_bytes(_lib.F32, 40265, 12, 1, 64, 768) == 0
 
 
 def test_packing_argument_checks():

@@ -222,6 +222,33 @@ __device__ inline void softmax_exp(f32x16_t& s0, f32x16_t& s1, float c, float m,
   }
 }
 
+// Probabilities without a reference: p = exp2(s) for scores already in log2
+// units and known to satisfy |s| <= log2(E::kPMax) (a bound computed from
+// |q| and max |k| before the loop), so p can neither overflow the fp32
+// accumulators nor underflow the 16-bit P operand; no row max, no rescale.
+template <typename E>
+__device__ inline void softmax_fixed(f32x16_t& s0, f32x16_t& s1, u32x4_t (&p)[4], float& l) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    s0[i] = fast_exp2(s0[i]);
+    s1[i] = fast_exp2(s1[i]);
+  }
+  float la = s0[0] + s0[1], lb = s1[0] + s1[1];
+#pragma unroll
+  for (int i = 2; i < 16; ++i) {
+    la += s0[i];
+    lb += s1[i];
+  }
+  l += la + lb;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    p[0][j] = E::pack2(s0[2 * j], s0[2 * j + 1]);
+    p[1][j] = E::pack2(s0[8 + 2 * j], s0[8 + 2 * j + 1]);
+    p[2][j] = E::pack2(s1[2 * j], s1[2 * j + 1]);
+    p[3][j] = E::pack2(s1[8 + 2 * j], s1[8 + 2 * j + 1]);
+  }
+}
+
 template <typename E>
 __device__ inline void softmax_tile(f32x16_t& s0, f32x16_t& s1, float c, float& m, float& l,
                                     f32x16_t& o0, f32x16_t& o1,
@@ -473,7 +500,9 @@ __device__ inline void attn_pipe_start(P& pol, int n, uint16_t* __restrict__ K0,
   }
 }
 
-template <typename E, typename P>
+// FIXED: scores arrive in log2 units within +-log2(E::kPMax) (softmax_fixed);
+// otherwise the online softmax with running max m and scale c.
+template <typename E, bool FIXED = false, typename P>
 __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t* __restrict__ K1,
                                     uint16_t* __restrict__ V0, uint16_t* __restrict__ V1, int n,
                                     const u32x4_t (&qf)[4], float c, float& m, float& l,
@@ -500,7 +529,10 @@ __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t*
       qk_tile_sw<E>(Kc, ko, qf, s0, s1);
       const bool exact = pol.modify(s0, s1, i, b);
       u32x4_t p[4];
-      softmax_tile<E>(s0, s1, c, m, l, o0, o1, p, exact);
+      if (FIXED)
+        softmax_fixed<E>(s0, s1, p, l);
+      else
+        softmax_tile<E>(s0, s1, c, m, l, o0, o1, p, exact);
       pv_tile_sw<E>(Vc, vo, p, o0, o1);
     }
     tile_barrier();
@@ -557,8 +589,9 @@ __device__ inline void rope_k_fetch(RopeK& r, const float* __restrict__ table, i
   for (int i = 0; i < 4; ++i) r.v[i] = valid ? t[i] : z;
 }
 
+// Rotates and multiplies by `scale` before the one rounding to 16 bits.
 template <typename E>
-__device__ inline void rope_k_apply(u32x4_t& k0, u32x4_t& k1, const RopeK& r) {
+__device__ inline void rope_k_apply(u32x4_t& k0, u32x4_t& k1, const RopeK& r, float scale = 1.f) {
   float a[8], b[8];
   unpack8<E>(k0, a);
   unpack8<E>(k1, b);
@@ -566,8 +599,8 @@ __device__ inline void rope_k_apply(u32x4_t& k0, u32x4_t& k1, const RopeK& r) {
   for (int i = 0; i < 8; ++i) {
     const float cs_ = r.v[i >> 1][2 * (i & 1)], sn = r.v[i >> 1][2 * (i & 1) + 1];
     const float x1 = a[i], x2 = b[i];
-    a[i] = x1 * cs_ - x2 * sn;
-    b[i] = x2 * cs_ + x1 * sn;
+    a[i] = (x1 * cs_ - x2 * sn) * scale;
+    b[i] = (x2 * cs_ + x1 * sn) * scale;
   }
   k0 = pack8<E>(a);
   k1 = pack8<E>(b);

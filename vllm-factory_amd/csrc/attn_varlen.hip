@@ -10,6 +10,15 @@
 // into a head-major workspace [H][T][64] (the role of the reference's separate
 // rotary step, kernels/fused_rope_global.py); Q is rotated in registers by the
 // attention kernel as it loads its rows.
+//
+// With RoPE the pre-pass also folds c = softmax_scale * log2(e) into K before
+// its one rounding to 16 bits, so the QK^T MFMA yields scores in log2 units,
+// and records the largest row norm of every 64-key tile. From |q| and those
+// norms each wave bounds |score| <= |q| max|k| before its loop; where the
+// bound stays within log2(kPMax) for all its rows, p = exp2(score) is taken
+// directly (no running max, no rescale: it can neither overflow the fp32
+// accumulators nor underflow the 16-bit P operand), otherwise the online
+// softmax with a running max runs as without RoPE.
 #include <math.h>
 
 #include <algorithm>
@@ -26,7 +35,9 @@ struct VarlenArgs {
   float c2;                 // softmax scale * log2(e)
   const float* rope;        // optional [positions][32][2] (cos, sin) table
   const uint8_t* key_valid; // optional, [T]
-  const void* kr;           // RoPE: rotated K, head-major [H][T][64]
+  const void* kr;           // RoPE: rotated, scaled K, head-major [H][T][64]
+  float* kmax;              // RoPE: max row norm of each key tile [H][nseq][nkt]
+  int nkt;                  // key tiles per sequence slot: ceil(max_seqlen / 64)
   int64_t T;
 };
 
@@ -59,23 +70,46 @@ constexpr int kPenLen = 2 * kPenOff;
 // sequence s for heads [kPackHeads g, kPackHeads g + kPackHeads); thread t
 // handles row t >> 2 and d chunks cp = t & 3 and cp + 4 (the rotate-half
 // partners d and d + 32), loading the row's cos/sin once for its heads. All
-// of a thread's loads are issued before any store, with head indices clamped
-// so that the loads are unconditional; one pass per block, no head loop.
+// of a thread's loads are issued before any store, with head and row indices
+// clamped so that the loads are unconditional; one pass per block, no head
+// loop. The rows are stored multiplied by c2 = softmax_scale * log2(e), and
+// the largest Euclidean norm of the tile's stored rows per head goes to
+// kmax[h][s][kt].
 constexpr int kPackHeads = 6;
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+template <typename E>
+__device__ inline float sumsq8(u32x4_t v) {
+  float f[8];
+  unpack8<E>(v, f);
+  float r = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r = __builtin_fmaf(f[i], f[i], r);
+  return r;
+}
 
 template <typename E>
 __global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int nkt) {
+  __shared__ float part[4][kPackHeads];
   const int kt = blockIdx.x % nkt;
   const int s = blockIdx.x / nkt;
   const int tok0 = a.cu[s];
   const int n = a.cu[s + 1] - tok0;
+  if (kt * 64 >= n) return;  // uniform: no row of the sequence in this tile
   const int row = kt * 64 + (threadIdx.x >> 2);
-  if (row >= n) return;
+  const bool valid = row < n;
+  const int rr = valid ? row : kt * 64;  // tail threads load a valid row, store nothing
   const int cp = threadIdx.x & 3;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int h0 = blockIdx.y * kPackHeads;
   RopeK rk;
-  rope_k_fetch(rk, a.rope, row, true);
-  const uint16_t* src = reinterpret_cast<const uint16_t*>(a.k) + (int64_t)(tok0 + row) * a.ks[0] + 8 * cp;
+  rope_k_fetch(rk, a.rope, rr, true);
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(a.k) + (int64_t)(tok0 + rr) * a.ks[0] + 8 * cp;
   uint16_t* dst = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(a.kr)) +
                   (int64_t)(tok0 + row) * 64 + 8 * cp;
   const int64_t hs = (int64_t)a.T * 64;
@@ -88,12 +122,27 @@ __global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int nkt)
   }
 #pragma unroll
   for (int u = 0; u < kPackHeads; ++u) {
+    float nrm = 0.f;
     if (h0 + u < a.H) {
-      rope_k_apply<E>(k0[u], k1[u], rk);
-      uint16_t* q = dst + (h0 + u) * hs;
-      *reinterpret_cast<u32x4_t*>(q) = k0[u];
-      *reinterpret_cast<u32x4_t*>(q + 32) = k1[u];
+      rope_k_apply<E>(k0[u], k1[u], rk, a.c2);
+      if (valid) {
+        uint16_t* q = dst + (h0 + u) * hs;
+        *reinterpret_cast<u32x4_t*>(q) = k0[u];
+        *reinterpret_cast<u32x4_t*>(q + 32) = k1[u];
+        nrm = sumsq8<E>(k0[u]) + sumsq8<E>(k1[u]);
+      }
     }
+    // squared row norm (the row's 4 threads form a quad), then the wave's max
+    nrm += __shfl_xor(nrm, 1);
+    nrm += __shfl_xor(nrm, 2);
+    nrm = wave_max(nrm);
+    if (lane == 0) part[w][u] = nrm;
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < kPackHeads && h0 + t < a.H) {
+    const float m = fmaxf(fmaxf(part[0][t], part[1][t]), fmaxf(part[2][t], part[3][t]));
+    a.kmax[((int64_t)(h0 + t) * a.nseq + s) * a.nkt + kt] = sqrtf(m);
   }
 }
 
@@ -145,7 +194,7 @@ struct VarlenPolicy {
 };
 
 template <typename E, bool ROPE, bool LOCAL, bool KVALID>
-__global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenArgs a) {
+__global__ __launch_bounds__(256, 4) void varlen_fwd_kernel(VarlenArgs a) {
   __shared__ __align__(16) uint16_t K0[kTileElems];
   __shared__ __align__(16) uint16_t K1[kTileElems];
   __shared__ __align__(16) uint16_t V0[kTileElems];
@@ -209,7 +258,27 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenArgs a) {
 
   float m = -INFINITY, l = 0.f;
   f32x16_t o0 = {}, o1 = {};
-  attn_loop_db<E>(pol, K0, K1, V0, V1, kt_end - kt_begin, qf, a.c2, m, l, o0, o1);
+  const int ntiles = kt_end - kt_begin;
+  if (ROPE) {
+    // |score| <= |q| max|k| over the workgroup's key tiles (scores are in
+    // log2 units: K carries c2); the margin covers the fp32 norms and the
+    // MFMA's fp32 accumulation
+    const float* km = a.kmax + ((int64_t)h * a.nseq + s) * a.nkt;
+    float kx = 0.f;
+    for (int j = kt_begin + lane; j < kt_end; j += 64) kx = fmaxf(kx, km[j]);
+    kx = wave_max(kx);
+    float q2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q2 += sumsq8<E>(qf[i]);
+    q2 = half_swap_sum(q2);
+    const float ub = sqrtf(q2) * kx * 1.0078125f + 0.0625f;
+    if (__builtin_amdgcn_ballot_w64(ub > E::kLog2PMax) == 0ull)
+      attn_loop_db<E, true>(pol, K0, K1, V0, V1, ntiles, qf, 1.f, m, l, o0, o1);
+    else
+      attn_loop_db<E, false>(pol, K0, K1, V0, V1, ntiles, qf, 1.f, m, l, o0, o1);
+  } else {
+    attn_loop_db<E, false>(pol, K0, K1, V0, V1, ntiles, qf, a.c2, m, l, o0, o1);
+  }
 
   const float l_tot = half_swap_sum(l);
   if (qvalid) {
@@ -324,10 +393,16 @@ static int check_thd(const vfk_tensor* t, const char* name, int dtype, int64_t T
   return VFK_OK;
 }
 
+static int64_t kr_bytes(int64_t T, int64_t H) { return (T * H * kHD * 2 + 255) / 256 * 256; }
+
 extern "C" int64_t vfk_varlen_attn_workspace_bytes(int32_t dtype, int64_t total_tokens,
-                                                  int32_t num_heads, int32_t rope) {
-  if (!rope || dtype == VFK_F32 || total_tokens <= 0 || num_heads <= 0) return 0;
-  return total_tokens * num_heads * kHD * 2;
+                                                  int32_t num_heads, int32_t rope,
+                                                  int32_t num_seqs, int32_t max_seqlen) {
+  if (!rope || dtype == VFK_F32 || total_tokens <= 0 || num_heads <= 0 || num_seqs <= 0 ||
+      max_seqlen <= 0)
+    return 0;
+  const int64_t nkt = (max_seqlen + 63) / 64;
+  return kr_bytes(total_tokens, num_heads) + (int64_t)num_heads * num_seqs * nkt * 4;
 }
 
 extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
@@ -383,7 +458,7 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: max_seqlen x row stride too large");
   const bool rope = a.rope != nullptr;
   if (rope) {
-    const int64_t need = vfk_varlen_attn_workspace_bytes(dt, T, (int32_t)H, 1);
+    const int64_t need = vfk_varlen_attn_workspace_bytes(dt, T, (int32_t)H, 1, num_seqs, max_seqlen);
     if (!workspace || workspace_bytes < need)
       return set_error(VFK_ERR_INVALID, "vfk_varlen_attn_fwd: RoPE needs a workspace of %lld bytes",
                        (long long)need);
@@ -391,6 +466,8 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
       return set_error(VFK_ERR_INVALID, "workspace must be 16-byte aligned");
     a.kr = workspace;
     const int nkt = ceil_div(max_seqlen, 64);
+    a.nkt = nkt;
+    a.kmax = reinterpret_cast<float*>(static_cast<char*>(workspace) + kr_bytes(T, H));
     const int64_t pblocks = (int64_t)num_seqs * nkt;
     if (pblocks >= (1ll << 31))
       return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: grid too large");

@@ -33,6 +33,7 @@ struct BF16 {
   // largest accepted probability bound of the softmax fast path: keeps the
   // fp32 output accumulators far from overflow
   static constexpr float kPMax = 1099511627776.0f;  // 2^40
+  static constexpr float kLog2PMax = 40.0f;
   typedef bf16x8_t vec8;
   __device__ static inline float to_f32(uint16_t b) {
     return __uint_as_float(((uint32_t)b) << 16);
@@ -63,6 +64,7 @@ struct F16 {
   static constexpr int code = VFK_F16;
   // probabilities must stay representable in f16 (max 65504)
   static constexpr float kPMax = 32768.0f;
+  static constexpr float kLog2PMax = 15.0f;
   typedef f16x8_t vec8;
   __device__ static inline float to_f32(uint16_t b) {
     return (float)__builtin_bit_cast(_Float16, b);

@@ -51,7 +51,7 @@ _SIGNATURES = {
     "vfk_deberta_fused_fwd": [_P, _P, _P, _vp, _P, _P, _f32, _i32, _i32, _i32, _P, _vp],
     "vfk_varlen_attn_fwd": [_P, _P, _P, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _i64,
                             _P, _vp],
-    "vfk_varlen_attn_workspace_bytes": [_i32, _i64, _i32, _i32],
+    "vfk_varlen_attn_workspace_bytes": [_i32, _i64, _i32, _i32, _i32, _i32],
     "vfk_rope_table": [_f32, _i32, _vp, _vp],
     "vfk_varlen_meta": [_vp, _i32, _i64, _i32, _vp, _vp, _vp, _i64, _vp],
     "vfk_pad_rows": [_vp, _i64, _vp, _i32, _i32, _i32, ctypes.c_uint64, _vp, _vp, _vp],

@@ -74,7 +74,8 @@ def varlen_rope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         tab = rope_table(rope_theta, int(max_seqlen), dev)
         tab_ptr, tab_n = tab.data_ptr(), tab.shape[0]
     ws_bytes = int(_lib.load().vfk_varlen_attn_workspace_bytes(
-        _lib.dtype_code(q.dtype), int(q.shape[0]), int(q.shape[1]), int(rope)))
+        _lib.dtype_code(q.dtype), int(q.shape[0]), int(q.shape[1]), int(rope),
+        int(cu_seqlens.numel() - 1), int(max_seqlen)))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     _lib.on_device(
         "vfk_varlen_attn_fwd", dev,
