@@ -322,6 +322,49 @@ constexpr int kTileElems = 64 * 64;          // u16 per K or V tile (8 KiB)
 
 __device__ inline int swz(int row) { return (((row >> 1) & 1) << 2) | ((row >> 2) & 3); }
 
+// Writes this wave's 32 normalised output rows through LDS so that the global
+// stores are whole rows: the lane's values (query row c, d in the O^T layout)
+// go to `stage` (32 rows x 128 B, 16-byte chunks swizzled like the tiles),
+// then lane l stores the 16-byte chunk l & 7 of rows l >> 3, +8, +16, +24,
+// eight lanes per 128-byte row. rowp(r) gives row r's output address (rows
+// for which valid(r) is false are skipped). Call with the stage free (after
+// the loop's last barrier); the stage is this wave's own.
+template <typename E, typename RowP, typename Valid>
+__device__ inline void store_out_rows(uint16_t* __restrict__ stage, f32x16_t o0, f32x16_t o1,
+                                      float l_tot, RowP rowp, Valid valid) {
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  const int f = swz(c);
+  char* st = reinterpret_cast<char*>(stage);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    u32x2_t w0, w1;
+    w0[0] = E::pack2(o0[4 * j] * inv, o0[4 * j + 1] * inv);
+    w0[1] = E::pack2(o0[4 * j + 2] * inv, o0[4 * j + 3] * inv);
+    w1[0] = E::pack2(o1[4 * j] * inv, o1[4 * j + 1] * inv);
+    w1[1] = E::pack2(o1[4 * j + 2] * inv, o1[4 * j + 3] * inv);
+    // d = 8j + 4h (chunk j) and d + 32 (chunk j + 4), 8 bytes at 8h in the chunk
+    *reinterpret_cast<u32x2_t*>(st + c * 128 + 16 * (j ^ f) + 8 * h) = w0;
+    *reinterpret_cast<u32x2_t*>(st + c * 128 + 16 * ((j + 4) ^ f) + 8 * h) = w1;
+  }
+  // other lanes of this wave read what each lane wrote
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int q = lane & 7;
+  u32x4_t v[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int r = (lane >> 3) + 8 * k;
+    v[k] = *reinterpret_cast<const u32x4_t*>(st + r * 128 + 16 * (q ^ swz(r)));
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int r = (lane >> 3) + 8 * k;
+    if (valid(r)) *reinterpret_cast<u32x4_t*>(rowp(r) + 8 * q) = v[k];
+  }
+}
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 

@@ -281,10 +281,12 @@ __global__ __launch_bounds__(256, 4) void varlen_fwd_kernel(VarlenArgs a) {
   }
 
   const float l_tot = half_swap_sum(l);
-  if (qvalid) {
-    uint16_t* orow = reinterpret_cast<uint16_t*>(a.o) + (int64_t)(tok0 + qrow) * a.os[0] + h * a.os[1];
-    store_out<E>(orow, o0, o1, l_tot);
-  }
+  // whole-row stores through this wave's half of K0 / K1 (free after the
+  // loop's last barrier; a workgroup with no key tile never touched them)
+  uint16_t* ob = reinterpret_cast<uint16_t*>(a.o) + (int64_t)tok0 * a.os[0] + h * a.os[1];
+  store_out_rows<E>((w < 2 ? K0 : K1) + (w & 1) * 2048, o0, o1, l_tot,
+                    [&](int r) { return ob + (int64_t)(wq_lo + r) * a.os[0]; },
+                    [&](int r) { return wq_lo + r < n; });
 }
 
 // fp32: one thread per query row, exact fp32 arithmetic, accurate sin/cos.
