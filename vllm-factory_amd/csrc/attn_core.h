@@ -520,7 +520,10 @@ __device__ inline void pv_tile_sw(const uint16_t* __restrict__ Vt, const VOff& v
 // The policy P supplies, for virtual tile index i in [0, n):
 //   int  key0(i)
 //   void loadK(int i, uint16_t* Kt), loadV(int i, uint16_t* Vt)   direct loads
-//   void meta(int i, int slot)          per-tile LDS metadata, slot = i & 1
+//   M    meta_ld(int i)                 per-tile metadata of tile i, loaded
+//                                       early (before the tile's DMA) ...
+//   void meta_st(M v, int slot)         ... and written to LDS slot i & 1
+//                                       late, before the step's barrier
 //   bool wave_active()                  the wave has a valid query row
 //   static constexpr bool kAllActive    every tile is active for such waves
 //   bool active(int i)                  the wave computes tile i
@@ -534,12 +537,14 @@ template <typename P>
 __device__ inline void attn_pipe_start(P& pol, int n, uint16_t* __restrict__ K0,
                                        uint16_t* __restrict__ K1, uint16_t* __restrict__ V0) {
   if (n <= 0) return;
+  const auto m0 = pol.meta_ld(0);
   pol.loadK(0, K0);
   pol.loadV(0, V0);
-  pol.meta(0, 0);
+  pol.meta_st(m0, 0);
   if (n > 1) {
+    const auto m1 = pol.meta_ld(1);
     pol.loadK(1, K1);
-    pol.meta(1, 1);
+    pol.meta_st(m1, 1);
   }
 }
 
@@ -559,12 +564,12 @@ __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t*
   tile_barrier();
   auto step = [&](int i, uint16_t* __restrict__ Kc, uint16_t* __restrict__ Vc,
                   uint16_t* __restrict__ Kn, uint16_t* __restrict__ Vn, int b) {
-    // tile 1's K and meta were issued with tile 0
+    // tile 1's K and meta were issued with tile 0; the next tile's metadata is
+    // loaded before its DMA and written to LDS after this tile's compute
+    const bool meta_next = i + 1 < n && i > 0;
+    const auto mn = pol.meta_ld(meta_next ? i + 1 : i);
     if (i + 1 < n) {
-      if (i > 0) {
-        pol.loadK(i + 1, Kn);
-        pol.meta(i + 1, b ^ 1);
-      }
+      if (i > 0) pol.loadK(i + 1, Kn);
       pol.loadV(i + 1, Vn);
     }
     if (wave_on && (P::kAllActive || __builtin_amdgcn_readfirstlane((int)pol.active(i)) != 0)) {
@@ -578,6 +583,7 @@ __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t*
         softmax_tile<E>(s0, s1, c, m, l, o0, o1, p, exact);
       pv_tile_sw<E>(Vc, vo, p, o0, o1);
     }
+    if (meta_next) pol.meta_st(mn, b ^ 1);
     tile_barrier();
   };
   int i = 0;

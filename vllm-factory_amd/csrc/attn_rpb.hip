@@ -16,6 +16,8 @@
 namespace vfk {
 
 enum { MASK_NONE = 0, MASK_KEY = 1, MASK_FULL = 2 };
+// LDS copy of the step thresholds: VFK_MAX_THR int16 rounded to 16 bytes
+constexpr int kThrPad = (VFK_MAX_THR + 7) & ~7;
 
 struct RpbArgs {
   const void* q; const void* k; const void* v; void* o;
@@ -71,20 +73,24 @@ struct RpbPolicy {
   float* maskt;          // MASK_KEY: [2][kBN] mask values of the tile in slot i & 1
   const float* lut;      // bias per relative position (raw score units) or nullptr
   int lut_base, b, h, t, hl, qrow, wq_lo, wq_hi;
+  bool nolive;           // MASK_KEY: every key of the row range masked away
 
   static constexpr bool kAllActive = !CAUSAL;
   __device__ int tile(int i) const { return tiles ? tiles[i] : i; }
   __device__ int key0(int i) const { return tile(i) * kBN; }
   __device__ void loadK(int i, uint16_t* Kt) { tile_load_buf(ksrc, key0(i), Kt); }
   __device__ void loadV(int i, uint16_t* Vt) { tile_load_buf(vsrc, key0(i), Vt); }
-  __device__ void meta(int i, int slot) {
-    if (MASK == MASK_KEY && t < kBN) {
-      const int j = key0(i) + t;
-      maskt[slot * kBN + t] =
-          j < a->Lk ? mask_raw(ld_f(a->mask, a->mask_dt, b * a->ms[0] + h * a->ms[1] + j * a->ms[3]),
-                               a->inv_scale)
-                    : 0.f;
-    }
+  // key-mask values of the tile, wave 0 one key per lane; only tiles that
+  // hold a nonzero value are loaded (right padding leaves one such tile)
+  __device__ float meta_ld(int i) const {
+    if (MASK != MASK_KEY || t >= kBN || !(tflag[tile(i)] & 1)) return 0.f;
+    const int j = key0(i) + t;
+    return j < a->Lk ? mask_raw(ld_f(a->mask, a->mask_dt, b * a->ms[0] + h * a->ms[1] + j * a->ms[3]),
+                                a->inv_scale)
+                     : 0.f;
+  }
+  __device__ void meta_st(float v, int slot) {
+    if (MASK == MASK_KEY && t < kBN) maskt[slot * kBN + t] = v;
   }
   __device__ bool wave_active() const { return wq_lo < a->Lq; }
   __device__ bool active(int i) const {
@@ -93,14 +99,19 @@ struct RpbPolicy {
   }
   __device__ bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot) const {
     const int k0 = key0(i);
-    if (lut) add_by_key(s0, s1, lut + k0 + lut_base);
     bool exact = false;
-    if (MASK == MASK_KEY) {
-      if (tflag[tile(i)] & 1) {
-        add_by_key(s0, s1, maskt + slot * kBN + 4 * hl);
-        exact = true;  // tiles carrying additive mask values: exact exponent form
-      }
-    } else if (MASK == MASK_FULL) {
+    if (MASK == MASK_KEY && nolive) {
+      // every key's mask is below -1e30 (raw units): scores and biases are
+      // absorbed by it, so the row averages V over its keys
+      s0 = f32x16_t{};
+      s1 = f32x16_t{};
+    } else {
+      if (lut) add_by_key(s0, s1, lut + k0 + lut_base);
+      // masked keys (-1e30) fall far below the row max of the live keys:
+      // the fma exponent form underflows them to 0 without an exact path
+      if (MASK == MASK_KEY && (tflag[tile(i)] & 1)) add_by_key(s0, s1, maskt + slot * kBN + 4 * hl);
+    }
+    if (MASK == MASK_FULL) {
       if (qrow < a->Lq) {
         const int64_t mo = b * a->ms[0] + h * a->ms[1] + (int64_t)qrow * a->ms[2];
         map_scores(s0, s1, [&](int e, float v) {
@@ -123,7 +134,7 @@ struct RpbPolicy {
 };
 
 template <typename E, int MASK, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void rpb_fwd_kernel(RpbArgs a) {
+__global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   __shared__ __align__(16) uint16_t K0[kTileElems];
   __shared__ __align__(16) uint16_t K1[kTileElems];
   __shared__ __align__(16) uint16_t V0[kTileElems];
@@ -146,12 +157,31 @@ __global__ __launch_bounds__(256, 2) void rpb_fwd_kernel(RpbArgs a) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, hl = lane >> 5;
 
   // ---- bias table over rel = key - query, rel in [-(q0+127), Lk-1-q0] ----
+  // the step thresholds and the head's table column go to LDS first, so each
+  // entry is a binary search and a lookup in LDS
   const bool has_table = a.table != nullptr;
   if (has_table) {
+    int16_t* thr = reinterpret_cast<int16_t*>(lut + a.lut_len);
+    float* tcol = reinterpret_cast<float*>(thr + kThrPad);
+    for (int e = t; e < a.step.nthr; e += 256) thr[e] = a.step.thr[e];
+    for (int e = t; e < a.total_buckets; e += 256)
+      tcol[e] = ld_f(a.table, a.table_dt, e * a.tb0 + h * a.tb1) * a.inv_scale;
+    __syncthreads();
+    const int a0 = a.step.a0, f0 = a.step.f0, nthr = a.step.nthr;
     for (int e = t; e < a.lut_len; e += 256) {
       const int rel = e - q0 - (kBM - 1);
-      const int bk = rpb_bucket(a, rel);
-      lut[e] = ld_f(a.table, a.table_dt, bk * a.tb0 + h * a.tb1) * a.inv_scale;
+      const int mag = a.bidir ? (rel < 0 ? -rel : rel) : (rel < 0 ? -rel : 0);
+      int bk = mag;
+      if (mag >= a0) {
+        int lo = 0, hi = nthr;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if ((int)thr[mid] <= mag) lo = mid + 1; else hi = mid;
+        }
+        bk = f0 + lo;
+      }
+      if (a.bidir && rel > 0) bk += a.offset_pos;
+      lut[e] = tcol[min(max(bk, 0), a.total_buckets - 1)];
     }
   }
   // ---- key tiles: causal limit, and (key mask) the tiles with a live key ----
@@ -193,6 +223,12 @@ __global__ __launch_bounds__(256, 2) void rpb_fwd_kernel(RpbArgs a) {
   pol.tflag = tflag;
   pol.maskt = maskt;
   pol.lut = has_table ? lut : nullptr;
+  pol.nolive = false;
+  if (MASK == MASK_KEY) {
+    int live = 0;
+    for (int i = 0; i < kt_end; ++i) live |= tflag[i] & 2;
+    pol.nolive = live == 0;
+  }
   pol.b = b; pol.h = h; pol.t = t; pol.hl = hl;
   pol.wq_lo = q0 + w * 32;
   pol.qrow = pol.wq_lo + (lane & 31);
@@ -210,11 +246,12 @@ __global__ __launch_bounds__(256, 2) void rpb_fwd_kernel(RpbArgs a) {
   f32x16_t o0 = {}, o1 = {};
   attn_loop_db<E>(pol, K0, K1, V0, V1, n, qf, a.c2, m, l, o0, o1);
   const float l_tot = half_swap_sum(l);
-  if (qvalid) {
-    uint16_t* orow = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1] +
-                     (int64_t)pol.qrow * a.os[2];
-    store_out<E>(orow, o0, o1, l_tot);
-  }
+  // whole-row stores through this wave's half of K0 / K1 (free after the loop)
+  uint16_t* ob = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1];
+  const int wq_lo = pol.wq_lo;
+  store_out_rows<E>((w < 2 ? K0 : K1) + (w & 1) * 2048, o0, o1, l_tot,
+                    [&](int r) { return ob + (int64_t)(wq_lo + r) * a.os[2]; },
+                    [&](int r) { return wq_lo + r < a.Lq; });
 }
 
 // ---------------------------------------------------------------------------
@@ -375,8 +412,10 @@ extern "C" int vfk_flash_rpb_fwd(const vfk_tensor* q, const vfk_tensor* k,
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_rpb_fwd: Lk x row stride too large");
   const int ntiles = ceil_div(Lk, kBN);
   a.lut_len = a.table ? ntiles * kBN + kBM : 0;
-  // dynamic LDS: tile flags and list, bias table (tiles and masks are static)
-  const size_t lds = (size_t)((ntiles + 3) & ~3) * 8 + (size_t)a.lut_len * 4;
+  // dynamic LDS: tile flags and list, bias table, step thresholds and the
+  // head's table column (tiles and masks are static)
+  const size_t lds = (size_t)((ntiles + 3) & ~3) * 8 + (size_t)a.lut_len * 4 +
+                     (a.table ? (size_t)kThrPad * 2 + (size_t)a.total_buckets * 4 : 0);
   if (lds + 4 * kTileElems * 2 + 2 * kBN * 4 > 160 * 1024)
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_rpb_fwd: Lk=%lld needs too much LDS",
                      (long long)Lk);

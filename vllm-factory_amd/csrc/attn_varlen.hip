@@ -159,15 +159,17 @@ struct VarlenPolicy {
   __device__ int key0(int i) const { return (kt0 + i) * kBN; }
   __device__ void loadK(int i, uint16_t* Kt) { tile_load_buf(ksrc, key0(i), Kt); }
   __device__ void loadV(int i, uint16_t* Vt) { tile_load_buf(vsrc, key0(i), Vt); }
-  __device__ void meta(int i, int slot) {
-    if (!KVALID) return;
-    if (t < kBN) {  // wave 0: one key per lane
-      const int j = key0(i) + t;
-      const bool ok = j < n && a->key_valid[tok0 + j] != 0;
-      kmask[slot * kBN + t] = ok ? 0.f : -INFINITY;
-      const unsigned long long dead = __builtin_amdgcn_ballot_w64(!ok);
-      if (t == 0) kflag[slot] = dead != 0ull;
-    }
+  // wave 0, one key per lane: key_valid of the tile's keys
+  __device__ bool meta_ld(int i) const {
+    if (!KVALID || t >= kBN) return true;
+    const int j = key0(i) + t;
+    return j < n && a->key_valid[tok0 + j] != 0;
+  }
+  __device__ void meta_st(bool ok, int slot) {
+    if (!KVALID || t >= kBN) return;
+    kmask[slot * kBN + t] = ok ? 0.f : -INFINITY;
+    const unsigned long long dead = __builtin_amdgcn_ballot_w64(!ok);
+    if (t == 0) kflag[slot] = dead != 0ull;
   }
   static constexpr bool kAllActive = !LOCAL;
   __device__ bool wave_active() const { return wq_lo < n; }
