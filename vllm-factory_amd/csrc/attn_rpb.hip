@@ -141,6 +141,7 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   __shared__ __align__(16) uint16_t V1[kTileElems];
   __shared__ float maskt[MASK == MASK_KEY ? 2 * kBN : 1];
   __shared__ int ntl;
+  __shared__ int nolive_s;
   extern __shared__ __align__(16) unsigned char smem[];
   const int ntiles_all = (a.Lk + kBN - 1) / kBN;
   const int nt4 = (ntiles_all + 3) & ~3;
@@ -188,29 +189,48 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   int kt_end = ntiles_all;
   if (CAUSAL) kt_end = min(kt_end, (min(q0 + kBM, a.Lq) - 1) / kBN + 1);
   int n = kt_end;
+  bool direct = true;  // live tiles are 0 .. n-1 (no list indirection)
   if (MASK == MASK_KEY) {
-    for (int i = t; i < nt4; i += 256) tflag[i] = 0;
-    __syncthreads();
+    // pass i: thread t reads key 256 i + t, so wave w holds key tile 4 i + w
+    // and its ballots give that tile's flags (no atomics)
     const char* mb = reinterpret_cast<const char*>(a.mask);
-    for (int j = t; j < a.Lk; j += 256) {
-      const float mv = ld_f(mb, a.mask_dt, b * a.ms[0] + h * a.ms[1] + j * a.ms[3]);
+    for (int j0 = 0; j0 < ntiles_all * kBN; j0 += 256) {
+      const int j = j0 + t;
+      float mv = 0.f;
+      if (j < a.Lk) mv = ld_f(mb, a.mask_dt, b * a.ms[0] + h * a.ms[1] + j * a.ms[3]);
       // bit0: some nonzero value; bit1: some key that is not clamped away
-      const int f = (mv != 0.f ? 1 : 0) | (mask_raw(mv, a.inv_scale) > -1.0e30f ? 2 : 0);
-      if (f) atomicOr(&tflag[j / kBN], f);
+      const unsigned long long nz = __builtin_amdgcn_ballot_w64(mv != 0.f);
+      const unsigned long long lv = __builtin_amdgcn_ballot_w64(j < a.Lk && mask_raw(mv, a.inv_scale) > -1.0e30f);
+      const int tile = (j0 >> 6) + w;
+      if (lane == 0 && tile < ntiles_all) tflag[tile] = (nz ? 1 : 0) | (lv ? 2 : 0);
     }
     __syncthreads();
-    if (t == 0) {
-      // tiles whose every key is masked away are skipped, unless no key of
-      // the row range is live (then the reference averages all of them)
-      int live = 0;
-      for (int i = 0; i < kt_end; ++i) live |= tflag[i] & 2;
+    // tiles whose every key is masked away are skipped, unless no key of the
+    // row range is live (then the reference averages all of them); wave 0
+    // compacts the list, 64 tiles per pass
+    if (w == 0) {
+      unsigned long long live_any = 0;
+      for (int i0 = 0; i0 < kt_end; i0 += 64)
+        live_any |= __builtin_amdgcn_ballot_w64(i0 + lane < kt_end && (tflag[i0 + lane] & 2));
       int c = 0;
-      for (int i = 0; i < kt_end; ++i)
-        if (!live || (tflag[i] & 2)) tiles[c++] = i;
-      ntl = c;
+      bool prefix = true;
+      for (int i0 = 0; i0 < kt_end; i0 += 64) {
+        const int i = i0 + lane;
+        const bool keep = i < kt_end && (!live_any || (tflag[i] & 2));
+        const unsigned long long kb = __builtin_amdgcn_ballot_w64(keep);
+        const int pos = c + __builtin_amdgcn_mbcnt_hi((unsigned)(kb >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)kb, 0u));
+        if (keep) tiles[pos] = i;
+        prefix = prefix && __builtin_amdgcn_ballot_w64(keep && pos != i) == 0ull;
+        c += __builtin_popcountll(kb);
+      }
+      if (lane == 0) {
+        ntl = prefix ? -c : c;  // negative: the list is 0 .. c-1
+        nolive_s = live_any == 0ull;
+      }
     }
     __syncthreads();
-    n = ntl;
+    n = ntl < 0 ? -ntl : ntl;
+    direct = ntl < 0;
   }
 
   RpbPolicy<E, MASK, CAUSAL> pol;
@@ -219,16 +239,11 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
                 (int)a.ks[2], a.Lk);
   tile_src_init(pol.vsrc, reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1],
                 (int)a.vs[2], a.Lk);
-  pol.tiles = MASK == MASK_KEY ? tiles : nullptr;
+  pol.tiles = (MASK == MASK_KEY && !direct) ? tiles : nullptr;
   pol.tflag = tflag;
   pol.maskt = maskt;
   pol.lut = has_table ? lut : nullptr;
-  pol.nolive = false;
-  if (MASK == MASK_KEY) {
-    int live = 0;
-    for (int i = 0; i < kt_end; ++i) live |= tflag[i] & 2;
-    pol.nolive = live == 0;
-  }
+  pol.nolive = MASK == MASK_KEY && nolive_s != 0;
   pol.b = b; pol.h = h; pol.t = t; pol.hl = hl;
   pol.wq_lo = q0 + w * 32;
   pol.qrow = pol.wq_lo + (lane & 31);
