@@ -10,7 +10,8 @@
  *     argument (message in vfk_last_error()), or a positive hipError_t value
  *     when the HIP launch itself failed.
  * The library keeps no mutable global state besides the thread-local error
- * message, so concurrent calls from several host threads are safe.
+ * message (and the per-GPU array of vfk_varlen_meta_noalloc, below), so
+ * concurrent calls from several host threads are safe, that one excepted.
  *
  * Strides are in elements. A stride of 0 broadcasts that dimension.
  */
@@ -201,6 +202,20 @@ int vfk_varlen_meta(const void* positions, int32_t pos_dtype_bytes,
 
 /* Workspace size of vfk_varlen_meta: 4 bytes per 1024 tokens. */
 int64_t vfk_varlen_meta_workspace_bytes(int64_t total_tokens);
+
+/* vfk_varlen_meta with no workspace argument and no allocation of any kind.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc). Same arguments, kernels and results as vfk_varlen_meta; the
+ * per-block counts live in a 64 KiB device array built into the library (one
+ * per GPU, held until the process ends), so total_tokens is limited to
+ * VFK_NOALLOC_MAX_TOKENS (VFK_ERR_UNSUPPORTED above it). Every call on one GPU
+ * shares that array: calls that overlap on one GPU (two streams, two host
+ * threads) race and must be serialised by the caller. */
+#define VFK_NOALLOC_MAX_TOKENS (16384LL * 1024LL)
+int vfk_varlen_meta_noalloc(const void* positions, int32_t pos_dtype_bytes,
+                            int64_t total_tokens, int32_t rule, int32_t* cu_seqlens,
+                            int32_t* meta, void* stream);
 
 /* Flat rows -> padded batch. Replaces the per-row copy loop of
  * plugins/deberta_gliner/model.py:171-191 (batched_ids[row, :length] =

@@ -32,7 +32,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     from kernels import _lib
-    assert _lib.load().vfk_abi_version() == 8
+    assert _lib.load().vfk_abi_version() == 9
 
 
 def _host_t5(rel, bidirectional, nb, md):
@@ -87,6 +87,16 @@ def test_deberta_unit_steps_matches_oracle(pb, mrp):
     assert _lib.load().vfk_deberta_unit_steps(pb, mrp, 0, L) == 1   # linear positions
     if (pb, mrp) in ((256, 256), (256, 300), (128, 128)):
         assert want == 0
+
+
+def test_noalloc_meta_rejects_sizes_above_its_array():
+    """vfk_varlen_meta_noalloc checks total_tokens against its built-in array
+    before any HIP call, so the rejection runs without a GPU."""
+    from kernels import _lib
+    lib = _lib.load()
+    rc = lib.vfk_varlen_meta_noalloc(None, 8, 16384 * 1024 + 1, 0, None, None, None)
+    assert rc == -2
+    assert b"above the 16777216" in lib.vfk_last_error()
 
 
 def test_invalid_arguments_raise():

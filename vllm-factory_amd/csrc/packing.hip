@@ -33,6 +33,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "launch_util.h"
 #include "vfk_common.h"
@@ -565,6 +566,54 @@ extern "C" int vfk_varlen_meta(const void* positions, int32_t pos_dtype_bytes, i
     else launch_meta<1>(static_cast<const int32_t*>(positions), T, nblk, counts, cu_seqlens, meta, st);
   }
   return launch_status("vfk_varlen_meta");
+}
+
+// ---------------------------------------------------------------------------
+// vfk_varlen_meta without a caller workspace: the per-block start counts live
+// in a file-scope device array (one copy per GPU, kept for the life of the
+// process). Host code never passes the array's name to a kernel: its device
+// address is looked up once per device with hipGetSymbolAddress and cached.
+// ---------------------------------------------------------------------------
+constexpr int kNoAllocMetaBlocks = (int)(VFK_NOALLOC_MAX_TOKENS / kMetaBlock);  // 64 KiB of counts
+static_assert((int64_t)kNoAllocMetaBlocks * kMetaBlock == VFK_NOALLOC_MAX_TOKENS, "whole blocks");
+static __device__ __align__(256) int32_t scratch[kNoAllocMetaBlocks];
+
+static std::mutex g_scratch_mu;
+static int32_t* g_scratch_ptr[64];
+
+// scratch's device address on the current device (looked up on first use)
+static int scratch_ptr(int32_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error((int)e, "vfk_varlen_meta_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_meta_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(e != hipSuccess ? (int)e : VFK_ERR_INVALID,
+                       "vfk_varlen_meta_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return VFK_OK;
+}
+
+extern "C" int vfk_varlen_meta_noalloc(const void* positions, int32_t pos_dtype_bytes,
+                                       int64_t total_tokens, int32_t rule, int32_t* cu_seqlens,
+                                       int32_t* meta, void* stream) {
+  if (total_tokens > VFK_NOALLOC_MAX_TOKENS)
+    return set_error(VFK_ERR_UNSUPPORTED,
+                     "vfk_varlen_meta_noalloc: total_tokens %lld above the %lld this entry point "
+                     "holds (use vfk_varlen_meta with a workspace)",
+                     (long long)total_tokens, (long long)VFK_NOALLOC_MAX_TOKENS);
+  int32_t* counts = nullptr;
+  int rc = scratch_ptr(&counts);
+  if (rc) return rc;
+  // every count the kernels read is written by the same call first
+  return vfk_varlen_meta(positions, pos_dtype_bytes, total_tokens, rule, cu_seqlens, meta, counts,
+                         (int64_t)kNoAllocMetaBlocks * (int64_t)sizeof(int32_t), stream);
 }
 
 // Copy unit: the widest of 16/8/4/2/1 bytes dividing the row size and both

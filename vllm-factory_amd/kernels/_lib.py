@@ -54,6 +54,7 @@ _SIGNATURES = {
     "vfk_varlen_attn_workspace_bytes": [_i32, _i64, _i32, _i32, _i32, _i32],
     "vfk_rope_table": [_f32, _i32, _vp, _vp],
     "vfk_varlen_meta": [_vp, _i32, _i64, _i32, _vp, _vp, _vp, _i64, _vp],
+    "vfk_varlen_meta_noalloc": [_vp, _i32, _i64, _i32, _vp, _vp, _vp],
     "vfk_pad_rows": [_vp, _i64, _vp, _i32, _i32, _i32, ctypes.c_uint64, _vp, _vp, _vp],
     "vfk_unpad_rows": [_vp, _i64, _vp, _i32, _i32, _vp, _vp],
     "vfk_varlen_meta_workspace_bytes": [_i64],
