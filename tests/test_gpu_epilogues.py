@@ -135,8 +135,10 @@ def test_rope_table(dev, dtype, cos_rank):
 def test_rope_fp32_tables_used_at_fp32(dev, dtype):
     """16-bit q/k with fp32 cos/sin (the reference's Triton kernel promotes
     the mixed product to fp32): the tables are not rounded to q's dtype first,
-    so the result is the fp32 rotation rounded once. Different head counts for
-    q and k put both tensors into one head group of the launch."""
+    so the result is the fp32 rotation rounded once. q and k have different
+    head counts (7 and 5, not multiples of the kernel's head slots), and
+    D = 64 runs the unit-layout kernel; test_rope_head_dim_32_general_kernel
+    covers the general one."""
     from kernels.fused_rope_global import fused_rope_global_apply
     from oracle.attention import rope_cos_sin
     B, S, D = 2, 333, 64
@@ -148,16 +150,34 @@ def test_rope_fp32_tables_used_at_fp32(dev, dtype):
         want = oe.rope_table(x, cos[None], sin[None])                  # fp32 tables, fp32 math
         assert got.dtype == dtype
         assert_elem_close(got, want, dtype, f"rope fp32-table {name}")
-        # the output is the fp32 result rounded once: it equals the oracle
-        # rounded to q's dtype except at rare rounding ties; tables rounded to
-        # q's dtype first would change many more elements
+        # the output is the fp32 result (products rounded separately, then
+        # the add) rounded once: it equals the oracle rounded to q's dtype at
+        # every element; tables rounded to q's dtype first would change about
+        # a quarter of them
         got_c = got.cpu()
         exact = (got_c == want.to(dtype)).float().mean().item()
         lossy = oe.rope_table(x, cos[None].to(dtype), sin[None].to(dtype)).to(dtype)
         lossy_exact = (lossy == want.to(dtype)).float().mean().item()
         print(f"rope {dtype} {name}: {exact:.5f} of elements equal the rounded fp32 result "
               f"(tables rounded first: {lossy_exact:.5f})")
-        assert exact >= 0.99 and exact > lossy_exact + 0.02, (exact, lossy_exact)
+        assert exact == 1.0 and lossy_exact < 0.9, (exact, lossy_exact)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_head_dim_32_general_kernel(dev, dtype):
+    """D = 32 (4 chunks of 8 per head: outside the unit layout) through the
+    general kernel, fp32 tables, q and k of 3 and 9 heads: every element
+    equals the oracle's fp32 result rounded once."""
+    from kernels.fused_rope_global import fused_rope_global_apply
+    from oracle.attention import rope_cos_sin
+    B, S, D = 3, 97, 32
+    q = _rand((B, S, 3, D), dtype, 23)
+    k = _rand((B, S, 9, D), dtype, 24)
+    cos, sin = rope_cos_sin(torch.arange(S) * 5 + 1, 10000.0, D)
+    gq, gk = fused_rope_global_apply(q.to(dev), k.to(dev), cos.to(dev), sin.to(dev))
+    for got, x in ((gq, q), (gk, k)):
+        want = oe.rope_table(x, cos[None], sin[None]).to(dtype)
+        assert torch.equal(got.cpu(), want)
 
 
 def test_rope_fp32(dev):

@@ -4,6 +4,8 @@
 #include <math.h>
 
 #include <algorithm>
+#include <cstdlib>
+#include <type_traits>
 
 #include "launch_util.h"
 #include "vfk_common.h"
@@ -832,13 +834,86 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeQKArgs p, Magic gcp, M
     if (h0 + u >= nh) break;
     const int ti = h0 + u >= p.nh[0] ? 1 : 0;
     float y1[VEC], y2[VEC];
+    {
+      // products rounded separately, as in the unfused fp32 formula
+#pragma clang fp contract(off)
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      y1[i] = x1[u][i] * c1[i] - x2[u][i] * s1[i];
-      y2[i] = x2[u][i] * c2[i] + x1[u][i] * s2[i];
+      for (int i = 0; i < VEC; ++i) {
+        y1[i] = x1[u][i] * c1[i] - x2[u][i] * s1[i];
+        y2[i] = x2[u][i] * c2[i] + x1[u][i] * s2[i];
+      }
     }
     L::store(p.y[ti], yo[u], y1);
     L::store(p.y[ti], yo[u] + p.half, y2);
+  }
+}
+
+// Unit layout of the same operation for D = CPU * VEC: a unit is one (row,
+// head) vector of D contiguous elements and CPU consecutive lanes own its
+// chunks, so a wave's load and store instructions cover whole units (for
+// D = 64 and 16-bit types: 2 rows x 4 adjacent heads, two 512-byte runs).
+// Lane j owns chunk j and also loads the chunk j +- CPU/2 that pairs with it
+// in the rotation (the wave's own first load has just brought that line into
+// the vector cache). A thread takes the heads hs, hs + kRopeSlots, ... of one
+// row, in q and then in k (the tensor is uniform over the wave, so its
+// strides stay scalar), and loads its cos/sin chunks once. Products are
+// rounded separately before the add (x cos, then the partner times sin), as
+// in the unfused fp32 formula.
+constexpr int kRopeSlots = 4;  // head slots per row
+constexpr int kRopeUnits = 3;  // heads per slot and tensor loaded together
+template <int DT, int CT, int CPU>
+__global__ __launch_bounds__(256) void rope_unit_kernel(RopeQKArgs p, Magic gs) {
+  using L = Elt<DT>;
+  constexpr int VEC = L::VEC;
+  constexpr int RB = 256 / (CPU * kRopeSlots);  // rows per block
+  static_assert(RB >= 1 && CPU % 2 == 0, "unit layout");
+  const int t = threadIdx.x;
+  const int j = t % CPU;
+  const int hs = (t / CPU) % kRopeSlots;
+  const uint32_t row = blockIdx.x * (uint32_t)RB + (uint32_t)(t / (CPU * kRopeSlots));
+  if (row >= p.rows) return;
+  const uint32_t b = magic_div(row, gs);
+  const uint32_t sq = row - b * gs.d;
+  const bool lo = j < CPU / 2;
+  const int d0 = j * VEC;
+  const int dp = lo ? d0 + p.half : d0 - p.half;
+  float c[VEC], s[VEC];
+  load_tab<CT, VEC>(p.c, (int64_t)b * p.cs[0] + (int64_t)sq * p.cs[1] + d0, c);
+  load_tab<CT, VEC>(p.s, (int64_t)b * p.ss[0] + (int64_t)sq * p.ss[1] + d0, s);
+  // first half: x cos - partner sin = x cos + partner (-sin), exactly
+  if (lo) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) s[i] = -s[i];
+  }
+  using U16 = typename std::conditional<DT == VFK_F32, float, uint16_t>::type;
+#pragma unroll
+  for (int ti = 0; ti < 2; ++ti) {
+    const int nh = p.nh[ti];
+    // row bases in 64 bits, head offsets in 32 (heads * head stride < 2^31)
+    const U16* xb = reinterpret_cast<const U16*>(p.x[ti]) + (int64_t)b * p.xs[ti][0] + (int64_t)sq * p.xs[ti][1];
+    U16* yb = reinterpret_cast<U16*>(p.y[ti]) + (int64_t)b * p.ys[ti][0] + (int64_t)sq * p.ys[ti][1];
+    const int xh = (int)p.xs[ti][2], yh = (int)p.ys[ti][2];
+    for (int hb = hs; hb < nh; hb += kRopeUnits * kRopeSlots) {
+      float x[kRopeUnits][VEC], xq[kRopeUnits][VEC];
+#pragma unroll
+      for (int u = 0; u < kRopeUnits; ++u) {
+        const int xo = min(hb + u * kRopeSlots, nh - 1) * xh;
+        L::load(xb, xo + d0, x[u]);
+        L::load(xb, xo + dp, xq[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kRopeUnits; ++u) {
+        const int h = hb + u * kRopeSlots;
+        if (h >= nh) break;
+        float y[VEC];
+        {
+#pragma clang fp contract(off)
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) y[i] = x[u][i] * c[i] + xq[u][i] * s[i];
+        }
+        L::store(yb, h * yh + d0, y);
+      }
+    }
   }
 }
 
@@ -1016,9 +1091,33 @@ extern "C" int vfk_rope_qk_fwd(const vfk_tensor* q, const vfk_tensor* k, const v
   p.rows = (uint32_t)rows;
   const Magic gcp = magic_for((uint32_t)cpr);
   const Magic gs = magic_for((uint32_t)std::max<int64_t>(1, S));
-  const dim3 grid((unsigned)((rows * cpr + 255) / 256), (unsigned)((nh + kRopeHG - 1) / kRopeHG));
   hipStream_t st = (hipStream_t)stream;
   const bool f32t = cos->dtype == VFK_F32;
+  // unit layout when a D-vector is 8 or 16 chunks (D = 64 or 128 for 16-bit types)
+  const int64_t cpu = 2 * cpr;
+  bool unit_ok = dt != VFK_F32 && (cpu == 8 || cpu == 16);
+  for (int i = 0; i < 2 && unit_ok; ++i) {
+    const vfk_tensor* xt = i ? (has_k ? k : q) : q;
+    const vfk_tensor* yt = i ? (has_k ? k_out : q_out) : q_out;
+    unit_ok = xt->size[2] * (std::llabs(xt->stride[2]) + 1) + D < (1ll << 31) &&
+              yt->size[2] * (std::llabs(yt->stride[2]) + 1) + D < (1ll << 31);
+  }
+  if (unit_ok) {
+#define VFK_RU(DT, CT, C)                                                              \
+  hipLaunchKernelGGL((rope_unit_kernel<DT, CT, C>),                                    \
+                     dim3((unsigned)((rows + 256 / (C * kRopeSlots) - 1) / (256 / (C * kRopeSlots)))), \
+                     dim3(256), 0, st, p, gs)
+    if (dt == VFK_BF16) {
+      if (cpu == 8) { if (f32t) VFK_RU(VFK_BF16, VFK_F32, 8); else VFK_RU(VFK_BF16, VFK_BF16, 8); }
+      else { if (f32t) VFK_RU(VFK_BF16, VFK_F32, 16); else VFK_RU(VFK_BF16, VFK_BF16, 16); }
+    } else {
+      if (cpu == 8) { if (f32t) VFK_RU(VFK_F16, VFK_F32, 8); else VFK_RU(VFK_F16, VFK_F16, 8); }
+      else { if (f32t) VFK_RU(VFK_F16, VFK_F32, 16); else VFK_RU(VFK_F16, VFK_F16, 16); }
+    }
+#undef VFK_RU
+    return launch_status("vfk_rope_qk_fwd");
+  }
+  const dim3 grid((unsigned)((rows * cpr + 255) / 256), (unsigned)((nh + kRopeHG - 1) / kRopeHG));
 #define VFK_RQK(DT, CT) hipLaunchKernelGGL((rope_qk_kernel<DT, CT>), grid, dim3(256), 0, st, p, gcp, gs)
   switch (dt) {
     case VFK_F32: VFK_RQK(VFK_F32, VFK_F32); break;
