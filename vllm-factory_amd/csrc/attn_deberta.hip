@@ -383,6 +383,17 @@ constexpr int kPTElems = kBN * kPTs;
 constexpr int kCElems = 32 * kCs;       // per wave
 constexpr int kFusedStaticLds = (3 * kTileElems + kPTElems + 4 * kCElems) * 2;
 
+// Buffer resource over nbytes from base, built from readfirstlane'd words:
+// the values are uniform, and saying so keeps the compiler from wrapping each
+// load through it in a loop over distinct resource values.
+__device__ inline rsrc_t uniform_rsrc(const void* base, int nbytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  void* ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, 0, __builtin_amdgcn_readfirstlane(nbytes), kRsrcWord3);
+}
+
 // Rel-table MFMA operand through a buffer resource over the table's 2S rows
 // (rows past the table read as zeros; their products are never used): lane
 // byte offset voff = row-in-block * rs2 + 16 h, block row offset in soff.
@@ -467,12 +478,10 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
   tile_src_init(vsrc, reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1], (int)a.vs[2], len);
   tile_load_buf(ksrc, 0, K0);
   const int kr_rs2 = C2P ? (int)a.krs[1] * 2 : 0, qr_rs2 = P2C ? (int)a.qrs[1] * 2 : 0;
-  const rsrc_t kr_r = __builtin_amdgcn_make_buffer_rsrc(
-      C2P ? const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(a.kr) + h * a.krs[0]) : nullptr, 0,
-      2 * a.span * kr_rs2, kRsrcWord3);
-  const rsrc_t qr_r = __builtin_amdgcn_make_buffer_rsrc(
-      P2C ? const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(a.qr) + h * a.qrs[0]) : nullptr, 0,
-      2 * a.span * qr_rs2, kRsrcWord3);
+  const rsrc_t kr_r = uniform_rsrc(
+      C2P ? reinterpret_cast<const uint16_t*>(a.kr) + h * a.krs[0] : nullptr, 2 * a.span * kr_rs2);
+  const rsrc_t qr_r = uniform_rsrc(
+      P2C ? reinterpret_cast<const uint16_t*>(a.qr) + h * a.qrs[0] : nullptr, 2 * a.span * qr_rs2);
   const int kr_lane = cl * kr_rs2 + 16 * hl, qr_lane = cl * qr_rs2 + 16 * hl;
 
   u32x4_t qf[4];
