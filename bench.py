@@ -366,6 +366,40 @@ def epilogue_bench(torch, args, c2):
     bench("gliner_span_rows", lambda: gliner_span_rows(st_rep, en_rep, row_cu, s_idx, s_mask, span_cu),
           S * (2 * row + 24) + 2 * W * row)
     res["gliner_span_rows"].update(spans=S)
+    # the marker's out_project first layer (Linear(1536, 3072) + ReLU) on all
+    # spans: pair rows then the [S, 1536] x [1536, 3072] GEMM, against the
+    # split form (relu(start) W1a^T and relu(end) W1b^T per word row, then
+    # relu(a[i] + b[j] + b1) per span); both end with [S, 3072] bf16
+    from kernels.activation import activation
+    from kernels.gliner_pooler import gliner_span_hidden
+    w1 = (torch.randn(3072, 1536, generator=g) * 0.02).bfloat16().to(dev)
+    b1 = (torch.randn(3072, generator=g) * 0.02).bfloat16().to(dev)
+    w1a, w1b = w1[:, :768].contiguous(), w1[:, 768:].contiguous()
+
+    def pair_linear():
+        return torch.relu_(torch.addmm(b1, gliner_span_rows(st_rep, en_rep, row_cu, s_idx, s_mask, span_cu),
+                                       w1.t()))
+
+    def split_linear():
+        a = torch.matmul(activation(st_rep, "relu"), w1a.t())
+        b = torch.matmul(activation(en_rep, "relu"), w1b.t())
+        return gliner_span_hidden(a, b, b1, row_cu, s_idx, s_mask, span_cu)
+    ha = torch.matmul(activation(st_rep, "relu"), w1a.t())
+    hb = torch.matmul(activation(en_rep, "relu"), w1b.t())
+    bench("gliner_span_hidden", lambda: gliner_span_hidden(ha, hb, b1, row_cu, s_idx, s_mask, span_cu),
+          S * (3072 * 2 + 24) + 2 * W * 3072 * 2)
+    res["gliner_span_hidden"].update(spans=S, note="bytes: output rows, index lists and a, b read once")
+    del ha, hb
+    for name, fn in (("span_first_layer_pair_rows", pair_linear), ("span_first_layer_split", split_linear)):
+        for _ in range(max(1, args.warmup // 5)):
+            fn()
+        res[name] = dict(ms=device_ms(torch, fn, max(2, args.steps // 10)), spans=S)
+    res["span_first_layer_split"]["speedup"] = (res["span_first_layer_pair_rows"]["ms"]
+                                                / res["span_first_layer_split"]["ms"])
+    hid = split_linear()
+    ref = pair_linear()
+    res["span_first_layer_split"]["max_abs_vs_pair"] = (hid.float() - ref.float()).abs().max().item()
+    del hid, ref
     return res
 
 

@@ -304,7 +304,12 @@ int vfk_gliner_word_rows(const void* tok, int64_t row_bytes,
  * for span s of request r (span_cu[r] <= s < span_cu[r + 1]) over r's
  * L = row_cu[r + 1] - row_cu[r] rows of start_rep / end_rep,
  * out[s] = relu(cat(start_rep[row_cu[r] + i], end_rep[row_cu[r] + j])) with
- * i, j = span_idx[s][0 / 1] * (span_mask[s] != 0) clamped to [0, L - 1].
+ * i, j = span_idx[s][0 / 1] * span_mask[s] (the reference multiplies the
+ * indices by the mask value, :286) clamped to [0, L - 1].
+ * L must be the request's fitted row count: the reference first pads (with
+ * zero word rows) or truncates its word rows to target_W =
+ * span_idx.size(1) // max_width (:285-286, _fit_length :299-311) and
+ * projects those, so row_cu describes the projections of the fitted rows.
  * start_rep, end_rep [num_rows = row_cu[num_requests], row_bytes] and out [num_spans,
  * 2 * row_bytes] of dtype VFK_BF16 / VFK_F16 / VFK_F32, rows 16-byte aligned,
  * row_bytes a multiple of 16; span_idx int64 [num_spans, 2], span_mask int64
@@ -316,6 +321,24 @@ int vfk_gliner_span_rows(const void* start_rep, const void* end_rep,
                          int32_t num_requests, const int64_t* span_idx,
                          const int64_t* span_mask, const int32_t* span_cu,
                          int64_t num_spans, void* out, void* stream);
+
+/* The first layer of SpanMarkerV0's out_project (poolers/gliner.py:141-143,
+ * create_projection_layer :26-37: Linear(2D, 4D) then ReLU) on every span
+ * without the pair rows: since relu(cat(s, e)) = cat(relu(s), relu(e)), the
+ * layer's output for the span (i, j) is relu(a[i] + b[j] + bias) with
+ * a = relu(start_rep) W1[:, :D]^T and b = relu(end_rep) W1[:, D:]^T computed
+ * once per row (the caller's GEMMs) and bias = b1. out[s] = relu(a[row_cu[r]
+ * + i] + b[row_cu[r] + j] + bias), summed in fp32 in that order and rounded
+ * once to the dtype, with r, i, j as in vfk_gliner_span_rows (a request with
+ * L == 0 gives relu(bias)). a, b [num_rows, row_bytes], bias [row_bytes] or
+ * NULL (no bias), out [num_spans, row_bytes], same dtypes and layout rules as
+ * vfk_gliner_span_rows. */
+int vfk_gliner_span_hidden(const void* a, const void* b, const void* bias,
+                           int64_t row_bytes, int64_t num_rows, int32_t dtype,
+                           const int32_t* row_cu, int32_t num_requests,
+                           const int64_t* span_idx, const int64_t* span_mask,
+                           const int32_t* span_cu, int64_t num_spans, void* out,
+                           void* stream);
 
 /* RoPE cos/sin table of transformers' ModernBertRotaryEmbedding (default rope,
  * head_dim 64; the module the reference calls at

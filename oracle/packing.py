@@ -10,7 +10,8 @@ re-pads them for a padded encoder:
     request of the flat stream (poolers/gliner.py:201, :219-255);
   * gliner_default_spans / gliner_span_rows: the pooler's default span list
     (poolers/gliner.py:270-283) and SpanMarkerV0's start/end pair rows
-    (:131-145 with extract_elements :40-45).
+    (:131-145 with extract_elements :40-45); gliner_fit_length (_fit_length
+    :299-311) and gliner_out_project (the marker's out_project, :141-144).
 Pinned in tests/test_oracle_packing.py by construction (positions built from
 known lengths; hidden rows that encode their own index), hand cases, a
 pairwise brute force and round trips.
@@ -130,12 +131,36 @@ def gliner_span_rows(start_rep: torch.Tensor, end_rep: torch.Tensor, span_idx: t
     L = start_rep.shape[0]
     rows = []
     for (a, b), m in zip(span_idx.tolist(), span_mask.tolist()):
-        a, b = (a, b) if m else (0, 0)
+        a, b = a * int(m), b * int(m)        # span_idx * span_mask.unsqueeze(-1), :286
         i, j = min(max(a, 0), L - 1), min(max(b, 0), L - 1)
         rows.append(torch.cat([start_rep[i], end_rep[j]]))
     if not rows:
         return start_rep.new_zeros(0, 2 * start_rep.shape[1])
     return torch.relu(torch.stack(rows))
+
+
+def gliner_fit_length(we: torch.Tensor, target_len: int) -> torch.Tensor:
+    """_fit_length of poolers/gliner.py:299-311 for one request's word rows
+    [L, D]: the first target_len rows, or all rows followed by zero rows up to
+    target_len (applied at :285-286 with target_W = span_idx.size(1) //
+    max_width)."""
+    L = we.shape[0]
+    if L >= target_len:
+        return we[:target_len]
+    return torch.cat([we, we.new_zeros(target_len - L, we.shape[1])])
+
+
+def gliner_out_project(pair_rows: torch.Tensor, w1: torch.Tensor, b1, w2: torch.Tensor,
+                       b2) -> torch.Tensor:
+    """SpanMarkerV0's out_project (poolers/gliner.py:141-144) in eval mode on
+    its pair rows: create_projection_layer (:26-37) is Linear(2D, 4D), ReLU,
+    Dropout (identity), Linear(4D, D); fp32."""
+    h = pair_rows.float() @ w1.float().t()
+    if b1 is not None:
+        h = h + b1.float()
+    h = torch.relu(h)
+    out = h @ w2.float().t()
+    return out + b2.float() if b2 is not None else out
 
 
 def gliner_default_spans(block_len: int, true_len: int, max_width: int):

@@ -6,6 +6,7 @@ import torch
 
 import workloads
 from oracle import packing as op
+from _tol import cosine
 
 pytestmark = pytest.mark.gpu
 
@@ -120,7 +121,7 @@ def _span_batch(dtype, D, seed):
         else:            # caller-given spans: out-of-range indices, random masks
             S = int(torch.randint(0, 60, (1,), generator=g))
             i = torch.randint(-5, L + 5, (S, 2), generator=g)
-            m = torch.randint(0, 2, (S,), generator=g)
+            m = torch.randint(0, 3, (S,), generator=g)   # mask values multiply the indices
         idxs.append(i)
         masks.append(m)
         counts.append(i.shape[0])
@@ -159,3 +160,113 @@ def test_gliner_span_rows_special_values():
     assert torch.equal(out[0, 1:8].view(torch.int16), want[1:8].view(torch.int16))
     assert torch.equal(out[0, 9:].view(torch.int16), want[9:].view(torch.int16))
     assert torch.all(out[1] == 0) and not torch.any(torch.signbit(out[1].float()))
+
+
+def _span_sources(lens, idxs, masks):
+    """(i, j) source rows of every span (global row numbers), read back from
+    the oracle's pair rows of rows that encode their own index."""
+    src, base = [], 0
+    for L, i, m in zip(lens, idxs, masks):
+        enc = (torch.arange(L, dtype=torch.float64) + 1).unsqueeze(1)
+        rows = op.gliner_span_rows(enc, enc, i, m)
+        src.append(rows.long() - 1 + base)
+        base += L
+    return torch.cat(src)
+
+
+@pytest.mark.parametrize("dtype, N", [(torch.bfloat16, 3072), (torch.float32, 256),
+                                      (torch.float16, 24)])
+def test_gliner_span_hidden_matches_gathered_sum(dtype, N):
+    """relu(a[i] + b[j] + bias) per span, bit for bit against the same fp32
+    sum in that order over the oracle's source rows (mask values of 0, 1, 2,
+    clamped indices, default and caller-given span lists)."""
+    from kernels.gliner_pooler import gliner_span_hidden
+    _, _, lens, idxs, masks, row_cu, span_cu = _span_batch(dtype, 8, 100 + N)
+    W = sum(lens)
+    g = torch.Generator().manual_seed(N)
+    a = torch.randn(W, N, generator=g).to(dtype)
+    b = torch.randn(W, N, generator=g).to(dtype)
+    bias = torch.randn(N, generator=g).to(dtype)
+    print(f"gliner span hidden {dtype} N={N} spans={int(span_cu[-1])}", flush=True)
+    got = gliner_span_hidden(a.cuda(), b.cuda(), bias.cuda(), row_cu.cuda(), torch.cat(idxs).cuda(),
+                             torch.cat(masks).cuda(), span_cu.cuda()).cpu()
+    src = _span_sources(lens, idxs, masks)
+    want = torch.relu((a.float()[src[:, 0]] + b.float()[src[:, 1]]) + bias.float()).to(dtype)
+    assert torch.equal(got, want)
+    nob = gliner_span_hidden(a.cuda(), b.cuda(), None, row_cu.cuda(), torch.cat(idxs).cuda(),
+                             torch.cat(masks).cuda(), span_cu.cuda()).cpu()
+    assert torch.equal(nob, torch.relu(a.float()[src[:, 0]] + b.float()[src[:, 1]]).to(dtype))
+
+
+def test_gliner_span_hidden_request_without_rows():
+    """A request with no rows gives relu(bias) for each of its spans."""
+    from kernels.gliner_pooler import gliner_span_hidden
+    a = torch.randn(3, 16).bfloat16()
+    bias = torch.linspace(-1, 1, 16).bfloat16()
+    out = gliner_span_hidden(a.cuda(), a.cuda(), bias.cuda(), torch.tensor([0, 3, 3]),
+                             torch.tensor([[0, 1], [1, 1], [0, 0]]), torch.tensor([1, 1, 1]),
+                             torch.tensor([0, 2, 3])).cpu()
+    assert torch.equal(out[2], torch.relu(bias.float()).bfloat16())
+    assert torch.equal(out[0], torch.relu(a[0].float() + a[1].float() + bias.float()).bfloat16())
+
+
+def test_fit_word_rows_matches_oracle():
+    """Per-request _fit_length over packed word rows: cut, kept and padded."""
+    from kernels.gliner_pooler import fit_word_rows
+    g = torch.Generator().manual_seed(9)
+    lens, targets = [5, 3, 0, 7], [3, 3, 4, 9]
+    we = torch.randn(sum(lens), 8, generator=g).bfloat16()
+    cu = [0] + torch.tensor(lens).cumsum(0).tolist()
+    rows, row_cu = fit_word_rows(we.cuda(), cu, targets)
+    assert row_cu.cpu().tolist() == [0, 3, 6, 10, 19]
+    want = torch.cat([op.gliner_fit_length(we[cu[r]:cu[r + 1]], t) for r, t in enumerate(targets)])
+    assert torch.equal(rows.cpu(), want)
+
+
+def test_span_marker_forward_matches_oracle():
+    """SpanMarkerV0's out_project over every span of a packed batch with the
+    first Linear split per word row, against the oracle's composition
+    (pair rows, then Linear(2D, 4D), ReLU, Linear(4D, D) in fp32) on the same
+    bf16 rows and weights. Two requests take caller span lists whose width
+    count differs from their text length, fitted by fit_word_rows as the
+    reference's _fit_length does. The GPU path rounds a, b, the hidden
+    layer and the output to bf16: max-abs error bounded by 2e-2 of the
+    output scale, cosine 0.9999."""
+    from kernels.gliner_pooler import default_spans, fit_word_rows, span_marker_forward
+    g = torch.Generator().manual_seed(77)
+    D, K = 64, 12
+    lens = [9, 14, 6, 11]
+    targets = [9, 10, 6, 13]                 # requests 1 and 3 fitted (cut, padded)
+    we = torch.randn(sum(lens), D, generator=g).bfloat16()
+    cu = [0] + torch.tensor(lens).cumsum(0).tolist()
+    idxs, masks = [], []
+    for r, (L, t) in enumerate(zip(lens, targets)):
+        i, m = default_spans(t, min(L, t), K)
+        if r == 3:
+            m = m * 2                        # mask value 2: indices doubled
+        idxs.append(i)
+        masks.append(m)
+    span_cu = torch.tensor([0] + torch.tensor([x.shape[0] for x in idxs]).cumsum(0).tolist(),
+                           dtype=torch.int32)
+    fitted, row_cu = fit_word_rows(we.cuda(), cu, targets)
+    # start/end projections stand in as two random linear maps of the rows
+    ps = (torch.randn(D, D, generator=g) / D ** 0.5).bfloat16()
+    pe_ = (torch.randn(D, D, generator=g) / D ** 0.5).bfloat16()
+    start = fitted @ ps.cuda()
+    end = fitted @ pe_.cuda()
+    w1 = (torch.randn(4 * D, 2 * D, generator=g) / (2 * D) ** 0.5).bfloat16()
+    b1 = (0.1 * torch.randn(4 * D, generator=g)).bfloat16()
+    w2 = (torch.randn(D, 4 * D, generator=g) / (4 * D) ** 0.5).bfloat16()
+    b2 = (0.1 * torch.randn(D, generator=g)).bfloat16()
+    got = span_marker_forward(start, end, row_cu, torch.cat(idxs).cuda(), torch.cat(masks).cuda(),
+                              span_cu.cuda(), w1.cuda(), b1.cuda(), w2.cuda(), b2.cuda()).float().cpu()
+    sc, ec, rc = start.cpu(), end.cpu(), row_cu.cpu().tolist()
+    want = torch.cat([op.gliner_out_project(op.gliner_span_rows(sc[rc[r]:rc[r + 1]].float(),
+                                                                ec[rc[r]:rc[r + 1]].float(), idxs[r], masks[r]),
+                                            w1, b1, w2, b2) for r in range(len(lens))])
+    assert got.shape == want.shape
+    err = (got - want).abs().max().item()
+    scale = want.abs().max().item()
+    cs = cosine(got, want)
+    print(f"span marker: max-abs {err:.3e} (scale {scale:.3f}) cosine {cs:.6f}", flush=True)
+    assert err <= 2e-2 * scale and cs >= 0.9999, (err, scale, cs)

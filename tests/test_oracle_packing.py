@@ -248,3 +248,46 @@ def test_gliner_span_rows_sources_and_relu():
     assert out[:, 2].tolist() == [102.0, 103.0, 100.0, 103.0]
     neg = op.gliner_span_rows(-start, end, idx[:1], torch.tensor([1]))
     assert neg[0].tolist() == [0.0, 0.0, 102.0, 102.0]
+
+
+def test_gliner_span_rows_multiply_by_mask_value():
+    """The reference multiplies the indices by the mask value (:286): a mask
+    of 2 doubles them before the clamp, 0 sends both to row 0."""
+    L = 4
+    start = (torch.arange(L, dtype=D64) + 1).unsqueeze(1)
+    end = (torch.arange(L, dtype=D64) + 100).unsqueeze(1)
+    idx = torch.tensor([[1, 1], [1, 2], [2, 0]])
+    out = op.gliner_span_rows(start, end, idx, torch.tensor([2, 2, 0]))
+    assert out[:, 0].tolist() == [3.0, 3.0, 1.0]       # rows 2, 2, 0
+    assert out[:, 1].tolist() == [102.0, 103.0, 100.0]  # rows 2, min(4, 3), 0
+
+
+def test_gliner_fit_length_pads_and_cuts():
+    we = torch.arange(6, dtype=D64).view(3, 2) + 1
+    assert torch.equal(op.gliner_fit_length(we, 3), we)
+    assert torch.equal(op.gliner_fit_length(we, 2), we[:2])
+    padded = op.gliner_fit_length(we, 5)
+    assert torch.equal(padded[:3], we) and torch.equal(padded[3:], torch.zeros(2, 2, dtype=D64))
+
+
+def test_gliner_out_project_selection_weights():
+    """With W1 = [I_2D; 0] (b1 = 0) and W2 = [I_D, I_D, 0, 0], out_project of
+    the pair rows is relu(start[i]) + relu(end[j]) in closed form; a bias b1
+    of -inf on the start half leaves only the end rows, and b2 shifts all."""
+    g = torch.Generator().manual_seed(5)
+    D, L = 3, 5
+    start = torch.randn(L, D, generator=g, dtype=D64)
+    end = torch.randn(L, D, generator=g, dtype=D64)
+    idx = torch.tensor([[0, 4], [2, 1], [3, 3]])
+    mask = torch.tensor([1, 1, 1])
+    pair = op.gliner_span_rows(start, end, idx, mask)
+    w1 = torch.cat([torch.eye(2 * D, dtype=D64), torch.zeros(2 * D, 2 * D, dtype=D64)])
+    w2 = torch.cat([torch.eye(D, dtype=D64), torch.eye(D, dtype=D64), torch.zeros(D, 2 * D, dtype=D64)], 1)
+    out = op.gliner_out_project(pair, w1, None, w2, None)
+    want = torch.stack([torch.relu(start[i]) + torch.relu(end[j]) for i, j in idx.tolist()])
+    torch.testing.assert_close(out, want.float(), rtol=1e-6, atol=1e-6)
+    b1 = torch.cat([torch.full((D,), -1e30, dtype=D64), torch.zeros(3 * D, dtype=D64)])
+    b2 = torch.full((D,), 0.5, dtype=D64)
+    out2 = op.gliner_out_project(pair, w1, b1, w2, b2)
+    want2 = torch.stack([torch.relu(end[j]) + 0.5 for _, j in idx.tolist()])
+    torch.testing.assert_close(out2, want2.float(), rtol=1e-6, atol=1e-6)

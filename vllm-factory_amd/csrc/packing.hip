@@ -450,8 +450,8 @@ __device__ inline u32x4_t relu_bits(u32x4_t v) {
 // extract_elements :40-45), for span s of request r (span_cu[r] <= s <
 // span_cu[r + 1]) over r's L = row_cu[r + 1] - row_cu[r] word rows:
 // i = clamp(span_idx[s][0] * m, 0, L - 1), j = clamp(span_idx[s][1] * m, 0,
-// L - 1) with m = (span_mask[s] != 0) (the reference multiplies the indices by
-// the mask), out[s] = relu(cat(start[row_cu[r] + i], end[row_cu[r] + j])).
+// L - 1) with m = span_mask[s] (the reference multiplies the indices by the
+// mask value), out[s] = relu(cat(start[row_cu[r] + i], end[row_cu[r] + j])).
 // L == 0 gives a zero row. Each wave writes kSpansPerWave consecutive spans:
 // lanes 0.. resolve their span's source rows in parallel, then every lane
 // issues all of its 16-byte loads (addresses selected per lane, rows clamped
@@ -485,8 +485,8 @@ __global__ __launch_bounds__(256) void span_rows_kernel(const uint8_t* __restric
     const int r = seq_of(span_cu, n, sp);
     const int64_t base = row_cu[r], L = (int64_t)row_cu[r + 1] - base;
     if (L > 0) {
-      const bool m = mask[sp] != 0;
-      const int64_t i = m ? idx[2 * sp] : 0, j = m ? idx[2 * sp + 1] : 0;
+      const int64_t m = mask[sp];
+      const int64_t i = idx[2 * sp] * m, j = idx[2 * sp + 1] * m;
       ra = base + min(max(i, (int64_t)0), L - 1);
       rb = base + min(max(j, (int64_t)0), L - 1);
     }
@@ -514,6 +514,128 @@ __global__ __launch_bounds__(256) void span_rows_kernel(const uint8_t* __restric
       for (int k = 0; k < kSpanPass; ++k) {
         const int c = c0 + lane + 64 * k;
         if (c < total) dst[c] = v[u][k];
+      }
+    }
+  }
+}
+
+// Source rows of span sp under the pair-row rules above, or -1 for a request
+// without rows.
+__device__ inline void span_rows_of(const int32_t* __restrict__ row_cu, const int64_t* __restrict__ idx,
+                                    const int64_t* __restrict__ mask, const int32_t* __restrict__ span_cu,
+                                    int n, int64_t sp, int64_t& ra, int64_t& rb) {
+  const int r = seq_of(span_cu, n, sp);
+  const int64_t base = row_cu[r], L = (int64_t)row_cu[r + 1] - base;
+  ra = rb = -1;
+  if (L > 0) {
+    const int64_t m = mask[sp];
+    ra = base + min(max(idx[2 * sp] * m, (int64_t)0), L - 1);
+    rb = base + min(max(idx[2 * sp + 1] * m, (int64_t)0), L - 1);
+  }
+}
+
+// 16 bytes of a row as fp32 and back; EB is the type tag of span_rows_kernel
+// (2 bf16, 3 fp16: 8 values; 4 fp32: 4 values).
+template <int EB>
+__device__ inline void ld16(const uint8_t* p, float* f) {
+  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
+  if constexpr (EB == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(v[i]);
+  } else if constexpr (EB == 2) {
+    unpack8<BF16>(v, f);
+  } else {
+    unpack8<F16>(v, f);
+  }
+}
+// The store is non-temporal: output rows stream out without displacing the
+// source rows that neighbouring spans read again from L2.
+template <int EB>
+__device__ inline void st16_nt(uint8_t* p, const float* f) {
+  u32x4_t v;
+  if constexpr (EB == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __float_as_uint(f[i]);
+  } else if constexpr (EB == 2) {
+    v = pack8<BF16>(f);
+  } else {
+    v = pack8<F16>(f);
+  }
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(p));
+}
+
+// SpanMarkerV0's out_project first layer without the pair rows: with
+// a = relu(start) W1[:, :D]^T and b = relu(end) W1[:, D:]^T computed per word
+// row, the layer's output for span s is relu(a[i] + b[j] + b1) (the ReLU of
+// cat(start[i], end[j]) distributes over the halves, and W1 splits with
+// them). out[s] = relu(a[ra] + b[rb] + bias), summed in fp32 in that order and
+// rounded once; ra, rb as for the pair rows (a request without rows adds
+// nothing: relu(bias)). Each wave writes kSpansPerWave consecutive spans;
+// every lane loads the bias chunk once for all of them.
+constexpr int kHidPass = 2;  // 16-byte chunks per lane and span in one pass
+
+template <int EB>
+__global__ __launch_bounds__(256) void span_hidden_kernel(const uint8_t* __restrict__ a,
+                                                          const uint8_t* __restrict__ b,
+                                                          const uint8_t* __restrict__ bias,
+                                                          int64_t row_bytes, int64_t W,
+                                                          const int32_t* __restrict__ row_cu,
+                                                          const int64_t* __restrict__ idx,
+                                                          const int64_t* __restrict__ mask,
+                                                          const int32_t* __restrict__ span_cu, int n,
+                                                          int64_t S, uint8_t* __restrict__ out) {
+  constexpr int V = EB == 4 ? 4 : 8;  // values per 16 bytes (EB: 2 bf16, 3 fp16, 4 fp32)
+  // each XCD takes a contiguous run of spans, so the rows that neighbouring
+  // spans share (a start row for max_width spans, an end row for the spans
+  // of nearby starts) are reused from that XCD's L2
+  const int64_t blk = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t s0 = (blk * 4 + (threadIdx.x >> 6)) * kSpansPerWave;
+  const int lane = threadIdx.x & 63;
+  if (s0 >= S) return;
+  const int chunks = (int)(row_bytes / 16);
+  int64_t ra = -1, rb = -1;  // source rows of span s0 + lane
+  if (lane < kSpansPerWave && s0 + lane < S && W > 0) span_rows_of(row_cu, idx, mask, span_cu, n, s0 + lane, ra, rb);
+  int64_t sa[kSpansPerWave], sb[kSpansPerWave];
+#pragma unroll
+  for (int u = 0; u < kSpansPerWave; ++u) {
+    sa[u] = __shfl(ra, u, 64);
+    sb[u] = __shfl(rb, u, 64);
+  }
+  // every load is unconditional: sources that do not exist (no bias, no
+  // rows at all) are read from a valid row and their values replaced by 0
+  const bool hb = bias != nullptr, hr = W > 0;
+  const uint8_t* src_a = hr ? a : (hb ? bias : out);
+  const uint8_t* src_b = hr ? b : (hb ? bias : out);
+  const uint8_t* src_c = hb ? bias : src_a;
+  const int64_t rs = hr ? row_bytes : 0, wmax = hr ? W - 1 : 0;
+  for (int c0 = 0; c0 < chunks; c0 += 64 * kHidPass) {
+    float bv[kHidPass][V], av[kSpansPerWave][kHidPass][V], cv[kSpansPerWave][kHidPass][V];
+#pragma unroll
+    for (int k = 0; k < kHidPass; ++k) {
+      const int64_t c16 = (int64_t)min(c0 + lane + 64 * k, chunks - 1) * 16;
+      ld16<EB>(src_c + c16, bv[k]);
+#pragma unroll
+      for (int u = 0; u < kSpansPerWave; ++u) {
+        ld16<EB>(src_a + min(max(sa[u], (int64_t)0), wmax) * rs + c16, av[u][k]);
+        ld16<EB>(src_b + min(max(sb[u], (int64_t)0), wmax) * rs + c16, cv[u][k]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSpansPerWave; ++u) {
+      if (s0 + u >= S) break;
+      const bool has = hr && sa[u] >= 0;
+#pragma unroll
+      for (int k = 0; k < kHidPass; ++k) {
+        const int c = c0 + lane + 64 * k;
+        if (c >= chunks) continue;
+        float y[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float bb = hb ? bv[k][e] : 0.f;
+          const float v = has ? (av[u][k][e] + cv[u][k][e]) + bb : bb;
+          y[e] = v < 0.f ? 0.f : v;
+        }
+        st16_nt<EB>(out + (s0 + u) * row_bytes + (int64_t)c * 16, y);
       }
     }
   }
@@ -820,5 +942,35 @@ extern "C" int vfk_gliner_span_rows(const void* start_rep, const void* end_rep, 
                        span_mask, span_cu, (int)num_requests, num_spans, op);
   else
     return set_error(VFK_ERR_INVALID, "%s: dtype must be bf16, fp16 or fp32", name);
+  return launch_status(name);
+}
+
+extern "C" int vfk_gliner_span_hidden(const void* a, const void* b, const void* bias, int64_t row_bytes,
+                                      int64_t num_rows, int32_t dtype, const int32_t* row_cu,
+                                      int32_t num_requests, const int64_t* span_idx,
+                                      const int64_t* span_mask, const int32_t* span_cu,
+                                      int64_t num_spans, void* out, void* stream) {
+  const char* name = "vfk_gliner_span_hidden";
+  if (!a || !b || !row_cu || !span_idx || !span_mask || !span_cu || !out)
+    return set_error(VFK_ERR_INVALID, "%s: NULL pointer", name);
+  if (int rc = check_rows(name, a, out, row_bytes)) return rc;
+  if (int rc = check_rows(name, b, bias ? bias : out, row_bytes)) return rc;
+  if (num_requests <= 0 || num_rows < 0 || num_spans < 0 || num_spans >= (1ll << 31) - 1)
+    return set_error(VFK_ERR_INVALID, "%s: bad sizes", name);
+  if (num_spans == 0) return VFK_OK;
+  const dim3 grid((unsigned)ceil_div(num_spans, 4 * kSpansPerWave));
+  hipStream_t st = (hipStream_t)stream;
+  const uint8_t* ap = static_cast<const uint8_t*>(a);
+  const uint8_t* bp = static_cast<const uint8_t*>(b);
+  const uint8_t* cp = static_cast<const uint8_t*>(bias);
+  uint8_t* op = static_cast<uint8_t*>(out);
+#define VFK_SH(EB)                                                                                  \
+  hipLaunchKernelGGL(span_hidden_kernel<EB>, grid, dim3(256), 0, st, ap, bp, cp, row_bytes, num_rows, \
+                     row_cu, span_idx, span_mask, span_cu, (int)num_requests, num_spans, op)
+  if (dtype == VFK_BF16) VFK_SH(2);
+  else if (dtype == VFK_F16) VFK_SH(3);
+  else if (dtype == VFK_F32) VFK_SH(4);
+  else return set_error(VFK_ERR_INVALID, "%s: dtype must be bf16, fp16 or fp32", name);
+#undef VFK_SH
   return launch_status(name);
 }

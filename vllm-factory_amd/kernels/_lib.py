@@ -65,6 +65,8 @@ _SIGNATURES = {
     "vfk_gliner_word_index": [_vp, _i64, _vp, _i32, _vp, _vp, _vp, _vp],
     "vfk_gliner_word_rows": [_vp, _i64, _i64, _vp, _i64, _vp, _vp],
     "vfk_gliner_span_rows": [_vp, _vp, _i64, _i64, _i32, _vp, _i32, _vp, _vp, _vp, _i64, _vp, _vp],
+    "vfk_gliner_span_hidden": [_vp, _vp, _vp, _i64, _i64, _i32, _vp, _i32, _vp, _vp, _vp, _i64, _vp,
+                               _vp],
     "vfk_rope_fwd": [_P, _P, _P, _P, _vp],
     "vfk_rope_qk_fwd": [_P, _P, _P, _P, _P, _P, _vp],
     "vfk_layernorm_fwd": [_P, _P, _P, _P, _f32, _P, _P, _vp],

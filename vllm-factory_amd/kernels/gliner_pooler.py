@@ -149,6 +149,58 @@ def default_spans(block_len: int, true_len: int, max_width: int):
     return idx, mask
 
 
+def fit_word_rows(we: torch.Tensor, we_cu: Sequence[int], target_rows: Sequence[int]):
+    """The reference's per-request _fit_length (poolers/gliner.py:285-286,
+    :299-311) over packed word rows: request r's rows we[we_cu[r]:we_cu[r+1]]
+    are cut to target_rows[r] or padded with zero rows to it (target_W =
+    span_idx.size(1) // max_width for its span list). Returns (rows
+    [sum(target_rows), H], row_cu int32 [n + 1] on the device), the rows that
+    the span marker's project_start / project_end take."""
+    dev = _lib.require_gpu(we)
+    cu = [int(x) for x in we_cu]
+    tw = [int(x) for x in target_rows]
+    if len(cu) != len(tw) + 1 or any(t < 0 for t in tw):
+        raise ValueError("we_cu needs one entry per request plus one; target_rows >= 0")
+    src = []
+    for r, t in enumerate(tw):
+        n = cu[r + 1] - cu[r]
+        src.append(torch.arange(cu[r], cu[r] + min(n, t)))
+        src.append(torch.full((max(t - n, 0),), we.shape[0], dtype=torch.int64))  # zero row
+    src = torch.cat(src).to(dev) if src else torch.zeros(0, dtype=torch.int64, device=dev)
+    padded = torch.cat([we, we.new_zeros(1, we.shape[1])])
+    row_cu = torch.tensor([0] + list(torch.tensor(tw).cumsum(0).tolist()), dtype=torch.int32, device=dev)
+    return padded.index_select(0, src), row_cu
+
+
+_SPAN_DT = {torch.bfloat16: 1, torch.float16: 2, torch.float32: 0}
+
+
+def _span_args(x: torch.Tensor, y: torch.Tensor, row_cu, span_idx, span_mask, span_cu):
+    """Shared checks of the span ops: x, y [W, N] rows of one dtype, the
+    index lists on x's device. Returns (x, y, idx, mask, row_cu, span_cu)."""
+    dev = _lib.require_gpu(x, y)
+    if x.dim() != 2 or x.shape != y.shape or x.dtype != y.dtype:
+        raise ValueError("the two row sets must be [W, N] of one dtype")
+    if x.dtype not in _SPAN_DT:
+        raise ValueError("rows must be bf16, fp16 or fp32")
+
+    def rows(t):
+        t = t.contiguous()
+        return t if t.data_ptr() % 16 == 0 else t.clone()
+    x, y = rows(x), rows(y)
+    if (x.shape[1] * x.element_size()) % 16:
+        raise ValueError("row size must be a multiple of 16 bytes")
+    idx = torch.as_tensor(span_idx).to(device=dev, dtype=torch.int64).reshape(-1, 2).contiguous()
+    mask = torch.as_tensor(span_mask).to(device=dev, dtype=torch.int64).reshape(-1).contiguous()
+    if mask.numel() != idx.shape[0]:
+        raise ValueError("span_mask must have one entry per span")
+    rcu = torch.as_tensor(row_cu).to(device=dev, dtype=torch.int32).contiguous()
+    scu = torch.as_tensor(span_cu).to(device=dev, dtype=torch.int32).contiguous()
+    if rcu.numel() < 2 or scu.numel() != rcu.numel():
+        raise ValueError("row_cu and span_cu need one entry per request plus one")
+    return x, y, idx, mask, rcu, scu
+
+
 def gliner_span_rows(start_rep: torch.Tensor, end_rep: torch.Tensor, row_cu: torch.Tensor,
                      span_idx: torch.Tensor, span_mask: torch.Tensor,
                      span_cu: torch.Tensor) -> torch.Tensor:
@@ -156,41 +208,73 @@ def gliner_span_rows(start_rep: torch.Tensor, end_rep: torch.Tensor, row_cu: tor
     relu(cat(start_rep[i], end_rep[j])) per span (poolers/gliner.py:131-145,
     extract_elements :40-45, the masked indices of :285).
 
-    start_rep / end_rep [W, D] (bf16, fp16 or fp32; the project_start /
-    project_end outputs over the requests' word rows, request r owning rows
-    row_cu[r] .. row_cu[r + 1] - 1), span_idx [S, 2] request-local word
-    indices and span_mask [S] (any integer or bool dtype), span_cu [n + 1]
-    (request r owns spans span_cu[r] .. span_cu[r + 1] - 1). Returns
-    [S, 2 * D]; for request r it equals the reference's cat(...).relu()
-    rows before out_project."""
-    dev = _lib.require_gpu(start_rep, end_rep)
-    if start_rep.dim() != 2 or start_rep.shape != end_rep.shape or start_rep.dtype != end_rep.dtype:
-        raise ValueError("start_rep and end_rep must be [W, D] of one dtype")
-    codes = {torch.bfloat16: 1, torch.float16: 2, torch.float32: 0}
-    if start_rep.dtype not in codes:
-        raise ValueError("start_rep must be bf16, fp16 or fp32")
-
-    def rows(t):
-        t = t.contiguous()
-        return t if t.data_ptr() % 16 == 0 else t.clone()
-    sr, er = rows(start_rep), rows(end_rep)
+    start_rep / end_rep [W, D] (bf16, fp16 or fp32): project_start /
+    project_end over each request's fitted word rows (fit_word_rows), request
+    r owning rows row_cu[r] .. row_cu[r + 1] - 1; span_idx [S, 2]
+    request-local word indices, span_mask [S] (any integer or bool dtype;
+    the indices are multiplied by its value, as the reference does), span_cu
+    [n + 1] (request r owns spans span_cu[r] .. span_cu[r + 1] - 1). Returns
+    [S, 2 * D]; for request r it equals the reference's cat(...).relu() rows
+    before out_project."""
+    sr, er, idx, mask, rcu, scu = _span_args(start_rep, end_rep, row_cu, span_idx, span_mask, span_cu)
     W, D = sr.shape
-    row_bytes = D * sr.element_size()
-    if row_bytes % 16:
-        raise ValueError("row size must be a multiple of 16 bytes")
-    idx = torch.as_tensor(span_idx).to(device=dev, dtype=torch.int64).reshape(-1, 2).contiguous()
     S = idx.shape[0]
-    mask = torch.as_tensor(span_mask).to(device=dev, dtype=torch.int64).reshape(-1).contiguous()
-    if mask.numel() != S:
-        raise ValueError("span_mask must have one entry per span")
-    rcu = torch.as_tensor(row_cu).to(device=dev, dtype=torch.int32).contiguous()
-    scu = torch.as_tensor(span_cu).to(device=dev, dtype=torch.int32).contiguous()
-    n = rcu.numel() - 1
-    if n < 1 or scu.numel() != n + 1:
-        raise ValueError("row_cu and span_cu need one entry per request plus one")
-    out = torch.empty(S, 2 * D, dtype=sr.dtype, device=dev)
+    out = torch.empty(S, 2 * D, dtype=sr.dtype, device=sr.device)
     if S:
-        _lib.on_device("vfk_gliner_span_rows", dev, sr.data_ptr(), er.data_ptr(), row_bytes, W,
-                       codes[sr.dtype], rcu.data_ptr(), n, idx.data_ptr(), mask.data_ptr(),
-                       scu.data_ptr(), S, out.data_ptr())
+        _lib.on_device("vfk_gliner_span_rows", sr.device, sr.data_ptr(), er.data_ptr(),
+                       D * sr.element_size(), W, _SPAN_DT[sr.dtype], rcu.data_ptr(), rcu.numel() - 1,
+                       idx.data_ptr(), mask.data_ptr(), scu.data_ptr(), S, out.data_ptr())
     return out
+
+
+def gliner_span_hidden(a: torch.Tensor, b: torch.Tensor, bias, row_cu: torch.Tensor,
+                       span_idx: torch.Tensor, span_mask: torch.Tensor,
+                       span_cu: torch.Tensor) -> torch.Tensor:
+    """relu(a[i] + b[j] + bias) per span: the first layer (Linear + ReLU) of
+    SpanMarkerV0's out_project without the pair rows, for a = relu(start_rep)
+    W1[:, :D]^T and b = relu(end_rep) W1[:, D:]^T (per word row) and bias =
+    b1 (or None). Rows, spans and masks as in gliner_span_rows. Returns
+    [S, N] of a's dtype, summed in fp32 and rounded once."""
+    a, b, idx, mask, rcu, scu = _span_args(a, b, row_cu, span_idx, span_mask, span_cu)
+    W, N = a.shape
+    S = idx.shape[0]
+    bp = None
+    if bias is not None:
+        bias = bias.to(device=a.device, dtype=a.dtype).reshape(-1).contiguous()
+        if bias.numel() != N:
+            raise ValueError("bias must have one entry per column")
+        if bias.data_ptr() % 16:
+            bias = bias.clone()
+        bp = bias.data_ptr()
+    out = torch.empty(S, N, dtype=a.dtype, device=a.device)
+    if S:
+        _lib.on_device("vfk_gliner_span_hidden", a.device, a.data_ptr(), b.data_ptr(), bp,
+                       N * a.element_size(), W, _SPAN_DT[a.dtype], rcu.data_ptr(), rcu.numel() - 1,
+                       idx.data_ptr(), mask.data_ptr(), scu.data_ptr(), S, out.data_ptr())
+    return out
+
+
+def span_marker_forward(start_rep: torch.Tensor, end_rep: torch.Tensor, row_cu: torch.Tensor,
+                        span_idx: torch.Tensor, span_mask: torch.Tensor, span_cu: torch.Tensor,
+                        w1: torch.Tensor, b1, w2: torch.Tensor, b2) -> torch.Tensor:
+    """SpanMarkerV0's out_project over every span of a packed batch
+    (poolers/gliner.py:141-144, create_projection_layer :26-37 in eval mode:
+    Linear(2D, 4D), ReLU, Linear(4D, D)) without the [S, 2D] pair rows. The
+    ReLU of cat(start[i], end[j]) acts on each half, so the first Linear
+    splits: relu(start) W1[:, :D]^T and relu(end) W1[:, D:]^T are formed once
+    per word row (W rows instead of S spans), gliner_span_hidden adds them per
+    span with b1 and applies the ReLU, and the second Linear follows. w1
+    [4D, 2D], w2 [D, 4D] (nn.Linear weights). Returns [S, D], the rows that
+    the reference views as [B, L, max_width, D]."""
+    D = start_rep.shape[1]
+    if w1.shape[1] != 2 * D:
+        raise ValueError("w1 must be [4D, 2D] for start/end rows of width D")
+    from .activation import activation
+    w1a = w1[:, :D].contiguous()
+    w1b = w1[:, D:].contiguous()
+    a = torch.matmul(activation(start_rep, "relu"), w1a.t())
+    b = torch.matmul(activation(end_rep, "relu"), w1b.t())
+    h = gliner_span_hidden(a, b, b1, row_cu, span_idx, span_mask, span_cu)
+    if b2 is None:
+        return torch.matmul(h, w2.t())
+    return torch.addmm(b2.to(h.dtype), h, w2.t())
