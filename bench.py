@@ -447,13 +447,26 @@ def mt5_layer_config4(torch, args):
     dev = torch.device("cuda:0")
     c = workloads.config4(device=dev)
     ws = (c.wq, c.wk, c.wv, c.wo, c.wi0, c.wi1, c.wff_o, c.ln1, c.ln2, c.table)
+    from encoders.mt5 import mt5_layer_packed
+    from kernels.packing import unpad_packed
     fn = lambda: mt5_layer_forward(c.hidden, *ws, c.mask)
-    for _ in range(args.warmup):
-        fn()
-    ms = device_ms(torch, fn, args.steps)
     tv = int(c.lengths.sum())
+    cu = torch.cat([c.lengths.new_zeros(1), c.lengths.cumsum(0)]).to(device=dev, dtype=torch.int32)
+    xf = unpad_packed(c.hidden, cu, tv)
+    wqkv = torch.cat((c.wq, c.wk, c.wv), 1)
+    L = c.hidden.shape[1]
+    fp = lambda: mt5_layer_packed(xf, cu, L, *ws, c.mask, wqkv=wqkv)
+    res = {}
+    for name, f in (("padded", fn), ("packed", fp)):
+        for _ in range(args.warmup):
+            f()
+        res[name] = device_ms(torch, f, args.steps)
+    ms = res["packed"]
     return dict(ms_per_layer=ms, valid_tokens_per_s=tv / (ms * 1e-3), valid_tokens=tv,
-                padded_tokens=int(c.hidden.shape[0] * c.hidden.shape[1]))
+                padded_tokens=int(c.hidden.shape[0] * c.hidden.shape[1]),
+                padded_layer_ms=res["padded"],
+                note="ms_per_layer: the layer on the packed valid rows (mt5_layer_packed); "
+                     "padded_layer_ms: the same layer over the padded batch")
 
 
 def deberta_layer_config3(torch, args):

@@ -84,3 +84,35 @@ def test_mt5_flat_stream_routed_per_sequence():
     want_b = mt5_layer_forward(mt5_layer_forward(xb, *lw, table, mask), *lw, table, mask)
     want = torch.cat([want_b[b, :n] for b, n in enumerate(lens)])
     assert torch.equal(got, want)
+
+
+def test_mt5_layer_packed_matches_oracle_and_padded_layer():
+    """mt5_layer_packed on the packed valid rows of three config-4 batch rows
+    against the fp32 oracle layer (bound as for the padded layer: max-abs
+    6e-2, cosine 0.9999) and against the padded layer's valid rows (same
+    kernels on fewer rows: the GEMMs may pick other tilings for the smaller
+    row count, so within 2 bf16 steps of the output scale)."""
+    from encoders.mt5 import mt5_layer_forward, mt5_layer_packed
+    from kernels.packing import unpad_packed
+    from oracle import encoders as oe
+    c = workloads.config4(batch=3)
+    dev = torch.device("cuda:0")
+    ws = (c.wq, c.wk, c.wv, c.wo, c.wi0, c.wi1, c.wff_o, c.ln1, c.ln2, c.table)
+    wd = tuple(w.to(dev) for w in ws)
+    lens = c.lengths.tolist()
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    L = c.hidden.shape[1]
+    x = c.hidden.to(dev)
+    mask = c.mask.to(dev)
+    xf = unpad_packed(x, cu, int(cu[-1]))
+    got = mt5_layer_packed(xf, cu, L, *wd, mask).float().cpu()
+    pad = unpad_packed(mt5_layer_forward(x, *wd, mask), cu, int(cu[-1])).float().cpu()
+    want = oe.mt5_layer(c.hidden, *ws, c.mask)
+    for b, n in enumerate(lens):
+        a, e = int(cu[b]), int(cu[b + 1])
+        err = (got[a:e] - want[b, :n]).abs().max().item()
+        cs = cosine(got[a:e], want[b, :n])
+        dp = (got[a:e] - pad[a:e]).abs().max().item()
+        print(f"packed row {b} (len {n}): max-abs {err:.3e} cosine {cs:.6f}; vs padded {dp:.3e}")
+        assert err <= 6e-2 and cs >= 0.9999, (b, err, cs)
+        assert dp <= 2 * 2.0 ** -7 * pad[a:e].abs().max().item(), (b, dp)

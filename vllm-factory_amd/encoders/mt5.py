@@ -43,15 +43,53 @@ def mt5_layer_forward(x: torch.Tensor, wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2
     return torch.addmm(x1.reshape(-1, D), g.reshape(-1, g.shape[-1]), wff_o).view(B, L, D)
 
 
+def mt5_layer_packed(x: torch.Tensor, cu_seqlens: torch.Tensor, max_len: int, wq, wk, wv, wo,
+                     wi0, wi1, wff_o, ln1, ln2, table, mask, num_buckets: int = 32,
+                     max_distance: int = 128, eps: float = 1e-6, wqkv=None) -> torch.Tensor:
+    """The layer of mt5_layer_forward on the packed valid rows of a padded batch.
+
+    x [T, d_model]: the valid rows of the batch in order (sequence b owns
+    rows cu_seqlens[b] .. cu_seqlens[b + 1] - 1, int32 on the device);
+    mask: the [B, 1, 1, max_len] additive key mask of the padded batch. The
+    RMSNorms, projections, FFN and residual adds run on the T valid rows
+    only; the fused q|k|v projection is padded once into [B, max_len, 3D] for
+    the RPB attention, which writes its output as [B, max_len, H, d] rows that
+    one unpad returns to [T, D] for the output projection. Row for row the
+    same arithmetic as the padded layer. wqkv: the [D, 3D] concatenation of
+    wq, wk, wv when the caller keeps one (built here otherwise)."""
+    from kernels.packing import pad_packed, unpad_packed
+    T, D = x.shape
+    B = cu_seqlens.numel() - 1
+    H = table.shape[1]
+    d = D // H
+    if wqkv is None:
+        wqkv = torch.cat((wq, wk, wv), 1)
+    h = rms_norm(x, ln1, eps)
+    qkv, _ = pad_packed(h @ wqkv, cu_seqlens, B, max_len)
+    q, k, v = (t.transpose(1, 2) for t in qkv.view(B, max_len, 3, H, d).unbind(2))
+    att = torch.empty(B, max_len, H, d, dtype=x.dtype, device=x.device)
+    flash_attention_rpb_final(q, k, v, table, num_buckets, max_distance, False, padding_mask=mask,
+                              softmax_scale=1.0, out=att.transpose(1, 2))
+    o = unpad_packed(att.view(B, max_len, D), cu_seqlens, T) @ wo
+    h2, x1 = fused_add_rms_norm(o, x, ln2, eps)
+    g = fused_gelu_mul_dropout(h2 @ wi0, h2 @ wi1, "gelu_new")
+    return torch.addmm(x1, g, wff_o)
+
+
 def mt5_encoder_forward(input_ids: Optional[torch.Tensor], attention_mask: Optional[torch.Tensor],
                         layers, table: torch.Tensor, final_ln: torch.Tensor,
                         embed: Optional[torch.Tensor] = None,
                         inputs_embeds: Optional[torch.Tensor] = None, num_buckets: int = 32,
-                        max_distance: int = 128, eps: float = 1e-6) -> torch.Tensor:
+                        max_distance: int = 128, eps: float = 1e-6,
+                        packed: bool = True) -> torch.Tensor:
     """Padded-batch encoder: input_ids [B, L] (or [L]) with embed [vocab, d_model],
     or inputs_embeds [B, L, d_model]; attention_mask [B, L] of 1 (keep) / 0
     (pad) or None; layers: (wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2) per
-    layer as for mt5_layer_forward; table: layer 0's [buckets, heads]."""
+    layer as for mt5_layer_forward; table: layer 0's [buckets, heads].
+    packed: when the mask is right padding, run the layers on the valid rows
+    only (mt5_layer_packed); rows past each length are then returned as
+    zeros (the reference's outputs there are never consumed: its callers
+    read the valid rows). Any other mask runs the padded layers."""
     x = embed[input_ids] if inputs_embeds is None else inputs_embeds
     squeeze = x.dim() == 2
     if squeeze:
@@ -60,10 +98,37 @@ def mt5_encoder_forward(input_ids: Optional[torch.Tensor], attention_mask: Optio
     if attention_mask is not None:
         m = attention_mask.reshape(x.shape[0], -1)[:, None, None, :].to(x.dtype)
         mask = (1.0 - m) * torch.finfo(x.dtype).min
+    cu = _right_padded_cu(attention_mask, x.shape[0], x.shape[1]) if packed else None
+    if cu is not None:
+        # right-padded batch: every layer on the valid rows only; rows past
+        # each length come back as zeros
+        from kernels.packing import pad_packed, unpad_packed
+        B, L, D = x.shape
+        T = int(cu[-1])
+        xf = unpad_packed(x, cu, T)
+        for lw in layers:
+            xf = mt5_layer_packed(xf, cu, L, *lw, table, mask, num_buckets, max_distance, eps,
+                                  wqkv=torch.cat(lw[:3], 1))
+        x, _ = pad_packed(rms_norm(xf, final_ln, eps), cu, B, L)
+        return x.squeeze(0) if squeeze else x
     for lw in layers:
         x = mt5_layer_forward(x, *lw, table, mask, num_buckets, max_distance, eps)
     x = rms_norm(x, final_ln, eps)
     return x.squeeze(0) if squeeze else x
+
+
+def _right_padded_cu(attention_mask: Optional[torch.Tensor], B: int, L: int):
+    """int32 cu_seqlens [B + 1] on the device when attention_mask [B, L] is 1
+    on a prefix of each row and 0 after it (right padding), else None (one
+    read-back of the check)."""
+    if attention_mask is None:
+        return None
+    m = attention_mask.reshape(B, L) != 0
+    lens = m.sum(1)
+    prefix = torch.arange(L, device=m.device)[None, :] < lens[:, None]
+    if not bool(torch.equal(m, prefix)):
+        return None
+    return torch.cat([lens.new_zeros(1), lens.cumsum(0)]).to(torch.int32)
 
 
 def mt5_encoder_flat(x: torch.Tensor, positions: torch.Tensor, layers, table: torch.Tensor,

@@ -27,12 +27,16 @@ def flash_attention_rpb_final(
     dropout_p: float = 0.0,
     softmax_scale: float = 1.0,
     use_autotune: bool = True,
+    out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """out = softmax(q k^T * softmax_scale + rpb[bucket(k - q)] + padding_mask) v.
 
     q [B,H,Lq,D], k/v [B,H,Lk,D] (D = 64, any strides); padding_mask is an
     additive mask broadcastable to [B,H,Lq,Lk] (typically [B,1,1,Lk]).
     `use_autotune` is accepted for signature compatibility; tiles are fixed.
+    `out` (an addition to the reference's signature): a [B,H,Lq,D] tensor of
+    q's dtype with a contiguous last dim and 16-byte aligned rows, written in
+    place (e.g. a [B,Lq,H,D] buffer viewed through transpose(1, 2)).
     """
     if dropout_p != 0.0:
         raise NotImplementedError("flash_attention_rpb_final: dropout is not supported (inference only)")
@@ -42,7 +46,10 @@ def flash_attention_rpb_final(
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("q, k, v must share a dtype")
     qq, kk, vv = (_lib.rows_aligned(t) for t in (q, k, v))
-    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
+        raise ValueError("out must match q's shape, dtype and device")
     mask = padding_mask
     if mask is not None:
         while mask.dim() < 4:
