@@ -369,12 +369,13 @@ __global__ __launch_bounds__(64) void deberta_gather_f32_kernel(DebArgs a) {
 // precision of the reference's pos_key / pos_query tensors) and written to
 // LDS as 8-byte runs; every score then adds C[row][c - cwl] and
 // P^T[key][c - wlo], with c read from a table of 2 c(d) over the
-// workgroup's relative positions. The Qr operands of tile i + 1 are fetched
-// into registers during tile i; the Kr operands at the start of the tile.
+// workgroup's relative positions. The Qr and Kr operands of tile i + 1 are
+// fetched into registers during tile i.
 //
-// Step for key tile i (K(i) resident since the previous step):
-//   direct load V(i); Kr loads; P^T and C blocks; S = K(i) Q^T; barrier;
-//   direct load K(i+1), Qr loads of tile i + 1; bias gathers; online
+// Step for key tile i (K(i), and the Qr and Kr operands, resident since the
+// previous step):
+//   direct load V(i); P^T and C blocks; S = K(i) Q^T; barrier;
+//   direct load K(i+1), Qr and Kr loads of tile i + 1; bias gathers; online
 //   softmax; O += V(i)^T P; barrier (K(i+1) landed, V / P^T / C free again)
 // ---------------------------------------------------------------------------
 constexpr int kPTs = 204;               // P^T row stride (u16): 8-byte rows, odd dword pairs
@@ -521,6 +522,15 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
     }
   };
   if (P2C) pt_loads(0);
+  // C operands (Kr rows of the wave's window), also loaded one tile ahead:
+  // always 3 blocks (rows past the table read as zeros), of which the tile
+  // multiplies the nbc that hold a used c
+  u32x4_t ca[3][4];
+  auto c_prefetch = [&](int i) {
+    const int cwl = __builtin_amdgcn_readfirstlane(lut[qw0 - i * kBN - 63 - dmin]) >> 1;
+    c_loads<3>(kr_r, kr_lane, cwl, kr_rs2, ca);
+  };
+  if (C2P && wave_on) c_prefetch(0);
 
   auto step = [&](int i, const uint16_t* __restrict__ Kc, uint16_t* __restrict__ Kn) {
     const int key0 = i * kBN;
@@ -530,12 +540,6 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
     // C blocks of the wave's window that hold a used c (1 to 3)
     const int cwh = __builtin_amdgcn_readfirstlane(lut[qw0 + 31 - key0 - dmin]) >> 1;
     const int nbc = (cwh - cwl) / 32 + 1;
-    u32x4_t ca[3][4];
-    if (C2P && wave_on) {
-      if (nbc >= 3) c_loads<3>(kr_r, kr_lane, cwl, kr_rs2, ca);
-      else if (nbc == 2) c_loads<2>(kr_r, kr_lane, cwl, kr_rs2, ca);
-      else c_loads<1>(kr_r, kr_lane, cwl, kr_rs2, ca);
-    }
     const int nbp = P2C ? pt_blocks(i) : 0;
     const bool two_i = two && w + 4 < nbp;
     if (P2C && w < nbp) {
@@ -566,6 +570,7 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
     if (i + 1 < kt_end) {
       tile_load_buf(ksrc, key0 + kBN, Kn);
       if (P2C) pt_loads(i + 1);
+      if (C2P && wave_on) c_prefetch(i + 1);
     }
     if (wave_on) {
       const int lb = lut_lane - key0;
