@@ -412,14 +412,6 @@ __device__ inline void tile_barrier() {
   __syncthreads();
 }
 
-// Workgroup barrier over LDS only: earlier LDS accesses complete and become
-// visible, while global loads and direct-to-LDS DMA stay in flight.
-__device__ inline void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Lane offsets are kept in bytes and passed through an empty asm at each use
 // so that the compiler adds the (constant) LDS buffer address in the
 // instruction's offset field instead of keeping one address register per
@@ -537,12 +529,6 @@ __device__ inline void pv_tile_sw(const uint16_t* __restrict__ Vt, const VOff& v
 //   bool active(int i)                  the wave computes tile i
 //   bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot)   bias / masks;
 //                                       returns "exact" for softmax_exp
-//   static constexpr bool kPrepK        tile i's K is transformed in LDS by
-//                                       the whole workgroup before use:
-//   R    prep_ld(int i)                 its global operands, loaded before
-//                                       the next tile's DMA is issued, and
-//   void prep_st(R r, uint16_t* Kt, int i)   the in-place transform, followed
-//                                       by an LDS-only barrier
 // ---------------------------------------------------------------------------
 
 // Issues the loads and metadata of tiles 0 and 1; call before the Q set-up so
@@ -582,22 +568,9 @@ __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t*
     // loaded before its DMA and written to LDS after this tile's compute
     const bool meta_next = i + 1 < n && i > 0;
     const auto mn = pol.meta_ld(meta_next ? i + 1 : i);
-    if constexpr (P::kPrepK) {
-      // the prep loads go out before the DMA, so waiting for them leaves the
-      // DMA in flight (loading them a tile ahead instead costs registers the
-      // loop does not have: it spills)
-      const auto pk = pol.prep_ld(i);
-      if (i + 1 < n) {
-        if (i > 0) pol.loadK(i + 1, Kn);
-        pol.loadV(i + 1, Vn);
-      }
-      pol.prep_st(pk, Kc, i);
-      lds_barrier();
-    } else {
-      if (i + 1 < n) {
-        if (i > 0) pol.loadK(i + 1, Kn);
-        pol.loadV(i + 1, Vn);
-      }
+    if (i + 1 < n) {
+      if (i > 0) pol.loadK(i + 1, Kn);
+      pol.loadV(i + 1, Vn);
     }
     if (wave_on && (P::kAllActive || __builtin_amdgcn_readfirstlane((int)pol.active(i)) != 0)) {
       f32x16_t s0, s1;

@@ -76,8 +76,6 @@ struct RpbPolicy {
   bool nolive;           // MASK_KEY: every key of the row range masked away
 
   static constexpr bool kAllActive = !CAUSAL;
-  static constexpr bool kPrepK = false;
-  __device__ int prep_ld(int) const { return 0; }
   __device__ int tile(int i) const { return tiles ? tiles[i] : i; }
   __device__ int key0(int i) const { return tile(i) * kBN; }
   __device__ void loadK(int i, uint16_t* Kt) { tile_load_buf(ksrc, key0(i), Kt); }

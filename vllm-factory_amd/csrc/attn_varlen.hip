@@ -146,11 +146,7 @@ __global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int nkt)
   }
 }
 
-// ROPE: 0 no rotation; 1 K rotated (and scaled by c2) by the pre-pass into
-// the workspace; 2 K rotated in LDS by the workgroup as each tile lands
-// (sliding-window layers, whose few key tiles per workgroup do not pay for
-// the pre-pass's round trip through HBM).
-template <typename E, int ROPE, bool LOCAL, bool KVALID>
+template <typename E, bool ROPE, bool LOCAL, bool KVALID>
 struct VarlenPolicy {
   const VarlenArgs* a;
   TileSrc ksrc, vsrc;
@@ -176,28 +172,6 @@ struct VarlenPolicy {
     if (t == 0) kflag[slot] = dead != 0ull;
   }
   static constexpr bool kAllActive = !LOCAL;
-  static constexpr bool kPrepK = ROPE == 2;
-  // ROPE 2: thread t rotates key row t >> 2 of the tile, d chunks (t & 3) and
-  // (t & 3) + 4 (the rotate-half partners), with the table row of the key's
-  // position (rows past n, zeros in the tile, use row n - 1)
-  __device__ auto prep_ld(int i) const {
-    if constexpr (ROPE == 2) {
-      RopeK r;
-      rope_k_fetch(r, a->rope, min(key0(i) + (t >> 2), n - 1), true);
-      return r;
-    } else {
-      return 0;
-    }
-  }
-  __device__ void prep_st(const RopeK& r, uint16_t* Kt, int i) const {
-    const int row = t >> 2, cp = t & 3, f = swz(row);
-    u32x4_t* p0 = reinterpret_cast<u32x4_t*>(Kt + row * 64 + 8 * (cp ^ f));
-    u32x4_t* p1 = reinterpret_cast<u32x4_t*>(Kt + row * 64 + 8 * ((cp + 4) ^ f));
-    u32x4_t k0 = *p0, k1 = *p1;
-    rope_k_apply<E>(k0, k1, r);
-    *p0 = k0;
-    *p1 = k1;
-  }
   __device__ bool wave_active() const { return wq_lo < n; }
   __device__ bool active(int i) const {
     if (wq_lo >= n) return false;
@@ -221,7 +195,7 @@ struct VarlenPolicy {
   }
 };
 
-template <typename E, int ROPE, bool LOCAL, bool KVALID>
+template <typename E, bool ROPE, bool LOCAL, bool KVALID>
 __global__ __launch_bounds__(256, 4) void varlen_fwd_kernel(VarlenArgs a) {
   __shared__ __align__(16) uint16_t K0[kTileElems];
   __shared__ __align__(16) uint16_t K1[kTileElems];
@@ -265,7 +239,7 @@ __global__ __launch_bounds__(256, 4) void varlen_fwd_kernel(VarlenArgs a) {
 
   VarlenPolicy<E, ROPE, LOCAL, KVALID> pol;
   pol.a = &a;
-  if (ROPE == 1)
+  if (ROPE)
     tile_src_init(pol.ksrc, reinterpret_cast<const uint16_t*>(a.kr) + ((int64_t)h * a.T + tok0) * 64,
                   64, n);
   else
@@ -287,7 +261,7 @@ __global__ __launch_bounds__(256, 4) void varlen_fwd_kernel(VarlenArgs a) {
   float m = -INFINITY, l = 0.f;
   f32x16_t o0 = {}, o1 = {};
   const int ntiles = kt_end - kt_begin;
-  if (ROPE == 1) {
+  if (ROPE) {
     // |score| <= |q| max|k| over the workgroup's key tiles (scores are in
     // log2 units: K carries c2); the margin covers the fp32 norms and the
     // MFMA's fp32 accumulation
@@ -487,10 +461,6 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
   if (span * std::max<int64_t>(a.ks[0], 64) >= (1ll << 31) || span * a.vs[0] >= (1ll << 31))
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: max_seqlen x row stride too large");
   const bool rope = a.rope != nullptr;
-  if (a.window >= 0 && a.window >= max_seqlen) a.window = -1;  // window covers every pair
-  if (a.window > kPenOff - kBM)
-    return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: window %d > %d", a.window, kPenOff - kBM);
-  const bool local = a.window >= 0, kv = key_valid != nullptr;
   if (rope) {
     const int64_t need = vfk_varlen_attn_workspace_bytes(dt, T, (int32_t)H, 1, num_seqs, max_seqlen);
     if (!workspace || workspace_bytes < need)
@@ -505,28 +475,29 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
     const int64_t pblocks = (int64_t)num_seqs * nkt;
     if (pblocks >= (1ll << 31))
       return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: grid too large");
-    // sliding-window layers rotate K in the attention kernel instead
-    if (!local) {
-      const dim3 pgrid((unsigned)pblocks, (unsigned)ceil_div(H, kPackHeads));
-      if (dt == VFK_BF16)
-        hipLaunchKernelGGL(rope_k_pack_kernel<BF16>, pgrid, dim3(256), 0, st, a, nkt);
-      else
-        hipLaunchKernelGGL(rope_k_pack_kernel<F16>, pgrid, dim3(256), 0, st, a, nkt);
-    }
+    const dim3 pgrid((unsigned)pblocks, (unsigned)ceil_div(H, kPackHeads));
+    if (dt == VFK_BF16)
+      hipLaunchKernelGGL(rope_k_pack_kernel<BF16>, pgrid, dim3(256), 0, st, a, nkt);
+    else
+      hipLaunchKernelGGL(rope_k_pack_kernel<F16>, pgrid, dim3(256), 0, st, a, nkt);
   }
+  if (a.window >= 0 && a.window >= max_seqlen) a.window = -1;  // window covers every pair
+  if (a.window > kPenOff - kBM)
+    return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: window %d > %d", a.window, kPenOff - kBM);
   a.nqt = ceil_div(max_seqlen, kBM);
   const int64_t blocks = (int64_t)a.nqt * H * num_seqs;
   if (blocks >= (1ll << 31))
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: grid too large");
+  const bool local = a.window >= 0, kv = key_valid != nullptr;
 #define VFK_VL(E, R, L, K) \
   hipLaunchKernelGGL((varlen_fwd_kernel<E, R, L, K>), dim3((unsigned)blocks), dim3(256), 0, st, a)
 #define VFK_VL_E(E)                                                   \
   if (rope) {                                                         \
-    if (local) { if (kv) VFK_VL(E, 2, true, true); else VFK_VL(E, 2, true, false); } \
-    else { if (kv) VFK_VL(E, 1, false, true); else VFK_VL(E, 1, false, false); }    \
+    if (local) { if (kv) VFK_VL(E, true, true, true); else VFK_VL(E, true, true, false); } \
+    else { if (kv) VFK_VL(E, true, false, true); else VFK_VL(E, true, false, false); }    \
   } else {                                                            \
-    if (local) { if (kv) VFK_VL(E, 0, true, true); else VFK_VL(E, 0, true, false); } \
-    else { if (kv) VFK_VL(E, 0, false, true); else VFK_VL(E, 0, false, false); }    \
+    if (local) { if (kv) VFK_VL(E, false, true, true); else VFK_VL(E, false, true, false); } \
+    else { if (kv) VFK_VL(E, false, false, true); else VFK_VL(E, false, false, false); }    \
   }
   if (dt == VFK_BF16) {
     VFK_VL_E(BF16)
