@@ -208,8 +208,20 @@ def rpb_config4(torch, args):
         fn()
     ms = device_ms(torch, fn, args.steps)
     tf = flops / (ms * 1e-3) / 1e12
+    # the same sequences packed (no padding): [T, 3, H, 64] rows of a fused
+    # projection, the varlen RPB kernel
+    from kernels.flash_attention_rpb import flash_attention_rpb_varlen
+    cu = torch.tensor([0] + c.lengths.cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    qkv = torch.stack([torch.cat([t[b, :, :n].transpose(0, 1) for b, n in enumerate(lens)])
+                       for t in (q, k, v)], 1).contiguous()
+    fv = lambda: flash_attention_rpb_varlen(qkv[:, 0], qkv[:, 1], qkv[:, 2], cu, L, c.table, 32, 128)
+    for _ in range(args.warmup):
+        fv()
+    vms = device_ms(torch, fv, args.steps)
     return dict(ms=ms, tflops=tf, gflop=flops / 1e9, frac=tf / PEAK_BF16_TFLOPS,
-                note="queries and keys of padded rows excluded from the FLOP count")
+                note="queries and keys of padded rows excluded from the FLOP count",
+                varlen_ms=vms, varlen_tflops=flops / (vms * 1e-3) / 1e12,
+                varlen_note="the same sequences packed as [T, 3, 16, 64] rows, no mask")
 
 
 def deberta_config3(torch, args):

@@ -103,6 +103,22 @@ int vfk_flash_rpb_fwd(const vfk_tensor* q, const vfk_tensor* k,
                       int32_t is_decoder, const vfk_tensor* mask,
                       float softmax_scale, vfk_tensor* out, void* stream);
 
+/* vfk_flash_rpb_fwd over packed sequences (no padding, no mask): sequence s
+ * is tokens cu_seqlens[s] .. cu_seqlens[s + 1] - 1 of q, k, v, out [T, H, 64]
+ * (16-byte aligned rows, any token / head strides; bf16 or fp16) and attends
+ * to its own tokens only, with relative positions inside the sequence. This
+ * is the reference's padded call (kernels/flash_attention_rpb.py:296-412 with
+ * the [B, 1, 1, L] key mask of models/mt5/mt5_encoder.py:571-576) on the
+ * valid rows: the flat mT5 callers (plugins/mt5_gliner/model.py:169-201) run
+ * on it without re-padding. cu_seqlens: device int32 [num_seqs + 1];
+ * max_seqlen >= every sequence length (rows past it are not computed). */
+int vfk_flash_rpb_varlen_fwd(const vfk_tensor* q, const vfk_tensor* k,
+                             const vfk_tensor* v, const int32_t* cu_seqlens,
+                             int32_t num_seqs, int32_t max_seqlen,
+                             const vfk_tensor* rpb_table, int32_t num_buckets,
+                             int32_t max_distance, int32_t is_decoder,
+                             float softmax_scale, vfk_tensor* out, void* stream);
+
 /* DeBERTa-v2/v3 disentangled flash attention, forward, gathering the bias
  * from precomputed position projections (the reference's interface).
  * Replaces kernels/flash_deberta_attention.py:455-499 (flash_deberta_attention)

@@ -62,10 +62,13 @@ def test_mt5_encoder_stack_matches_oracle():
 
 def test_mt5_flat_stream_routed_per_sequence():
     """The GLiNER flat call (plugins/mt5_gliner/model.py:169-201) routed per
-    sequence: two layers on the packed valid rows of three config-4 rows equal
-    the padded-batch forward with the reference's key mask, row for row
-    (same kernels on the same padded batch)."""
+    sequence: two layers on the packed rows of three config-4 rows (varlen RPB
+    attention, no padding) against the padded-batch forward with the
+    reference's key mask, on the valid rows. The GEMMs run on a different row
+    count, so the bound is 2 bf16 steps of the output scale; and against the
+    fp32 oracle at the layer tolerance (6e-2, cosine 0.9999)."""
     from encoders.mt5 import mt5_encoder_flat, mt5_layer_forward
+    from oracle import encoders as oe
     c = workloads.config4(batch=3)
     dev = torch.device("cuda:0")
     lens = [int(n) for n in c.lengths]
@@ -73,17 +76,28 @@ def test_mt5_flat_stream_routed_per_sequence():
     xb = c.hidden[:, :L].clone()
     for b, n in enumerate(lens):
         xb[b, n:] = 0
-    xb = xb.to(dev)
-    lw = tuple(w.to(dev) for w in (c.wq, c.wk, c.wv, c.wo, c.wi0, c.wi1, c.wff_o, c.ln1, c.ln2))
+    xbd = xb.to(dev)
+    ws = (c.wq, c.wk, c.wv, c.wo, c.wi0, c.wi1, c.wff_o, c.ln1, c.ln2)
+    lw = tuple(w.to(dev) for w in ws)
     table = c.table.to(dev)
-    flat = torch.cat([xb[b, :n] for b, n in enumerate(lens)])
+    flat = torch.cat([xbd[b, :n] for b, n in enumerate(lens)])
     pos = torch.cat([torch.arange(n) for n in lens]).to(dev)
-    got = mt5_encoder_flat(flat, pos, [lw, lw], table)
+    got = mt5_encoder_flat(flat, pos, [lw, lw], table).float().cpu()
     valid = torch.arange(L, device=dev)[None, :] < torch.tensor(lens, device=dev)[:, None]
     mask = ((~valid).to(xb.dtype) * torch.finfo(xb.dtype).min).view(3, 1, 1, L)
-    want_b = mt5_layer_forward(mt5_layer_forward(xb, *lw, table, mask), *lw, table, mask)
-    want = torch.cat([want_b[b, :n] for b, n in enumerate(lens)])
-    assert torch.equal(got, want)
+    want_b = mt5_layer_forward(mt5_layer_forward(xbd, *lw, table, mask), *lw, table, mask).float().cpu()
+    cmask = ((~valid.cpu()).to(xb.dtype) * torch.finfo(xb.dtype).min).view(3, 1, 1, L)
+    ref = oe.mt5_layer(oe.mt5_layer(xb, *ws, c.table, cmask), *ws, c.table, cmask)
+    a = 0
+    for b, n in enumerate(lens):
+        g_, w_ = got[a:a + n], want_b[b, :n]
+        dp = (g_ - w_).abs().max().item()
+        err = (g_ - ref[b, :n]).abs().max().item()
+        cs = cosine(g_, ref[b, :n])
+        print(f"flat row {b} (len {n}): vs padded {dp:.3e}; vs oracle {err:.3e} cosine {cs:.6f}")
+        assert dp <= 2 * 2.0 ** -7 * w_.abs().max().item(), (b, dp)
+        assert err <= 6e-2 and cs >= 0.9999, (b, err, cs)
+        a += n
 
 
 def test_mt5_layer_packed_matches_oracle_and_padded_layer():

@@ -146,3 +146,41 @@ def test_device_buckets_exact(dev, dtype, bidirectional):
         rows = member.any(dim=1)
         got = out[0, 0].float().cpu() > 1e-3
         assert torch.equal(got[rows], member[rows]), f"bucket {hot}"
+
+
+@pytest.mark.parametrize("lens", [[768, 512, 700, 601], [1, 130, 0, 257, 64]])
+def test_varlen_matches_padded_call_and_oracle(dev, lens):
+    """flash_attention_rpb_varlen on packed [T, H, 64] rows (a view of a fused
+    [T, 3, H, 64] projection, so strided) against the padded call with the
+    reference's [B, 1, 1, L] key mask on the same sequences: the kernel runs
+    the same tiles in the same order and masked keys contribute exact zeros,
+    so the valid rows are equal bit for bit; and against the oracle at the
+    attention tolerance. Includes an empty and a one-token sequence and
+    lengths that are not tile multiples."""
+    from kernels.flash_attention_rpb import flash_attention_rpb_varlen
+    g = torch.Generator().manual_seed(sum(lens))
+    B, H, L = len(lens), 16, max(lens)
+    T = sum(lens)
+    qkv = (torch.randn(T, 3, H, 64, generator=g) * 0.64).bfloat16()
+    table = (torch.randn(32, H, generator=g) * 0.1).bfloat16()
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    pad = torch.zeros(B, L, 3, H, 64, dtype=torch.bfloat16)
+    for b in range(B):
+        pad[b, :lens[b]] = qkv[int(cu[b]):int(cu[b + 1])]
+    q, k, v = (pad[:, :, i].transpose(1, 2) for i in range(3))      # [B, H, L, 64]
+    keep = (torch.arange(L)[None] < torch.tensor(lens)[:, None]).bfloat16()
+    mask = ((1.0 - keep) * torch.finfo(torch.bfloat16).min)[:, None, None, :]
+    print(f"rpb varlen lens {lens}", flush=True)
+    qd = qkv.to(dev)
+    got = flash_attention_rpb_varlen(qd[:, 0], qd[:, 1], qd[:, 2], cu.to(dev), L, table.to(dev),
+                                     32, 128).cpu()
+    padded = _rpb()(q.contiguous().to(dev), k.contiguous().to(dev), v.contiguous().to(dev),
+                    table.to(dev), 32, 128, False, padding_mask=mask.to(dev)).cpu()
+    want = oa.rpb_attention(q, k, v, table, 32, 128, False, mask, 1.0)
+    for b in range(B):
+        a, e = int(cu[b]), int(cu[b + 1])
+        if e == a:
+            continue
+        gb = got[a:e].transpose(0, 1)                                 # [H, n, 64]
+        assert torch.equal(gb, padded[b, :, :e - a]), f"sequence {b}"
+        assert_attn_close(gb, want[b, :, :e - a], f"varlen seq {b}")

@@ -30,6 +30,10 @@ struct RpbArgs {
   int bidir, causal, offset_pos;  // offset added for rel > 0 (bidirectional)
   int lut_len;  // ntiles * kBN + kBM (LDS bias table entries)
   StepFn step;
+  // packed sequences (nullptr: the padded batch): "batch" b is sequence b,
+  // tokens cu[b] .. cu[b + 1] - 1 of [T, H, D] tensors (strides [.][1] =
+  // head, [.][2] = token); Lq = Lk = the longest sequence
+  const int32_t* cu;
 };
 
 __device__ inline float ld_f(const void* p, int dt, int64_t i) {
@@ -73,6 +77,7 @@ struct RpbPolicy {
   float* maskt;          // MASK_KEY: [2][kBN] mask values of the tile in slot i & 1
   const float* lut;      // bias per relative position (raw score units) or nullptr
   int lut_base, b, h, t, hl, qrow, wq_lo, wq_hi;
+  int Lq, Lk;            // query / key rows of this (batch, head) or sequence
   bool nolive;           // MASK_KEY: every key of the row range masked away
 
   static constexpr bool kAllActive = !CAUSAL;
@@ -85,16 +90,16 @@ struct RpbPolicy {
   __device__ float meta_ld(int i) const {
     if (MASK != MASK_KEY || t >= kBN || !(tflag[tile(i)] & 1)) return 0.f;
     const int j = key0(i) + t;
-    return j < a->Lk ? mask_raw(ld_f(a->mask, a->mask_dt, b * a->ms[0] + h * a->ms[1] + j * a->ms[3]),
+    return j < Lk ? mask_raw(ld_f(a->mask, a->mask_dt, b * a->ms[0] + h * a->ms[1] + j * a->ms[3]),
                                 a->inv_scale)
                      : 0.f;
   }
   __device__ void meta_st(float v, int slot) {
     if (MASK == MASK_KEY && t < kBN) maskt[slot * kBN + t] = v;
   }
-  __device__ bool wave_active() const { return wq_lo < a->Lq; }
+  __device__ bool wave_active() const { return wq_lo < Lq; }
   __device__ bool active(int i) const {
-    if (wq_lo >= a->Lq) return false;
+    if (wq_lo >= Lq) return false;
     return !CAUSAL || key0(i) <= wq_hi;
   }
   __device__ bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot) const {
@@ -112,21 +117,21 @@ struct RpbPolicy {
       if (MASK == MASK_KEY && (tflag[tile(i)] & 1)) add_by_key(s0, s1, maskt + slot * kBN + 4 * hl);
     }
     if (MASK == MASK_FULL) {
-      if (qrow < a->Lq) {
+      if (qrow < Lq) {
         const int64_t mo = b * a->ms[0] + h * a->ms[1] + (int64_t)qrow * a->ms[2];
         map_scores(s0, s1, [&](int e, float v) {
           const int j = k0 + x_key(e, hl);
-          return j < a->Lk ? v + mask_raw(ld_f(a->mask, a->mask_dt, mo + (int64_t)j * a->ms[3]),
+          return j < Lk ? v + mask_raw(ld_f(a->mask, a->mask_dt, mo + (int64_t)j * a->ms[3]),
                                           a->inv_scale)
                            : v;
         });
       }
       exact = true;
     }
-    if (k0 + kBN > a->Lk || (CAUSAL && k0 + kBN - 1 > wq_lo)) {
+    if (k0 + kBN > Lk || (CAUSAL && k0 + kBN - 1 > wq_lo)) {
       map_scores(s0, s1, [&](int e, float v) {
         const int j = k0 + x_key(e, hl);
-        return (j >= a->Lk || (CAUSAL && j > qrow)) ? -INFINITY : v;
+        return (j >= Lk || (CAUSAL && j > qrow)) ? -INFINITY : v;
       });
     }
     return exact;
@@ -143,12 +148,6 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   __shared__ int ntl;
   __shared__ int nolive_s;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int ntiles_all = (a.Lk + kBN - 1) / kBN;
-  const int nt4 = (ntiles_all + 3) & ~3;
-  int* tflag = reinterpret_cast<int*>(smem);  // [nt4]
-  int* tiles = tflag + nt4;                   // [nt4]
-  float* lut = reinterpret_cast<float*>(tiles + nt4);
-
   const int nqt = (a.Lq + kBM - 1) / kBM;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
   const int qt = work % nqt;
@@ -156,6 +155,26 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   const int h = bh % a.H, b = bh / a.H;
   const int q0 = qt * kBM;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, hl = lane >> 5;
+  // rows of this (batch, head) or sequence, and their offsets in q, k, v, o
+  int Lq = a.Lq, Lk = a.Lk;
+  int64_t qo = b * a.qs[0], ko = b * a.ks[0], vo = b * a.vs[0], oo = b * a.os[0];
+  if (a.cu) {
+    const int tok0 = a.cu[b];
+    // rows past max_seqlen (a.Lq) are not computed: the LDS tables are sized
+    // for a.Lk keys
+    Lq = Lk = min(a.cu[b + 1] - tok0, a.Lq);
+    if (q0 >= Lq) return;  // whole workgroup: uniform exit
+    qo = (int64_t)tok0 * a.qs[2]; ko = (int64_t)tok0 * a.ks[2];
+    vo = (int64_t)tok0 * a.vs[2]; oo = (int64_t)tok0 * a.os[2];
+  }
+  // the host sizes the dynamic LDS for a.Lk keys, an upper bound of Lk
+  const int ntiles_all = (Lk + kBN - 1) / kBN;
+  const int nt4 = (ntiles_all + 3) & ~3;
+  const int nt4_lds = (((a.Lk + kBN - 1) / kBN) + 3) & ~3;
+  int* tflag = reinterpret_cast<int*>(smem);  // [nt4]
+  int* tiles = tflag + nt4_lds;               // [nt4]
+  float* lut = reinterpret_cast<float*>(tiles + nt4_lds);
+  (void)nt4;
 
   // ---- bias table over rel = key - query, rel in [-(q0+127), Lk-1-q0] ----
   // the step thresholds and the head's table column go to LDS first, so each
@@ -187,7 +206,7 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   }
   // ---- key tiles: causal limit, and (key mask) the tiles with a live key ----
   int kt_end = ntiles_all;
-  if (CAUSAL) kt_end = min(kt_end, (min(q0 + kBM, a.Lq) - 1) / kBN + 1);
+  if (CAUSAL) kt_end = min(kt_end, (min(q0 + kBM, Lq) - 1) / kBN + 1);
   int n = kt_end;
   bool direct = true;  // live tiles are 0 .. n-1 (no list indirection)
   if (MASK == MASK_KEY) {
@@ -197,10 +216,10 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
     for (int j0 = 0; j0 < ntiles_all * kBN; j0 += 256) {
       const int j = j0 + t;
       float mv = 0.f;
-      if (j < a.Lk) mv = ld_f(mb, a.mask_dt, b * a.ms[0] + h * a.ms[1] + j * a.ms[3]);
+      if (j < Lk) mv = ld_f(mb, a.mask_dt, b * a.ms[0] + h * a.ms[1] + j * a.ms[3]);
       // bit0: some nonzero value; bit1: some key that is not clamped away
       const unsigned long long nz = __builtin_amdgcn_ballot_w64(mv != 0.f);
-      const unsigned long long lv = __builtin_amdgcn_ballot_w64(j < a.Lk && mask_raw(mv, a.inv_scale) > -1.0e30f);
+      const unsigned long long lv = __builtin_amdgcn_ballot_w64(j < Lk && mask_raw(mv, a.inv_scale) > -1.0e30f);
       const int tile = (j0 >> 6) + w;
       if (lane == 0 && tile < ntiles_all) tflag[tile] = (nz ? 1 : 0) | (lv ? 2 : 0);
     }
@@ -235,10 +254,9 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
 
   RpbPolicy<E, MASK, CAUSAL> pol;
   pol.a = &a;
-  tile_src_init(pol.ksrc, reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1],
-                (int)a.ks[2], a.Lk);
-  tile_src_init(pol.vsrc, reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1],
-                (int)a.vs[2], a.Lk);
+  tile_src_init(pol.ksrc, reinterpret_cast<const uint16_t*>(a.k) + ko + h * a.ks[1], (int)a.ks[2], Lk);
+  tile_src_init(pol.vsrc, reinterpret_cast<const uint16_t*>(a.v) + vo + h * a.vs[1], (int)a.vs[2], Lk);
+  pol.Lq = Lq; pol.Lk = Lk;
   pol.tiles = (MASK == MASK_KEY && !direct) ? tiles : nullptr;
   pol.tflag = tflag;
   pol.maskt = maskt;
@@ -247,26 +265,26 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   pol.b = b; pol.h = h; pol.t = t; pol.hl = hl;
   pol.wq_lo = q0 + w * 32;
   pol.qrow = pol.wq_lo + (lane & 31);
-  pol.wq_hi = min(pol.wq_lo + 31, a.Lq - 1);
+  pol.wq_hi = min(pol.wq_lo + 31, Lq - 1);
   // lut index of element e in the tile at key0: key0 + x_key(e, 0) + lut_base
   pol.lut_base = 4 * hl - w * 32 - (lane & 31) + (kBM - 1);
   attn_pipe_start(pol, n, K0, K1, V0);
 
-  const bool qvalid = pol.qrow < a.Lq;
+  const bool qvalid = pol.qrow < Lq;
   u32x4_t qf[4];
-  load_q(qf, reinterpret_cast<const uint16_t*>(a.q) + b * a.qs[0] + h * a.qs[1] +
-                 (int64_t)pol.qrow * a.qs[2], qvalid);
+  load_q(qf, reinterpret_cast<const uint16_t*>(a.q) + qo + h * a.qs[1] + (int64_t)pol.qrow * a.qs[2],
+         qvalid);
 
   float m = -INFINITY, l = 0.f;
   f32x16_t o0 = {}, o1 = {};
   attn_loop_db<E>(pol, K0, K1, V0, V1, n, qf, a.c2, m, l, o0, o1);
   const float l_tot = half_swap_sum(l);
   // whole-row stores through this wave's half of K0 / K1 (free after the loop)
-  uint16_t* ob = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1];
+  uint16_t* ob = reinterpret_cast<uint16_t*>(a.o) + oo + h * a.os[1];
   const int wq_lo = pol.wq_lo;
   store_out_rows<E>((w < 2 ? K0 : K1) + (w & 1) * 2048, o0, o1, l_tot,
                     [&](int r) { return ob + (int64_t)(wq_lo + r) * a.os[2]; },
-                    [&](int r) { return wq_lo + r < a.Lq; });
+                    [&](int r) { return wq_lo + r < Lq; });
 }
 
 // ---------------------------------------------------------------------------
@@ -351,12 +369,73 @@ static int check_bhld(const vfk_tensor* t, const char* name, int dtype) {
   return VFK_OK;
 }
 
+// Scale, bucket step function and bias table of a launch (shared by the
+// padded and packed entry points).
+static int rpb_setup(RpbArgs& a, const vfk_tensor* rpb_table, int32_t num_buckets,
+                     int32_t max_distance, int32_t is_decoder, float softmax_scale, int64_t H,
+                     const char* name) {
+  if (!(softmax_scale > 0.f) || !isfinite(softmax_scale))
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: softmax_scale must be > 0", name);
+  a.c2 = softmax_scale * VFK_LOG2E;
+  a.inv_scale = 1.0f / softmax_scale;
+  a.bidir = is_decoder ? 0 : 1;
+  a.causal = is_decoder ? 1 : 0;
+  if (present(rpb_table)) {
+    int rc;
+    if ((rc = check_tensor(rpb_table, "rpb_table", 2))) return rc;
+    if (rpb_table->size[1] != H)
+      return set_error(VFK_ERR_INVALID, "rpb_table: expected [buckets, %lld]", (long long)H);
+    if (rpb_table->size[0] < 1)
+      return set_error(VFK_ERR_INVALID, "rpb_table: no buckets");
+    a.table = rpb_table->data; a.table_dt = rpb_table->dtype;
+    a.tb0 = rpb_table->stride[0]; a.tb1 = rpb_table->stride[1];
+    a.total_buckets = (int)rpb_table->size[0];
+    if ((rc = build_t5_step(a.bidir, num_buckets, max_distance, &a.step))) return rc;
+    a.offset_pos = num_buckets / 2;
+  }
+  return VFK_OK;
+}
+
+// MFMA launch over a.B x a.H x ceil(a.Lq / 128) workgroups, LDS sized for
+// a.Lk keys.
+static int rpb_launch(RpbArgs& a, int mode, int dt, hipStream_t st, const char* name) {
+  // tile buffer resources span Lk rows of one (batch, head): byte sizes < 2^31
+  if ((int64_t)a.Lk * std::max(a.ks[2], a.vs[2]) * 2 >= (1ll << 31))
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: Lk x row stride too large", name);
+  const int ntiles = ceil_div(a.Lk, kBN);
+  a.lut_len = a.table ? ntiles * kBN + kBM : 0;
+  // dynamic LDS: tile flags and list, bias table, step thresholds and the
+  // head's table column (tiles and masks are static)
+  const size_t lds = (size_t)((ntiles + 3) & ~3) * 8 + (size_t)a.lut_len * 4 +
+                     (a.table ? (size_t)kThrPad * 2 + (size_t)a.total_buckets * 4 : 0);
+  if (lds + 4 * kTileElems * 2 + 2 * kBN * 4 > 160 * 1024)
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: Lk=%d needs too much LDS", name, a.Lk);
+  const int nqt = ceil_div(a.Lq, kBM);
+  dim3 grid((unsigned)((int64_t)nqt * a.B * a.H));
+#define VFK_RPB_GO(E, M, C) hipLaunchKernelGGL((rpb_fwd_kernel<E, M, C>), grid, dim3(256), lds, st, a)
+#define VFK_RPB_LAUNCH(E)                                                               \
+  switch (mode) {                                                                       \
+    case MASK_NONE: if (a.causal) VFK_RPB_GO(E, MASK_NONE, true); else VFK_RPB_GO(E, MASK_NONE, false); break; \
+    case MASK_KEY: if (a.causal) VFK_RPB_GO(E, MASK_KEY, true); else VFK_RPB_GO(E, MASK_KEY, false); break;    \
+    default: if (a.causal) VFK_RPB_GO(E, MASK_FULL, true); else VFK_RPB_GO(E, MASK_FULL, false); break;        \
+  }
+  if (dt == VFK_BF16) {
+    VFK_RPB_LAUNCH(BF16)
+  } else {
+    VFK_RPB_LAUNCH(F16)
+  }
+#undef VFK_RPB_LAUNCH
+#undef VFK_RPB_GO
+  return launch_status(name);
+}
+
 extern "C" int vfk_flash_rpb_fwd(const vfk_tensor* q, const vfk_tensor* k,
                                  const vfk_tensor* v, const vfk_tensor* rpb_table,
                                  int32_t num_buckets, int32_t max_distance,
                                  int32_t is_decoder, const vfk_tensor* mask,
                                  float softmax_scale, vfk_tensor* out,
                                  void* stream) {
+  const char* name = "vfk_flash_rpb_fwd";
   int rc = check_tensor(q, "q", 4);
   if (rc) return rc;
   const int dt = q->dtype;
@@ -379,24 +458,8 @@ extern "C" int vfk_flash_rpb_fwd(const vfk_tensor* q, const vfk_tensor* k,
     a.vs[i] = v->stride[i]; a.os[i] = out->stride[i];
   }
   a.B = (int)B; a.H = (int)H; a.Lq = (int)Lq; a.Lk = (int)Lk;
-  if (!(softmax_scale > 0.f) || !isfinite(softmax_scale))
-    return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_rpb_fwd: softmax_scale must be > 0");
-  a.c2 = softmax_scale * VFK_LOG2E;
-  a.inv_scale = 1.0f / softmax_scale;
-  a.bidir = is_decoder ? 0 : 1;
-  a.causal = is_decoder ? 1 : 0;
-  if (present(rpb_table)) {
-    if ((rc = check_tensor(rpb_table, "rpb_table", 2))) return rc;
-    if (rpb_table->size[1] != H)
-      return set_error(VFK_ERR_INVALID, "rpb_table: expected [buckets, %lld]", (long long)H);
-    if (rpb_table->size[0] < 1)
-      return set_error(VFK_ERR_INVALID, "rpb_table: no buckets");
-    a.table = rpb_table->data; a.table_dt = rpb_table->dtype;
-    a.tb0 = rpb_table->stride[0]; a.tb1 = rpb_table->stride[1];
-    a.total_buckets = (int)rpb_table->size[0];
-    if ((rc = build_t5_step(a.bidir, num_buckets, max_distance, &a.step))) return rc;
-    a.offset_pos = num_buckets / 2;
-  }
+  if ((rc = rpb_setup(a, rpb_table, num_buckets, max_distance, is_decoder, softmax_scale, H, name)))
+    return rc;
   int mode = MASK_NONE;
   if (present(mask)) {
     if ((rc = check_tensor(mask, "padding_mask", 4))) return rc;
@@ -420,35 +483,55 @@ extern "C" int vfk_flash_rpb_fwd(const vfk_tensor* q, const vfk_tensor* k,
       hipLaunchKernelGGL(rpb_fwd_f32_kernel<MASK_NONE>, grid, dim3(64), 0, st, a);
     else
       hipLaunchKernelGGL(rpb_fwd_f32_kernel<MASK_FULL>, grid, dim3(64), 0, st, a);
-    return launch_status("vfk_flash_rpb_fwd");
+    return launch_status(name);
   }
-  // tile buffer resources span Lk rows of one (batch, head): byte sizes < 2^31
-  if ((int64_t)Lk * std::max(a.ks[2], a.vs[2]) * 2 >= (1ll << 31))
-    return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_rpb_fwd: Lk x row stride too large");
-  const int ntiles = ceil_div(Lk, kBN);
-  a.lut_len = a.table ? ntiles * kBN + kBM : 0;
-  // dynamic LDS: tile flags and list, bias table, step thresholds and the
-  // head's table column (tiles and masks are static)
-  const size_t lds = (size_t)((ntiles + 3) & ~3) * 8 + (size_t)a.lut_len * 4 +
-                     (a.table ? (size_t)kThrPad * 2 + (size_t)a.total_buckets * 4 : 0);
-  if (lds + 4 * kTileElems * 2 + 2 * kBN * 4 > 160 * 1024)
-    return set_error(VFK_ERR_UNSUPPORTED, "vfk_flash_rpb_fwd: Lk=%lld needs too much LDS",
-                     (long long)Lk);
-  const int nqt = ceil_div(Lq, kBM);
-  dim3 grid((unsigned)(nqt * B * H));
-#define VFK_RPB_GO(E, M, C) hipLaunchKernelGGL((rpb_fwd_kernel<E, M, C>), grid, dim3(256), lds, st, a)
-#define VFK_RPB_LAUNCH(E)                                                               \
-  switch (mode) {                                                                       \
-    case MASK_NONE: if (a.causal) VFK_RPB_GO(E, MASK_NONE, true); else VFK_RPB_GO(E, MASK_NONE, false); break; \
-    case MASK_KEY: if (a.causal) VFK_RPB_GO(E, MASK_KEY, true); else VFK_RPB_GO(E, MASK_KEY, false); break;    \
-    default: if (a.causal) VFK_RPB_GO(E, MASK_FULL, true); else VFK_RPB_GO(E, MASK_FULL, false); break;        \
-  }
-  if (dt == VFK_BF16) {
-    VFK_RPB_LAUNCH(BF16)
-  } else {
-    VFK_RPB_LAUNCH(F16)
-  }
-#undef VFK_RPB_LAUNCH
-#undef VFK_RPB_GO
-  return launch_status("vfk_flash_rpb_fwd");
+  return rpb_launch(a, mode, dt, st, name);
+}
+
+// [T, H, 64] tensor of a packed stream (token stride [0], head stride [1]).
+static int check_thd_rpb(const vfk_tensor* t, const char* name, int dtype, int64_t T, int64_t H) {
+  int rc = check_tensor(t, name, 3);
+  if (rc) return rc;
+  if (t->dtype != dtype) return set_error(VFK_ERR_INVALID, "%s: dtype differs from q", name);
+  if (t->size[0] != T || t->size[1] != H)
+    return set_error(VFK_ERR_INVALID, "%s: expected [%lld, %lld, 64]", name, (long long)T, (long long)H);
+  if (t->size[2] != kHD)
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: head_dim %lld (only 64 is built)", name, (long long)t->size[2]);
+  if (t->stride[2] != 1) return set_error(VFK_ERR_INVALID, "%s: head_dim must be contiguous", name);
+  if (!aligned16(t->data) || t->stride[0] % 8 || t->stride[1] % 8)
+    return set_error(VFK_ERR_INVALID, "%s: rows must be 16-byte aligned", name);
+  return VFK_OK;
+}
+
+extern "C" int vfk_flash_rpb_varlen_fwd(const vfk_tensor* q, const vfk_tensor* k, const vfk_tensor* v,
+                                        const int32_t* cu_seqlens, int32_t num_seqs, int32_t max_seqlen,
+                                        const vfk_tensor* rpb_table, int32_t num_buckets,
+                                        int32_t max_distance, int32_t is_decoder, float softmax_scale,
+                                        vfk_tensor* out, void* stream) {
+  const char* name = "vfk_flash_rpb_varlen_fwd";
+  int rc = check_tensor(q, "q", 3);
+  if (rc) return rc;
+  const int dt = q->dtype;
+  if (dt != VFK_BF16 && dt != VFK_F16)
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: bf16 or fp16 only", name);
+  const int64_t T = q->size[0], H = q->size[1];
+  if ((rc = check_thd_rpb(q, "q", dt, T, H)) || (rc = check_thd_rpb(k, "k", dt, T, H)) ||
+      (rc = check_thd_rpb(v, "v", dt, T, H)) || (rc = check_thd_rpb(out, "out", dt, T, H)))
+    return rc;
+  if (!cu_seqlens) return set_error(VFK_ERR_INVALID, "%s: NULL cu_seqlens", name);
+  if (num_seqs < 0 || max_seqlen < 0 || max_seqlen > (1 << 20) || (int64_t)num_seqs * H > (1 << 24))
+    return set_error(VFK_ERR_INVALID, "%s: bad num_seqs / max_seqlen", name);
+  RpbArgs a = {};
+  a.q = q->data; a.k = k->data; a.v = v->data; a.o = out->data;
+  // [T, H, D] as the padded kernel's [., H, L, D]: head stride [1], row stride [2]
+  a.qs[1] = q->stride[1]; a.qs[2] = q->stride[0]; a.qs[3] = 1;
+  a.ks[1] = k->stride[1]; a.ks[2] = k->stride[0]; a.ks[3] = 1;
+  a.vs[1] = v->stride[1]; a.vs[2] = v->stride[0]; a.vs[3] = 1;
+  a.os[1] = out->stride[1]; a.os[2] = out->stride[0]; a.os[3] = 1;
+  a.B = num_seqs; a.H = (int)H; a.Lq = max_seqlen; a.Lk = max_seqlen;
+  a.cu = cu_seqlens;
+  if ((rc = rpb_setup(a, rpb_table, num_buckets, max_distance, is_decoder, softmax_scale, H, name)))
+    return rc;
+  if (num_seqs == 0 || H == 0 || max_seqlen == 0 || T == 0) return VFK_OK;
+  return rpb_launch(a, MASK_NONE, dt, (hipStream_t)stream, name);
 }

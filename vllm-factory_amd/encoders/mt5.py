@@ -44,33 +44,30 @@ def mt5_layer_forward(x: torch.Tensor, wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2
 
 
 def mt5_layer_packed(x: torch.Tensor, cu_seqlens: torch.Tensor, max_len: int, wq, wk, wv, wo,
-                     wi0, wi1, wff_o, ln1, ln2, table, mask, num_buckets: int = 32,
+                     wi0, wi1, wff_o, ln1, ln2, table, mask=None, num_buckets: int = 32,
                      max_distance: int = 128, eps: float = 1e-6, wqkv=None) -> torch.Tensor:
-    """The layer of mt5_layer_forward on the packed valid rows of a padded batch.
+    """The layer of mt5_layer_forward on packed sequences, without padding.
 
-    x [T, d_model]: the valid rows of the batch in order (sequence b owns
-    rows cu_seqlens[b] .. cu_seqlens[b + 1] - 1, int32 on the device);
-    mask: the [B, 1, 1, max_len] additive key mask of the padded batch. The
-    RMSNorms, projections, FFN and residual adds run on the T valid rows
-    only; the fused q|k|v projection is padded once into [B, max_len, 3D] for
-    the RPB attention, which writes its output as [B, max_len, H, d] rows that
-    one unpad returns to [T, D] for the output projection. Row for row the
-    same arithmetic as the padded layer. wqkv: the [D, 3D] concatenation of
-    wq, wk, wv when the caller keeps one (built here otherwise)."""
-    from kernels.packing import pad_packed, unpad_packed
+    x [T, d_model]: sequence s owns rows cu_seqlens[s] .. cu_seqlens[s + 1] -
+    1 (int32 on the device), max_len >= every sequence length. Every part
+    runs on the T rows: the RMSNorms, the fused q|k|v projection, the RPB
+    attention over the packed sequences (flash_attention_rpb_varlen: each
+    sequence attends to its own rows, as the padded layer with the
+    reference's key mask does on its valid rows), the output projection, FFN
+    and residual adds. mask is accepted for the padded layer's signature and
+    not used. wqkv: the [D, 3D] concatenation of wq, wk, wv when the caller
+    keeps one (built here otherwise)."""
+    from kernels.flash_attention_rpb import flash_attention_rpb_varlen
     T, D = x.shape
-    B = cu_seqlens.numel() - 1
     H = table.shape[1]
     d = D // H
     if wqkv is None:
         wqkv = torch.cat((wq, wk, wv), 1)
     h = rms_norm(x, ln1, eps)
-    qkv, _ = pad_packed(h @ wqkv, cu_seqlens, B, max_len)
-    q, k, v = (t.transpose(1, 2) for t in qkv.view(B, max_len, 3, H, d).unbind(2))
-    att = torch.empty(B, max_len, H, d, dtype=x.dtype, device=x.device)
-    flash_attention_rpb_final(q, k, v, table, num_buckets, max_distance, False, padding_mask=mask,
-                              softmax_scale=1.0, out=att.transpose(1, 2))
-    o = unpad_packed(att.view(B, max_len, D), cu_seqlens, T) @ wo
+    qkv = (h @ wqkv).view(T, 3, H, d)
+    att = flash_attention_rpb_varlen(qkv[:, 0], qkv[:, 1], qkv[:, 2], cu_seqlens, max_len, table,
+                                     num_buckets, max_distance, False, 1.0)
+    o = att.view(T, D) @ wo
     h2, x1 = fused_add_rms_norm(o, x, ln2, eps)
     g = fused_gelu_mul_dropout(h2 @ wi0, h2 @ wi1, "gelu_new")
     return torch.addmm(x1, g, wff_o)
@@ -107,7 +104,7 @@ def mt5_encoder_forward(input_ids: Optional[torch.Tensor], attention_mask: Optio
         T = int(cu[-1])
         xf = unpad_packed(x, cu, T)
         for lw in layers:
-            xf = mt5_layer_packed(xf, cu, L, *lw, table, mask, num_buckets, max_distance, eps,
+            xf = mt5_layer_packed(xf, cu, L, *lw, table, None, num_buckets, max_distance, eps,
                                   wqkv=torch.cat(lw[:3], 1))
         x, _ = pad_packed(rms_norm(xf, final_ln, eps), cu, B, L)
         return x.squeeze(0) if squeeze else x
@@ -140,18 +137,15 @@ def mt5_encoder_flat(x: torch.Tensor, positions: torch.Tensor, layers, table: to
     runs the encoder on the flat [1, T] stream with an all-ones mask, so the
     tokens of different requests attend to each other. Here the sequences are
     found from the position ids on the device (a sequence starts at position
-    0, kernels.packing.seq_metadata rule "zero"), padded into [n, L, d_model]
-    once, run with the reference's additive key mask (1 - m) * finfo.min
-    (models/mt5/mt5_encoder.py:571-576), and the valid rows are concatenated
-    back; each sequence gets the attention it would get alone.
+    0, kernels.packing.seq_metadata rule "zero") and every layer runs on the
+    packed rows (mt5_layer_packed: attention over the packed sequences, no
+    padding); each sequence gets the attention it would get alone.
     x: embedding output [T, d_model]; layers: (wq, wk, wv, wo, wi0, wi1, wff_o,
     ln1, ln2) per layer as for mt5_layer_forward."""
-    from kernels.packing import pad_packed, read_metadata, seq_metadata, unpad_packed
+    from kernels.packing import read_metadata, seq_metadata
     cu, meta = seq_metadata(positions, "zero")
     cu, n, max_len, _ = read_metadata(cu, meta)
-    xb, lens = pad_packed(x, cu, n, max_len)
-    valid = torch.arange(max_len, device=x.device)[None, :] < lens[:, None]
-    mask = ((~valid).to(x.dtype) * torch.finfo(x.dtype).min).view(n, 1, 1, max_len)
     for lw in layers:
-        xb = mt5_layer_forward(xb, *lw, table, mask, num_buckets, max_distance, eps)
-    return unpad_packed(xb, cu, x.shape[0])
+        x = mt5_layer_packed(x, cu, max_len, *lw, table, None, num_buckets, max_distance, eps,
+                             wqkv=torch.cat(lw[:3], 1))
+    return x

@@ -64,3 +64,45 @@ def flash_attention_rpb_final(
     )
     return out
 
+
+
+def flash_attention_rpb_varlen(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    max_seqlen: int,
+    rpb_table: Optional[torch.Tensor],
+    num_buckets: int,
+    max_distance: int,
+    is_decoder: bool = False,
+    softmax_scale: float = 1.0,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """flash_attention_rpb_final over packed sequences, without padding.
+
+    q, k, v [T, H, 64] (bf16 / fp16, any token and head strides with a
+    contiguous last dim); sequence s is rows cu_seqlens[s] .. cu_seqlens[s+1]
+    - 1 (int32 on the device) and attends to its own rows only, relative
+    positions counted inside the sequence. Equals the padded call with the
+    reference's [B, 1, 1, L] key mask on the valid rows. max_seqlen must be
+    >= every sequence length. Returns [T, H, 64] (or writes `out`)."""
+    dev = _lib.require_gpu(q, k, v, cu_seqlens, rpb_table)
+    if q.dim() != 3 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("q, k, v must be [T, H, D] of one shape")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, v must share a dtype")
+    qq, kk, vv = (_lib.rows_aligned(t) for t in (q, k, v))
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
+        raise ValueError("out must match q's shape, dtype and device")
+    cu = cu_seqlens.to(torch.int32).contiguous()
+    _lib.on_device(
+        "vfk_flash_rpb_varlen_fwd", dev,
+        _lib.ref(_lib.desc(qq)), _lib.ref(_lib.desc(kk)), _lib.ref(_lib.desc(vv)),
+        cu.data_ptr(), int(cu.numel() - 1), int(max_seqlen),
+        _lib.ref(_lib.desc(rpb_table)), int(num_buckets), int(max_distance), int(bool(is_decoder)),
+        float(softmax_scale), _lib.ref(_lib.desc(out)),
+    )
+    return out
