@@ -493,13 +493,24 @@ def deberta_layer_config3(torch, args):
     x, sl = hidden.to(dev, torch.bfloat16), lens.to(dev)
     w = random_weights(num_layers=1).to(dev)
     rel = deberta_rel_embeddings(w)
+    from encoders.deberta import deberta_layer_packed
+    from kernels.packing import unpad_packed
     fn = lambda: deberta_layer_forward(x, sl, rel, w.layers[0], w)
-    for _ in range(args.warmup):
-        fn()
-    ms = device_ms(torch, fn, args.steps)
     tv = int(lens.sum())
+    cu = torch.cat([lens.new_zeros(1), lens.cumsum(0)]).to(device=dev, dtype=torch.int32)
+    xf = unpad_packed(x, cu, tv)
+    L = x.shape[1]
+    fp = lambda: deberta_layer_packed(xf, cu, L, rel, w.layers[0], w)
+    res = {}
+    for name, f in (("padded", fn), ("packed", fp)):
+        for _ in range(args.warmup):
+            f()
+        res[name] = device_ms(torch, f, args.steps)
+    ms = res["packed"]
     return dict(ms_per_layer=ms, valid_tokens_per_s=tv / (ms * 1e-3), valid_tokens=tv,
-                padded_tokens=int(x.shape[0] * x.shape[1]))
+                padded_tokens=int(x.shape[0] * x.shape[1]), padded_layer_ms=res["padded"],
+                note="ms_per_layer: the layer on the packed valid rows (deberta_layer_packed, "
+                     "varlen attention); padded_layer_ms: the same layer over the padded batch")
 
 
 def deberta_v1_layer_config3(torch, args):

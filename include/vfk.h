@@ -153,6 +153,24 @@ int vfk_deberta_fused_fwd(const vfk_tensor* q, const vfk_tensor* k,
                           int32_t use_log_bucket, vfk_tensor* out,
                           void* stream);
 
+/* vfk_deberta_fused_fwd over packed sequences (no padding): sequence s is
+ * tokens cu_seqlens[s] .. cu_seqlens[s + 1] - 1 of q, k, v, out [T, H, 64]
+ * (bf16 / fp16, 16-byte aligned rows, any token / head strides) and attends
+ * to its own tokens only, relative positions inside the sequence. It is the
+ * padded call with seq_lengths on the valid rows: the flat DeBERTa callers
+ * (plugins/deberta_gliner/model.py:166-202,
+ * plugins/deberta_gliner2/model.py:124-137) run on it without re-padding.
+ * cu_seqlens: device int32 [num_seqs + 1]; max_seqlen >= every sequence
+ * length (rows past it are not computed); bucket steps must be unit
+ * (vfk_deberta_unit_steps). */
+int vfk_deberta_fused_varlen_fwd(const vfk_tensor* q, const vfk_tensor* k,
+                                 const vfk_tensor* v, const int32_t* cu_seqlens,
+                                 int32_t num_seqs, int32_t max_seqlen,
+                                 const vfk_tensor* key_rel, const vfk_tensor* query_rel,
+                                 float sm_scale, int32_t position_buckets,
+                                 int32_t max_relative_distance, int32_t use_log_bucket,
+                                 vfk_tensor* out, void* stream);
+
 /* Varlen (packed) bidirectional attention with optional RoPE and sliding
  * window, for ModernBERT (no counterpart kernel in the reference: it replaces
  * the rotary step and F.scaled_dot_product_attention with the dense O(T^2)

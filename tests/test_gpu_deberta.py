@@ -212,3 +212,34 @@ def test_gather_staged_c2p_only_vs_oracle(dev):
                                        None, False, SM, 128, 256, True)
     assert_attn_close(got[0], want[0], "staged c2p-only b=0")
     assert_attn_close(got[1, :, :131], want[1, :, :131], "staged c2p-only b=1")
+
+
+@pytest.mark.parametrize("log_bucket", [True, False])
+def test_fused_varlen_equals_padded_call(dev, log_bucket):
+    """flash_deberta_attention_varlen on packed [T, H, 64] rows (strided views
+    of a [T, 3, H, 64] projection) against the padded fused call with
+    seq_lengths on the same sequences: the kernel runs the same tiles in the
+    same order, so every valid row is equal bit for bit; and against the
+    oracle at the attention tolerance. Lengths 512, 1, 0, 300 and 130 cover
+    one-token and empty sequences and partial tiles."""
+    lens = [512, 1, 0, 300, 130]
+    B, H, S, L = len(lens), 4, 256, max(lens)
+    q, k, v, kr, qr, ln = _case(B, H, L, S, torch.bfloat16, 77, lens=lens)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    qkv = torch.stack([torch.cat([t[b, :, :n].transpose(0, 1) for b, n in enumerate(lens)])
+                       for t in (q, k, v)], 1)                      # [T, 3, H, 64]
+    print(f"deberta varlen log={log_bucket} lens {lens}", flush=True)
+    qd = qkv.to(dev)
+    got = _k().flash_deberta_attention_varlen(qd[:, 0], qd[:, 1], qd[:, 2], cu.to(dev), L, kr.to(dev),
+                                              qr.to(dev), SM, S, 512, log_bucket).cpu()
+    pad = _k().flash_deberta_attention_fused(q.to(dev), k.to(dev), v.to(dev), ln.to(dev), kr.to(dev),
+                                             qr.to(dev), SM, S, 512, log_bucket).cpu()
+    pk, pq = oa.deberta_position_projections(q, k, kr, qr)
+    want = oa.deberta_flash_attention(q, k, v, ln, pk, pq, SM, S, 512, log_bucket)
+    for b, n in enumerate(lens):
+        if n == 0:
+            continue
+        a = int(cu[b])
+        gb = got[a:a + n].transpose(0, 1)
+        assert torch.equal(gb, pad[b, :, :n]), f"sequence {b}"
+        assert_attn_close(gb, want[b, :, :n], f"varlen b={b}")

@@ -32,6 +32,10 @@ struct DebArgs {
   const void* qr; int64_t qrs[2];   // fused: query_rel [H, 2S, 64] (p2c) or null
   StepFn step;                      // |bucket| as a function of |d| (log mode)
   int unit;                         // c(d) moves by at most 1 per unit of d
+  // packed sequences (fused kernel; nullptr: the padded batch): "batch" b is
+  // sequence b, tokens cu[b] .. cu[b + 1] - 1 of [T, H, D] tensors (strides
+  // [.][1] = head, [.][2] = token); M = N = the longest sequence
+  const int32_t* cu;
 };
 
 __device__ inline int deb_index(const DebArgs& a, int d) {
@@ -456,12 +460,25 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
   const int q0 = qt * kBM;
   const int t = threadIdx.x, lane = t & 63, hl = lane >> 5, cl = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int len = a.seq_lengths ? min(max(a.seq_lengths[b], 0), a.N) : a.N;
+  // rows of this (batch, head) or sequence and their offsets in q, k, v, o;
+  // packed sequences have no rows past their length to write
+  int len, mrows;
+  int64_t qb, kb, vb, ob;
+  if (a.cu) {
+    const int tok0 = a.cu[b];
+    len = mrows = min(max(a.cu[b + 1] - tok0, 0), a.N);
+    qb = (int64_t)tok0 * a.qs[2]; kb = (int64_t)tok0 * a.ks[2];
+    vb = (int64_t)tok0 * a.vs[2]; ob = (int64_t)tok0 * a.os[2];
+  } else {
+    len = a.seq_lengths ? min(max(a.seq_lengths[b], 0), a.N) : a.N;
+    mrows = a.M;
+    qb = b * a.qs[0]; kb = b * a.ks[0]; vb = b * a.vs[0]; ob = b * a.os[0];
+  }
   const int qw0 = q0 + w * 32;
   const int qrow = qw0 + cl;
-  const bool qstore = qrow < a.M;
-  const bool qvalid = qrow < min(len, a.M);
-  uint16_t* orow = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1] + (int64_t)qrow * a.os[2];
+  const bool qstore = qrow < mrows;
+  const bool qvalid = qrow < min(len, mrows);
+  uint16_t* orow = reinterpret_cast<uint16_t*>(a.o) + ob + h * a.os[1] + (int64_t)qrow * a.os[2];
   if (q0 >= len) {  // every row of the tile is padding (len may be 0): zeros
     if (qstore) {
       f32x16_t z = {};
@@ -473,10 +490,10 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
   const int dmin = q0 - (kt_end * kBN - 1);
   for (int e = t; e < a.lut_len; e += 256) lut[e] = (int16_t)(2 * deb_index(a, dmin + e));
 
-  const uint16_t* Qp = reinterpret_cast<const uint16_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const uint16_t* Qp = reinterpret_cast<const uint16_t*>(a.q) + qb + h * a.qs[1];
   TileSrc ksrc, vsrc;
-  tile_src_init(ksrc, reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1], (int)a.ks[2], len);
-  tile_src_init(vsrc, reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1], (int)a.vs[2], len);
+  tile_src_init(ksrc, reinterpret_cast<const uint16_t*>(a.k) + kb + h * a.ks[1], (int)a.ks[2], len);
+  tile_src_init(vsrc, reinterpret_cast<const uint16_t*>(a.v) + vb + h * a.vs[1], (int)a.vs[2], len);
   tile_load_buf(ksrc, 0, K0);
   const int kr_rs2 = C2P ? (int)a.krs[1] * 2 : 0, qr_rs2 = P2C ? (int)a.qrs[1] * 2 : 0;
   const rsrc_t kr_r = uniform_rsrc(
@@ -493,7 +510,7 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
   VOff vo;
   k_offsets(ko);
   v_offsets(vo);
-  const bool wave_on = __builtin_amdgcn_readfirstlane((int)(qw0 < min(len, a.M))) != 0;
+  const bool wave_on = __builtin_amdgcn_readfirstlane((int)(qw0 < min(len, mrows))) != 0;
   const int lut_lane = qrow - 4 * hl - dmin;  // table index of (qrow, key0 + 4hl) is lut_lane - key0
   const int c_row = (w * 32 + cl) * kCs * 2;  // byte offset of this lane's C row
   const int pt_row = 4 * hl * kPTs * 2;       // byte offset of P^T row 4h
@@ -689,6 +706,28 @@ static int check_bhld_deb(const vfk_tensor* t, const char* name, int dtype) {
   return VFK_OK;
 }
 
+// Scale, attention span and bucket step function (max_abs: the largest
+// |i - j| the launch can meet + 1).
+static int setup_scalars(DebArgs& a, float sm_scale, int position_buckets, int max_relative_distance,
+                         int use_log_bucket, int max_abs, const char* name) {
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale))
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: sm_scale must be > 0", name);
+  a.c2 = sm_scale * VFK_LOG2E;
+  // flash_deberta_attention.py:323, :366-368
+  a.span = position_buckets > 0 ? position_buckets : max_relative_distance;
+  const int nb = position_buckets > 0 ? position_buckets : max_relative_distance * 2;
+  const int maxd = max_relative_distance > 0 ? max_relative_distance : 512;
+  a.log_bucket = use_log_bucket ? 1 : 0;
+  if (a.span <= 0) return set_error(VFK_ERR_INVALID, "%s: att_span must be > 0", name);
+  a.unit = 1;
+  if (a.log_bucket) {
+    int rc;
+    if ((rc = build_deberta_step(nb, maxd, max_abs, a.span, &a.step))) return rc;
+    a.unit = step_is_unit(a.step) ? 1 : 0;
+  }
+  return VFK_OK;
+}
+
 static int setup_common(DebArgs& a, const vfk_tensor* q, const vfk_tensor* k, const vfk_tensor* v,
                         const int32_t* seq_lengths, float sm_scale, int position_buckets,
                         int max_relative_distance, int use_log_bucket, vfk_tensor* out,
@@ -706,28 +745,14 @@ static int setup_common(DebArgs& a, const vfk_tensor* q, const vfk_tensor* k, co
     if (out->size[i] != q->size[i]) return set_error(VFK_ERR_INVALID, "%s: out must match q", name);
   if (M > 32767 || N > 32767 || B * H > (1 << 24))
     return set_error(VFK_ERR_UNSUPPORTED, "%s: sizes too large", name);
-  if (!(sm_scale > 0.f) || !isfinite(sm_scale))
-    return set_error(VFK_ERR_UNSUPPORTED, "%s: sm_scale must be > 0", name);
   a.q = q->data; a.k = k->data; a.v = v->data; a.o = out->data;
   for (int i = 0; i < 4; ++i) {
     a.qs[i] = q->stride[i]; a.ks[i] = k->stride[i]; a.vs[i] = v->stride[i]; a.os[i] = out->stride[i];
   }
   a.B = (int)B; a.H = (int)H; a.M = (int)M; a.N = (int)N;
   a.seq_lengths = seq_lengths;
-  a.c2 = sm_scale * VFK_LOG2E;
-  // flash_deberta_attention.py:323, :366-368
-  a.span = position_buckets > 0 ? position_buckets : max_relative_distance;
-  const int nb = position_buckets > 0 ? position_buckets : max_relative_distance * 2;
-  const int maxd = max_relative_distance > 0 ? max_relative_distance : 512;
-  a.log_bucket = use_log_bucket ? 1 : 0;
-  if (a.span <= 0) return set_error(VFK_ERR_INVALID, "%s: att_span must be > 0", name);
-  a.unit = 1;
-  if (a.log_bucket) {
-    const int max_abs = (int)(M > N ? M : N);
-    if ((rc = build_deberta_step(nb, maxd, max_abs, a.span, &a.step))) return rc;
-    a.unit = step_is_unit(a.step) ? 1 : 0;
-  }
-  return VFK_OK;
+  return setup_scalars(a, sm_scale, position_buckets, max_relative_distance, use_log_bucket,
+                       (int)(M > N ? M : N), name);
 }
 
 static int check_pos(const vfk_tensor* p, const char* name, const DebArgs& a, int rows, int dt) {
@@ -803,6 +828,65 @@ extern "C" int vfk_flash_deberta_fwd(const vfk_tensor* q, const vfk_tensor* k, c
   return launch_status("vfk_flash_deberta_fwd");
 }
 
+// Relative-table checks and the launch of the fused kernel (padded and
+// packed entry points).
+static int deb_fused_launch(DebArgs& a, int dt, const vfk_tensor* key_rel, const vfk_tensor* query_rel,
+                            hipStream_t st, const char* name) {
+  int rc;
+  const vfk_tensor* rel[2] = {key_rel, query_rel};
+  const char* names[2] = {"key_rel", "query_rel"};
+  for (int i = 0; i < 2; ++i) {
+    if (!present(rel[i])) continue;
+    const vfk_tensor* r = rel[i];
+    if ((rc = check_tensor(r, names[i], 3))) return rc;
+    if (r->dtype != dt) return set_error(VFK_ERR_INVALID, "%s: dtype differs from q", names[i]);
+    if (r->size[0] != a.H || r->size[1] < 2 * a.span || r->size[2] != kHD || r->stride[2] != 1)
+      return set_error(VFK_ERR_INVALID, "%s: expected [H, >= %d, 64] with unit last stride", names[i],
+                       2 * a.span);
+    if (dt != VFK_F32 && (!aligned16(r->data) || r->stride[0] % 8 || r->stride[1] % 8))
+      return set_error(VFK_ERR_INVALID, "%s: rows must be 16-byte aligned", names[i]);
+    if (i == 0) { a.kr = r->data; a.krs[0] = r->stride[0]; a.krs[1] = r->stride[1]; }
+    else { a.qr = r->data; a.qrs[0] = r->stride[0]; a.qrs[1] = r->stride[1]; }
+  }
+  if (a.B == 0 || a.H == 0 || a.M == 0) return VFK_OK;
+  if (dt == VFK_F32) {
+    const int nqt = ceil_div(a.M, 64);
+    hipLaunchKernelGGL(deberta_fused_f32_kernel, dim3((unsigned)(nqt * a.B * a.H)), dim3(64), 0, st, a);
+    return launch_status(name);
+  }
+  const int ntk = ceil_div(a.N, kBN);
+  a.lut_len = ntk * kBN + kBM;
+  const size_t dyn = (size_t)a.lut_len * 2;
+  if (kFusedStaticLds + dyn > 160 * 1024)
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: N too large", name);
+  // the table holds 2 c in int16; the K / V buffer resources span N rows
+  if (a.span > 8192)
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: att_span above 8192", name);
+  if ((a.kr && 4 * (int64_t)a.span * a.krs[1] >= ((int64_t)1 << 31)) ||
+      (a.qr && 4 * (int64_t)a.span * a.qrs[1] >= ((int64_t)1 << 31)))
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: rel tables span 2 GiB or more", name);
+  if ((int64_t)a.N * (a.ks[2] > a.vs[2] ? a.ks[2] : a.vs[2]) * 2 >= ((int64_t)1 << 31))
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: K / V rows span 2 GiB or more", name);
+  const int nqt = ceil_div(a.M, kBM);
+  dim3 grid((unsigned)(nqt * a.B * a.H));
+#define VFK_DEB_GO(E, C, P) \
+  hipLaunchKernelGGL((deberta_fused_kernel<E, C, P>), grid, dim3(256), dyn, st, a)
+  const bool c2p = a.kr != nullptr, p2c = a.qr != nullptr;
+  if (dt == VFK_BF16) {
+    if (c2p && p2c) VFK_DEB_GO(BF16, true, true);
+    else if (c2p) VFK_DEB_GO(BF16, true, false);
+    else if (p2c) VFK_DEB_GO(BF16, false, true);
+    else VFK_DEB_GO(BF16, false, false);
+  } else {
+    if (c2p && p2c) VFK_DEB_GO(F16, true, true);
+    else if (c2p) VFK_DEB_GO(F16, true, false);
+    else if (p2c) VFK_DEB_GO(F16, false, true);
+    else VFK_DEB_GO(F16, false, false);
+  }
+#undef VFK_DEB_GO
+  return launch_status(name);
+}
+
 extern "C" int vfk_deberta_fused_fwd(const vfk_tensor* q, const vfk_tensor* k, const vfk_tensor* v,
                                      const int32_t* seq_lengths, const vfk_tensor* key_rel,
                                      const vfk_tensor* query_rel, float sm_scale,
@@ -821,57 +905,58 @@ extern "C" int vfk_deberta_fused_fwd(const vfk_tensor* q, const vfk_tensor* k, c
                      "vfk_deberta_fused_fwd: position_buckets=%d / max_relative_positions=%d give "
                      "bucket steps above 1 (use flash_deberta_attention)",
                      position_buckets, max_relative_distance);
-  const vfk_tensor* rel[2] = {key_rel, query_rel};
-  const char* names[2] = {"key_rel", "query_rel"};
-  for (int i = 0; i < 2; ++i) {
-    if (!present(rel[i])) continue;
-    const vfk_tensor* r = rel[i];
-    if ((rc = check_tensor(r, names[i], 3))) return rc;
-    if (r->dtype != q->dtype) return set_error(VFK_ERR_INVALID, "%s: dtype differs from q", names[i]);
-    if (r->size[0] != a.H || r->size[1] < 2 * a.span || r->size[2] != kHD || r->stride[2] != 1)
-      return set_error(VFK_ERR_INVALID, "%s: expected [H, >= %d, 64] with unit last stride", names[i],
-                       2 * a.span);
-    if (q->dtype != VFK_F32 && (!aligned16(r->data) || r->stride[0] % 8 || r->stride[1] % 8))
-      return set_error(VFK_ERR_INVALID, "%s: rows must be 16-byte aligned", names[i]);
-    if (i == 0) { a.kr = r->data; a.krs[0] = r->stride[0]; a.krs[1] = r->stride[1]; }
-    else { a.qr = r->data; a.qrs[0] = r->stride[0]; a.qrs[1] = r->stride[1]; }
-  }
-  if (a.B == 0 || a.H == 0 || a.M == 0) return VFK_OK;
-  hipStream_t st = (hipStream_t)stream;
-  if (q->dtype == VFK_F32) {
-    const int nqt = ceil_div(a.M, 64);
-    hipLaunchKernelGGL(deberta_fused_f32_kernel, dim3((unsigned)(nqt * a.B * a.H)), dim3(64), 0, st, a);
-    return launch_status("vfk_deberta_fused_fwd");
-  }
-  const int ntk = ceil_div(a.N, kBN);
-  a.lut_len = ntk * kBN + kBM;
-  const size_t dyn = (size_t)a.lut_len * 2;
-  if (kFusedStaticLds + dyn > 160 * 1024)
-    return set_error(VFK_ERR_UNSUPPORTED, "vfk_deberta_fused_fwd: N too large");
-  // the table holds 2 c in int16; the K / V buffer resources span N rows
-  if (a.span > 8192)
-    return set_error(VFK_ERR_UNSUPPORTED, "vfk_deberta_fused_fwd: att_span above 8192");
-  if ((a.kr && 4 * (int64_t)a.span * a.krs[1] >= ((int64_t)1 << 31)) ||
-      (a.qr && 4 * (int64_t)a.span * a.qrs[1] >= ((int64_t)1 << 31)))
-    return set_error(VFK_ERR_UNSUPPORTED, "vfk_deberta_fused_fwd: rel tables span 2 GiB or more");
-  if ((int64_t)a.N * (a.ks[2] > a.vs[2] ? a.ks[2] : a.vs[2]) * 2 >= ((int64_t)1 << 31))
-    return set_error(VFK_ERR_UNSUPPORTED, "vfk_deberta_fused_fwd: K / V rows span 2 GiB or more");
-  const int nqt = ceil_div(a.M, kBM);
-  dim3 grid((unsigned)(nqt * a.B * a.H));
-#define VFK_DEB_GO(E, C, P) \
-  hipLaunchKernelGGL((deberta_fused_kernel<E, C, P>), grid, dim3(256), dyn, st, a)
-  const bool c2p = a.kr != nullptr, p2c = a.qr != nullptr;
-  if (q->dtype == VFK_BF16) {
-    if (c2p && p2c) VFK_DEB_GO(BF16, true, true);
-    else if (c2p) VFK_DEB_GO(BF16, true, false);
-    else if (p2c) VFK_DEB_GO(BF16, false, true);
-    else VFK_DEB_GO(BF16, false, false);
-  } else {
-    if (c2p && p2c) VFK_DEB_GO(F16, true, true);
-    else if (c2p) VFK_DEB_GO(F16, true, false);
-    else if (p2c) VFK_DEB_GO(F16, false, true);
-    else VFK_DEB_GO(F16, false, false);
-  }
-#undef VFK_DEB_GO
-  return launch_status("vfk_deberta_fused_fwd");
+  return deb_fused_launch(a, q->dtype, key_rel, query_rel, (hipStream_t)stream, "vfk_deberta_fused_fwd");
+}
+
+// [T, H, 64] tensor of a packed stream (token stride [0], head stride [1]).
+static int check_thd_deb(const vfk_tensor* t, const char* name, int dtype, int64_t T, int64_t H) {
+  int rc = check_tensor(t, name, 3);
+  if (rc) return rc;
+  if (t->dtype != dtype) return set_error(VFK_ERR_INVALID, "%s: dtype differs from q", name);
+  if (t->size[0] != T || t->size[1] != H)
+    return set_error(VFK_ERR_INVALID, "%s: expected [%lld, %lld, 64]", name, (long long)T, (long long)H);
+  if (t->size[2] != kHD)
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: head_dim %lld (only 64 is built)", name, (long long)t->size[2]);
+  if (t->stride[2] != 1) return set_error(VFK_ERR_INVALID, "%s: head_dim must be contiguous", name);
+  if (!aligned16(t->data) || t->stride[0] % 8 || t->stride[1] % 8)
+    return set_error(VFK_ERR_INVALID, "%s: rows must be 16-byte aligned", name);
+  return VFK_OK;
+}
+
+extern "C" int vfk_deberta_fused_varlen_fwd(const vfk_tensor* q, const vfk_tensor* k, const vfk_tensor* v,
+                                            const int32_t* cu_seqlens, int32_t num_seqs,
+                                            int32_t max_seqlen, const vfk_tensor* key_rel,
+                                            const vfk_tensor* query_rel, float sm_scale,
+                                            int32_t position_buckets, int32_t max_relative_distance,
+                                            int32_t use_log_bucket, vfk_tensor* out, void* stream) {
+  const char* name = "vfk_deberta_fused_varlen_fwd";
+  int rc = check_tensor(q, "q", 3);
+  if (rc) return rc;
+  const int dt = q->dtype;
+  if (dt != VFK_BF16 && dt != VFK_F16) return set_error(VFK_ERR_UNSUPPORTED, "%s: bf16 or fp16 only", name);
+  const int64_t T = q->size[0], H = q->size[1];
+  if ((rc = check_thd_deb(q, "q", dt, T, H)) || (rc = check_thd_deb(k, "k", dt, T, H)) ||
+      (rc = check_thd_deb(v, "v", dt, T, H)) || (rc = check_thd_deb(out, "out", dt, T, H)))
+    return rc;
+  if (!cu_seqlens) return set_error(VFK_ERR_INVALID, "%s: NULL cu_seqlens", name);
+  if (num_seqs < 0 || max_seqlen < 0 || max_seqlen > 32767 || (int64_t)num_seqs * H > (1 << 24))
+    return set_error(VFK_ERR_INVALID, "%s: bad num_seqs / max_seqlen", name);
+  DebArgs a = {};
+  a.q = q->data; a.k = k->data; a.v = v->data; a.o = out->data;
+  // [T, H, D] as the padded kernel's [., H, L, D]: head stride [1], row stride [2]
+  a.qs[1] = q->stride[1]; a.qs[2] = q->stride[0]; a.qs[3] = 1;
+  a.ks[1] = k->stride[1]; a.ks[2] = k->stride[0]; a.ks[3] = 1;
+  a.vs[1] = v->stride[1]; a.vs[2] = v->stride[0]; a.vs[3] = 1;
+  a.os[1] = out->stride[1]; a.os[2] = out->stride[0]; a.os[3] = 1;
+  a.B = num_seqs; a.H = (int)H; a.M = max_seqlen; a.N = max_seqlen;
+  a.cu = cu_seqlens;
+  if ((rc = setup_scalars(a, sm_scale, position_buckets, max_relative_distance, use_log_bucket,
+                          max_seqlen, name)))
+    return rc;
+  if (!a.unit)
+    return set_error(VFK_ERR_UNSUPPORTED,
+                     "%s: position_buckets=%d / max_relative_positions=%d give bucket steps above 1",
+                     name, position_buckets, max_relative_distance);
+  if (num_seqs == 0 || T == 0 || max_seqlen == 0) return VFK_OK;
+  return deb_fused_launch(a, dt, key_rel, query_rel, (hipStream_t)stream, name);
 }

@@ -140,6 +140,35 @@ def deberta_layer_forward(x: torch.Tensor, seq_lengths: torch.Tensor, rel: torch
                                return_sum=False)
 
 
+def deberta_layer_packed(x: torch.Tensor, cu_seqlens: torch.Tensor, max_len: int,
+                         rel: torch.Tensor, lw: DebertaLayerWeights,
+                         w: DebertaWeights) -> torch.Tensor:
+    """deberta_layer_forward on packed sequences, without padding: x [T,
+    hidden], sequence s owns rows cu_seqlens[s] .. cu_seqlens[s + 1] - 1
+    (int32 on the device), max_len >= every sequence length. The projections,
+    LayerNorms and FFN run on the T rows; the attention runs over the packed
+    sequences (flash_deberta_attention_varlen), which needs unit bucket steps
+    (`unit_steps`, true for the DeBERTa-v3 settings)."""
+    from kernels.flash_deberta_attention import flash_deberta_attention_varlen
+    T, D = x.shape
+    H = w.heads
+    d = D // H
+    span = w.position_buckets if w.position_buckets > 0 else w.max_relative_positions
+    qkv = F.linear(x, lw.wqkv, lw.bqkv).view(T, 3, H, d)
+    pr = F.linear(rel[:2 * span], lw.wqkv[:2 * D], lw.bqkv[:2 * D]).view(2 * span, 2, H, d)
+    query_rel, key_rel = pr[:, 0].transpose(0, 1), pr[:, 1].transpose(0, 1)
+    pb = w.position_buckets if w.position_buckets > 0 else span
+    log = w.position_buckets > 0
+    ctx = flash_deberta_attention_varlen(qkv[:, 0], qkv[:, 1], qkv[:, 2], cu_seqlens, max_len,
+                                         key_rel, query_rel, 1.0 / math.sqrt(3 * d), pb,
+                                         w.max_relative_positions, log)
+    h = fused_add_layernorm(F.linear(ctx.view(T, D), lw.wo, lw.bo), x, lw.ln1_w, lw.ln1_b,
+                            w.eps, return_sum=False)
+    inter = activation(F.linear(h, lw.wi, lw.bi), "gelu")
+    return fused_add_layernorm(F.linear(inter, lw.wo2, lw.bo2), h, lw.ln2_w, lw.ln2_b, w.eps,
+                               return_sum=False)
+
+
 def deberta_forward(x: torch.Tensor, seq_lengths: torch.Tensor, w: DebertaWeights,
                     num_layers: Optional[int] = None) -> torch.Tensor:
     """Encoder stack on embedding output x [B, L, hidden] -> last hidden state."""
@@ -269,10 +298,20 @@ def deberta_forward_flat(x: torch.Tensor, positions: torch.Tensor, w: DebertaWei
     GLiNER2 plugin, plugins/deberta_gliner2/model.py:124-137, runs the flat
     stream as one sequence and gets per-sequence attention from this path):
     embedding output x [T, hidden] of a packed stream whose sequences start at
-    position 0 -> last hidden state [T, hidden]. The re-padding and the
-    concatenation of valid rows run on the device (kernels.packing); the
-    number of sequences and the longest length are read back once."""
+    position 0 -> last hidden state [T, hidden]. The sequence boundaries come
+    from the positions on the device; the number of sequences and the longest
+    length are read back once. Every layer then runs on the packed rows
+    (deberta_layer_packed); bucket settings with steps above 1 re-pad into the
+    padded forward instead."""
     cu, meta = seq_metadata(positions, "zero")
     cu, n, max_len, _ = read_metadata(cu, meta)
+    pb = w.position_buckets if w.position_buckets > 0 else w.max_relative_positions
+    if unit_steps(pb, w.max_relative_positions, w.position_buckets > 0, max_len):
+        # every layer on the packed rows (varlen attention, no padding)
+        rel = deberta_rel_embeddings(w)
+        nl = len(w.layers) if num_layers is None else num_layers
+        for i in range(nl):
+            x = deberta_layer_packed(x, cu, max_len, rel, w.layers[i], w)
+        return x
     xb, lens = pad_packed(x, cu, n, max_len)
     return unpad_packed(deberta_forward(xb, lens, w, num_layers), cu, x.shape[0])

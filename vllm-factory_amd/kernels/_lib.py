@@ -50,6 +50,8 @@ _SIGNATURES = {
     "vfk_flash_rpb_varlen_fwd": [_P, _P, _P, _vp, _i32, _i32, _P, _i32, _i32, _i32, _f32, _P, _vp],
     "vfk_flash_deberta_fwd": [_P, _P, _P, _vp, _P, _P, _i32, _f32, _i32, _i32, _i32, _P, _vp],
     "vfk_deberta_fused_fwd": [_P, _P, _P, _vp, _P, _P, _f32, _i32, _i32, _i32, _P, _vp],
+    "vfk_deberta_fused_varlen_fwd": [_P, _P, _P, _vp, _i32, _i32, _P, _P, _f32, _i32, _i32, _i32, _P,
+                                     _vp],
     "vfk_varlen_attn_fwd": [_P, _P, _P, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _i64,
                             _P, _vp],
     "vfk_varlen_attn_workspace_bytes": [_i32, _i64, _i32, _i32, _i32, _i32],

@@ -142,5 +142,51 @@ def flash_deberta_attention_fused(
     return out
 
 
-__all__ = ["flash_deberta_attention", "flash_deberta_attention_fused", "unit_steps",
+def flash_deberta_attention_varlen(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    max_seqlen: int,
+    key_rel: Optional[torch.Tensor],
+    query_rel: Optional[torch.Tensor],
+    sm_scale: float,
+    position_buckets: int = 256,
+    max_relative_distance: int = 512,
+    use_log_bucket: bool = True,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """flash_deberta_attention_fused over packed sequences, without padding.
+
+    q, k, v [T, H, 64] (bf16 / fp16, any token and head strides with a
+    contiguous last dim); sequence s is rows cu_seqlens[s] .. cu_seqlens[s+1]
+    - 1 (int32 on the device) and attends to its own rows only, relative
+    positions counted inside the sequence: the padded call with seq_lengths
+    on the valid rows. max_seqlen must be >= every sequence length; bucket
+    steps must be unit (`unit_steps`). Returns [T, H, 64] (or writes `out`)."""
+    dev = _lib.require_gpu(q, k, v, cu_seqlens, key_rel, query_rel)
+    if q.dim() != 3 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("q, k, v must be [T, H, D] of one shape")
+    qq, kk, vv = (_lib.rows_aligned(t) for t in (q, k, v))
+    kr = _lib.rows_aligned(key_rel.to(q.dtype)) if key_rel is not None else None
+    qr = _lib.rows_aligned(query_rel.to(q.dtype)) if query_rel is not None else None
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    elif (out.shape != q.shape or out.dtype != q.dtype or out.device != q.device
+          or _lib.rows_aligned(out) is not out):
+        raise ValueError("out must match q's shape, dtype and device, with contiguous 16-byte rows")
+    cu = cu_seqlens.to(torch.int32).contiguous()
+    _lib.on_device(
+        "vfk_deberta_fused_varlen_fwd", dev,
+        _lib.ref(_lib.desc(qq)), _lib.ref(_lib.desc(kk)), _lib.ref(_lib.desc(vv)),
+        cu.data_ptr(), int(cu.numel() - 1), int(max_seqlen),
+        _lib.ref(_lib.desc(kr)), _lib.ref(_lib.desc(qr)), float(sm_scale),
+        int(position_buckets), int(max_relative_distance), int(bool(use_log_bucket)),
+        _lib.ref(_lib.desc(out)),
+    )
+    return out
+
+
+__all__ = ["flash_deberta_attention", "flash_deberta_attention_fused",
+           "flash_deberta_attention_varlen", "unit_steps",
            "clear_config_cache", "HAS_TRITON"]
