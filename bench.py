@@ -450,6 +450,43 @@ def encoder_config5(torch, args):
                 note="wall clock per forward (embeddings to final LayerNorm), GEMMs via torch/hipBLASLt")
 
 
+def glu_linear_config5(torch, args):
+    """ModernBERT-base MLP projection over the 256-sequence pack (x [163 736,
+    768] bf16, Wi [2304, 768]): the fused GLU projection (vfk_glu_linear_fwd,
+    act(x W_in^T) * (x W_gate^T) in one MFMA kernel) against the unfused path
+    (hipBLASLt F.linear, then the GELU-gate kernel) and the plain GEMM."""
+    import torch.nn.functional as F
+    from kernels.fused_glu_mlp import fused_gelu_mul_dropout, glu_linear
+
+    dev = torch.device("cuda:0")
+    M, K, I = 163736, 768, 1152
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(2 * I, K, device=dev, generator=g) * 0.036).to(torch.bfloat16)
+    out = torch.empty(M, I, device=dev, dtype=torch.bfloat16)
+    fused = lambda: glu_linear(x, w, "gelu", out=out)
+
+    def unfused():
+        y = F.linear(x, w)
+        return fused_gelu_mul_dropout(y[:, :I], y[:, I:], "gelu")
+
+    gemm = lambda: F.linear(x, w)
+    # interleaved rounds, best of 3 per path: the first kernels of a process
+    # run before the clock has settled
+    res = {}
+    for _ in range(3):
+        for name, fn in (("fused", fused), ("unfused", unfused), ("gemm_only", gemm)):
+            for _ in range(args.warmup):
+                fn()
+            ms = device_ms(torch, fn, args.steps)
+            res[name] = min(res.get(name, ms), ms)
+    flop = 2.0 * M * K * 2 * I
+    return dict(fused_ms=res["fused"], unfused_ms=res["unfused"], hipblaslt_gemm_ms=res["gemm_only"],
+                gflop=flop / 1e9, fused_tflops=flop / (res["fused"] * 1e-3) / 1e12,
+                fused_frac=flop / (res["fused"] * 1e-3) / 2.5e15,
+                note="fused: one kernel writes [M, 1152]; unfused: [M, 2304] projection + GELU-gate pass")
+
+
 def mt5_layer_config4(torch, args):
     """One mT5-large encoder layer (RMSNorm, RPB attention, gated-GELU FFN) at
     config 4 (B=32, L=768, lengths U{512..768}); tokens/s over valid tokens."""
@@ -468,17 +505,21 @@ def mt5_layer_config4(torch, args):
     wqkv = torch.cat((c.wq, c.wk, c.wv), 1)
     L = c.hidden.shape[1]
     fp = lambda: mt5_layer_packed(xf, cu, L, *ws, c.mask, wqkv=wqkv)
+    from encoders.mt5 import stack_glu_weight
+    wg = stack_glu_weight(c.wi0, c.wi1)
+    ff = lambda: mt5_layer_packed(xf, cu, L, *ws, c.mask, wqkv=wqkv, wi_glu=wg)
     res = {}
-    for name, f in (("padded", fn), ("packed", fp)):
+    for name, f in (("padded", fn), ("packed", fp), ("packed_glu", ff)):
         for _ in range(args.warmup):
             f()
         res[name] = device_ms(torch, f, args.steps)
-    ms = res["packed"]
+    ms = res["packed_glu"]
     return dict(ms_per_layer=ms, valid_tokens_per_s=tv / (ms * 1e-3), valid_tokens=tv,
                 padded_tokens=int(c.hidden.shape[0] * c.hidden.shape[1]),
-                padded_layer_ms=res["padded"],
-                note="ms_per_layer: the layer on the packed valid rows (mt5_layer_packed); "
-                     "padded_layer_ms: the same layer over the padded batch")
+                padded_layer_ms=res["padded"], packed_unfused_ff_ms=res["packed"],
+                note="ms_per_layer: the layer on the packed valid rows (mt5_layer_packed) with the "
+                     "gated FF as one GLU projection kernel; packed_unfused_ff_ms: the same with "
+                     "two GEMMs + the gelu_new gate pass; padded_layer_ms: the padded batch")
 
 
 def deberta_layer_config3(torch, args):
@@ -614,6 +655,7 @@ def main():
     sections = (("rpb", "rpb_mt5_large_config4", lambda: rpb_config4(torch, args)),
                 ("deberta", "deberta_v3_large_config3", lambda: deberta_config3(torch, args)),
                 ("epilogues", "epilogues", lambda: epilogue_bench(torch, args, c2)),
+                ("glu_linear", "glu_linear_modernbert_config5", lambda: glu_linear_config5(torch, args)),
                 ("mt5_layer", "mt5_large_layer_config4", lambda: mt5_layer_config4(torch, args)),
                 ("deberta_layer", "deberta_v3_large_layer_config3",
                  lambda: deberta_layer_config3(torch, args)),

@@ -448,6 +448,18 @@ int vfk_rmsnorm_fwd(const vfk_tensor* x, const vfk_tensor* residual,
 int vfk_glu_fwd(int32_t act, const vfk_tensor* a, const vfk_tensor* b,
                 vfk_tensor* out, void* stream);
 
+/* GLU projection with the activation and gate product fused into the GEMM:
+ * out[t, f] = act(x[t] . w[f]) * (x[t] . w[I + f]), x [M, K], w [2I, K]
+ * (activation-input rows, then gate rows), out [M, I]; fp32 accumulation,
+ * the [M, 2I] projection is never written. Replaces the Wi projection plus
+ * chunk / act / gate product of models/modernbert/modernbert_encoder.py:157-178
+ * (ModernBertMLP.forward up to Wo) and the T5 gated FF's wi_0 / wi_1 products
+ * (models/mt5/mt5_encoder.py T5DenseGatedActDense); kernels/fused_glu_mlp.py:61-104
+ * is the elementwise part. bf16 / fp16; rows contiguous and 16-byte aligned;
+ * K a multiple of 64, I a multiple of 8. */
+int vfk_glu_linear_fwd(int32_t act, const vfk_tensor* x, const vfk_tensor* w,
+                       vfk_tensor* out, void* stream);
+
 /* Activation out = act(x) over [rows, n] (row strides). Replaces the
  * intermediate activation of models/deberta_v2/deberta_v2_encoder.py:535-550
  * (DebertaV2Intermediate, ACT2FN[hidden_act]) in inference. */

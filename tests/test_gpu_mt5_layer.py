@@ -130,3 +130,30 @@ def test_mt5_layer_packed_matches_oracle_and_padded_layer():
         print(f"packed row {b} (len {n}): max-abs {err:.3e} cosine {cs:.6f}; vs padded {dp:.3e}")
         assert err <= 6e-2 and cs >= 0.9999, (b, err, cs)
         assert dp <= 2 * 2.0 ** -7 * pad[a:e].abs().max().item(), (b, dp)
+
+
+def test_mt5_layer_packed_fused_glu_matches_oracle():
+    """mt5_layer_packed with the gated FF as one GLU projection kernel
+    (wi_glu = stack_glu_weight(wi0, wi1)) against the fp32 oracle layer, same
+    bound as the unfused packed layer."""
+    from encoders.mt5 import mt5_layer_packed, stack_glu_weight
+    from kernels.packing import unpad_packed
+    from oracle import encoders as oe
+    c = workloads.config4(batch=3)
+    dev = torch.device("cuda:0")
+    ws = (c.wq, c.wk, c.wv, c.wo, c.wi0, c.wi1, c.wff_o, c.ln1, c.ln2, c.table)
+    wd = tuple(w.to(dev) for w in ws)
+    lens = c.lengths.tolist()
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    L = c.hidden.shape[1]
+    xf = unpad_packed(c.hidden.to(dev), cu, int(cu[-1]))
+    wg = stack_glu_weight(wd[4], wd[5])
+    assert wg is not None and wg.shape == (2 * c.wi0.shape[1], c.wi0.shape[0])
+    got = mt5_layer_packed(xf, cu, L, *wd, None, wi_glu=wg).float().cpu()
+    want = oe.mt5_layer(c.hidden, *ws, c.mask)
+    for b, n in enumerate(lens):
+        a, e = int(cu[b]), int(cu[b + 1])
+        err = (got[a:e] - want[b, :n]).abs().max().item()
+        cs = cosine(got[a:e], want[b, :n])
+        print(f"fused-FF packed row {b} (len {n}): max-abs {err:.3e} cosine {cs:.6f}")
+        assert err <= 6e-2 and cs >= 0.9999, (b, err, cs)

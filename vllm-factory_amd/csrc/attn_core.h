@@ -405,6 +405,17 @@ __device__ inline void tile_load_buf(const TileSrc& s, int row0, uint16_t* tile)
                                              s.vo[j], soff, 0, 0);
 }
 
+// Buffer resource over nbytes from base, built from readfirstlane'd words:
+// the values are uniform, and saying so keeps the compiler from wrapping each
+// load through it in a loop over distinct resource values.
+__device__ inline rsrc_t uniform_rsrc(const void* base, int nbytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  void* ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, 0, __builtin_amdgcn_readfirstlane(nbytes), kRsrcWord3);
+}
+
 // Waits for this wave's outstanding loads and LDS traffic, then joins the
 // workgroup barrier: afterwards every direct-loaded tile is visible.
 __device__ inline void tile_barrier() {

@@ -388,17 +388,6 @@ constexpr int kPTElems = kBN * kPTs;
 constexpr int kCElems = 32 * kCs;       // per wave
 constexpr int kFusedStaticLds = (3 * kTileElems + kPTElems + 4 * kCElems) * 2;
 
-// Buffer resource over nbytes from base, built from readfirstlane'd words:
-// the values are uniform, and saying so keeps the compiler from wrapping each
-// load through it in a loop over distinct resource values.
-__device__ inline rsrc_t uniform_rsrc(const void* base, int nbytes) {
-  const uint64_t p = reinterpret_cast<uint64_t>(base);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
-  void* ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(ub, 0, __builtin_amdgcn_readfirstlane(nbytes), kRsrcWord3);
-}
-
 // Rel-table MFMA operand through a buffer resource over the table's 2S rows
 // (rows past the table read as zeros; their products are never used): lane
 // byte offset voff = row-in-block * rs2 + 16 h, block row offset in soff.

@@ -4,6 +4,8 @@ Follows models/modernbert/modernbert_encoder.py (embeddings :102-128, layer
 :289-352, model :430-480): tok_embeddings -> LayerNorm; 22 x [attn_norm
 (Identity in layer 0) -> Wqkv -> RoPE attention -> Wo -> + residual ->
 mlp_norm -> Wi -> GELU(input) * gate -> Wo -> + residual]; final LayerNorm.
+The Wi projection and the GELU gate run as one kernel (glu_linear), which
+rounds the GLU output once where the reference rounds the projection first.
 Global layers (layer_id % 3 == 0) attend inside each sequence with RoPE theta
 160000, local layers within |i - j| <= 64 with theta 10000; tokens with id
 50284 are hidden as keys (:456-460).
@@ -25,7 +27,7 @@ import torch
 import torch.nn.functional as F
 
 from kernels.colbert_head import colbert_head
-from kernels.fused_glu_mlp import fused_gelu_mul_dropout
+from kernels.fused_glu_mlp import fused_gelu_mul_dropout, glu_linear
 from kernels.fused_layernorm import fused_add_layernorm, fused_layernorm
 from kernels.varlen_attention import varlen_from_positions, varlen_rope_attention
 
@@ -86,6 +88,13 @@ def random_weights(num_layers: int = 22, hidden: int = 768, heads: int = 12, int
                              ones.clone())
 
 
+def _glu_fusable(wi: torch.Tensor, h: torch.Tensor) -> bool:
+    """Whether the Wi projection and GELU gate run as one kernel (glu_linear:
+    16-bit weights, hidden a multiple of 64, intermediate of 8)."""
+    return (wi.dtype in (torch.bfloat16, torch.float16) and h.dtype == wi.dtype
+            and wi.shape[1] % 64 == 0 and (wi.shape[0] // 2) % 8 == 0)
+
+
 def _encode(ids: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int, w: ModernBertWeights,
             num_layers: Optional[int]):
     """Embeddings and layers; returns (pending MLP output or None, residual
@@ -110,8 +119,11 @@ def _encode(ids: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int, w: Mod
                                     1.0 / math.sqrt(d), key_valid)
         o = F.linear(att.view(T, w.hidden), lw.wo)
         h, x = fused_add_layernorm(o, x, lw.mlp_norm, None, w.eps)
-        y = F.linear(h, lw.wi)
-        g = fused_gelu_mul_dropout(y[:, :w.inter], y[:, w.inter:], "gelu")
+        if _glu_fusable(lw.wi, h):
+            g = glu_linear(h, lw.wi, "gelu")
+        else:
+            y = F.linear(h, lw.wi)
+            g = fused_gelu_mul_dropout(y[:, :w.inter], y[:, w.inter:], "gelu")
         pending = F.linear(g, lw.wo_mlp)
     return pending, x
 

@@ -21,6 +21,7 @@ from typing import Optional
 import torch
 
 from kernels.ff_fused import fused_gelu_mul_dropout
+from kernels.fused_glu_mlp import glu_linear
 from kernels.flash_attention_rpb import flash_attention_rpb_final
 from kernels.rms_norm import fused_add_rms_norm, rms_norm
 
@@ -45,7 +46,8 @@ def mt5_layer_forward(x: torch.Tensor, wq, wk, wv, wo, wi0, wi1, wff_o, ln1, ln2
 
 def mt5_layer_packed(x: torch.Tensor, cu_seqlens: torch.Tensor, max_len: int, wq, wk, wv, wo,
                      wi0, wi1, wff_o, ln1, ln2, table, mask=None, num_buckets: int = 32,
-                     max_distance: int = 128, eps: float = 1e-6, wqkv=None) -> torch.Tensor:
+                     max_distance: int = 128, eps: float = 1e-6, wqkv=None,
+                     wi_glu=None) -> torch.Tensor:
     """The layer of mt5_layer_forward on packed sequences, without padding.
 
     x [T, d_model]: sequence s owns rows cu_seqlens[s] .. cu_seqlens[s + 1] -
@@ -56,7 +58,11 @@ def mt5_layer_packed(x: torch.Tensor, cu_seqlens: torch.Tensor, max_len: int, wq
     reference's key mask does on its valid rows), the output projection, FFN
     and residual adds. mask is accepted for the padded layer's signature and
     not used. wqkv: the [D, 3D] concatenation of wq, wk, wv when the caller
-    keeps one (built here otherwise)."""
+    keeps one (built here otherwise). wi_glu: wi0 and wi1 stacked as the
+    [2 d_ff, D] rows of one GLU projection (stack_glu_weight); given, the
+    gated FF's two projections and gelu_new gate run as one kernel
+    (glu_linear), which rounds the gate product once where the reference
+    rounds both projections first."""
     from kernels.flash_attention_rpb import flash_attention_rpb_varlen
     T, D = x.shape
     H = table.shape[1]
@@ -69,8 +75,21 @@ def mt5_layer_packed(x: torch.Tensor, cu_seqlens: torch.Tensor, max_len: int, wq
                                      num_buckets, max_distance, False, 1.0)
     o = att.view(T, D) @ wo
     h2, x1 = fused_add_rms_norm(o, x, ln2, eps)
-    g = fused_gelu_mul_dropout(h2 @ wi0, h2 @ wi1, "gelu_new")
+    if wi_glu is not None:
+        g = glu_linear(h2, wi_glu, "gelu_new")
+    else:
+        g = fused_gelu_mul_dropout(h2 @ wi0, h2 @ wi1, "gelu_new")
     return torch.addmm(x1, g, wff_o)
+
+
+def stack_glu_weight(wi0: torch.Tensor, wi1: torch.Tensor) -> Optional[torch.Tensor]:
+    """[D, d_ff] wi0, wi1 ([in, out]) -> the [2 d_ff, D] weight of glu_linear,
+    or None where glu_linear does not take the shapes (D a multiple of 64,
+    d_ff of 8, 16-bit weights)."""
+    D, F_ = wi0.shape
+    if D % 64 or F_ % 8 or wi0.dtype not in (torch.bfloat16, torch.float16):
+        return None
+    return torch.cat((wi0.t(), wi1.t()), 0).contiguous()
 
 
 def mt5_encoder_forward(input_ids: Optional[torch.Tensor], attention_mask: Optional[torch.Tensor],
@@ -105,7 +124,7 @@ def mt5_encoder_forward(input_ids: Optional[torch.Tensor], attention_mask: Optio
         xf = unpad_packed(x, cu, T)
         for lw in layers:
             xf = mt5_layer_packed(xf, cu, L, *lw, table, None, num_buckets, max_distance, eps,
-                                  wqkv=torch.cat(lw[:3], 1))
+                                  wqkv=torch.cat(lw[:3], 1), wi_glu=stack_glu_weight(lw[4], lw[5]))
         x, _ = pad_packed(rms_norm(xf, final_ln, eps), cu, B, L)
         return x.squeeze(0) if squeeze else x
     for lw in layers:
@@ -147,5 +166,5 @@ def mt5_encoder_flat(x: torch.Tensor, positions: torch.Tensor, layers, table: to
     cu, n, max_len, _ = read_metadata(cu, meta)
     for lw in layers:
         x = mt5_layer_packed(x, cu, max_len, *lw, table, None, num_buckets, max_distance, eps,
-                             wqkv=torch.cat(lw[:3], 1))
+                             wqkv=torch.cat(lw[:3], 1), wi_glu=stack_glu_weight(lw[4], lw[5]))
     return x

@@ -75,6 +75,7 @@ _SIGNATURES = {
     "vfk_layernorm_fwd": [_P, _P, _P, _P, _f32, _P, _P, _vp],
     "vfk_rmsnorm_fwd": [_P, _P, _P, _f32, _P, _P, _vp],
     "vfk_glu_fwd": [_i32, _P, _P, _P, _vp],
+    "vfk_glu_linear_fwd": [_i32, _P, _P, _P, _vp],
     "vfk_act_fwd": [_i32, _P, _P, _vp],
     "vfk_residual_add": [_P, _P, _P, _vp],
     "vfk_colbert_head_fwd": [_P, _P, _P, _P, _f32, _P, _P, _P, _P, _vp],
