@@ -174,3 +174,23 @@ def test_varlen_bound_fallback_and_fast_waves(dev, window):
     got = _vl()(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), max(lengths), window, 160000.0, 0.125,
                 key_valid=key_valid.to(dev))
     assert_attn_close(got, want, f"bound fallback w={window}")
+
+
+@pytest.mark.parametrize("window", [64, 5])
+@pytest.mark.parametrize("masked", [False, True])
+def test_local_many_sequences(dev, window, masked):
+    """Sliding-window attention over a pack of 160 sequences (lengths 1..700,
+    among them 1, 129 and 700 rows): every sequence is checked against the
+    oracle, with and without a key_valid mask."""
+    g = torch.Generator().manual_seed(40 + window)
+    lengths = torch.randint(1, 701, (160,), generator=g).tolist()
+    lengths[:4] = [1, 700, 129, 384]
+    qkv, cu = _pack(lengths, torch.bfloat16, 41)
+    T = qkv.shape[0]
+    key_valid = (torch.rand(T, generator=g) > 0.1) if masked else None
+    q, k, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
+    want = oa.varlen_attention(q, k, v, cu, window, 10000.0, key_valid, 0.125)
+    qd = qkv.to(dev)
+    got = _vl()(qd[:, 0], qd[:, 1], qd[:, 2], cu.to(dev), max(lengths), window, 10000.0, 0.125,
+                key_valid=None if key_valid is None else key_valid.to(dev))
+    assert_attn_close(got, want, f"local pack w={window} masked={masked}")
