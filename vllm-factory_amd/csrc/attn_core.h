@@ -277,6 +277,16 @@ __device__ inline void add_by_key(f32x16_t& s0, f32x16_t& s1, const float* __res
   }
 }
 
+// Score element e of the accumulator pair := tab[x_key(e, 0)] (tab already
+// offset by the lane's 4*h), the form of add_by_key that initialises.
+__device__ inline void load_by_key(f32x16_t& s0, f32x16_t& s1, const float* __restrict__ tab) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    s0[e] = tab[x_key(e, 0)];
+    s1[e] = tab[x_key(e + 16, 0)];
+  }
+}
+
 // Writes this lane's normalised output row (query c) for d in the O^T layout.
 // Rows with no visible key (l == 0) are written as zeros.
 template <typename E>
@@ -423,14 +433,16 @@ __device__ inline void tile_barrier() {
   __syncthreads();
 }
 
-// Lane offsets are kept in bytes and passed through an empty asm at each use
-// so that the compiler adds the (constant) LDS buffer address in the
-// instruction's offset field instead of keeping one address register per
-// buffer live across the loop.
+// Lane offsets are kept in bytes and passed through an empty asm so that the
+// compiler adds the (constant) LDS buffer address in the instruction's offset
+// field instead of keeping one address register per buffer live across the
+// loop. lds_opaque returns an opaque copy (one move per use); lds_refresh
+// makes a loop-carried offset opaque in place, once per step, with no move.
 __device__ inline int lds_opaque(int x) {
   asm volatile("" : "+v"(x));
   return x;
 }
+__device__ inline void lds_refresh(int& x) { asm volatile("" : "+v"(x)); }
 template <typename T>
 __device__ inline T lds_at(const uint16_t* base, int byte_off) {
   return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + byte_off);
@@ -440,6 +452,10 @@ __device__ inline T lds_at(const uint16_t* base, int byte_off) {
 // (+32 for the second key block, +4096 bytes), chunk 2*ds + h.
 struct KOff {
   int o[4];
+  __device__ void refresh() {
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) lds_refresh(o[ds]);
+  }
 };
 __device__ inline void k_offsets(KOff& k) {
   const int l = threadIdx.x & 63, c = l & 31, h = l >> 5;
@@ -454,9 +470,8 @@ __device__ inline void qk_tile_sw(const uint16_t* __restrict__ Kt, const KOff& k
   u32x4_t a0[4], a1[4];
 #pragma unroll
   for (int ds = 0; ds < 4; ++ds) {
-    const int off = lds_opaque(ko.o[ds]);
-    a0[ds] = lds_at<u32x4_t>(Kt, off);
-    a1[ds] = lds_at<u32x4_t>(Kt, off + 4096);
+    a0[ds] = lds_at<u32x4_t>(Kt, ko.o[ds]);
+    a1[ds] = lds_at<u32x4_t>(Kt, ko.o[ds] + 4096);
   }
   // keys 0-31 first, so their softmax can start while keys 32-63 multiply
   const f32x16_t z = {};
@@ -468,12 +483,36 @@ __device__ inline void qk_tile_sw(const uint16_t* __restrict__ Kt, const KOff& k
   for (int ds = 1; ds < 4; ++ds) s1 = E::mfma32(a1[ds], q[ds], s1);
 }
 
+// As qk_tile_sw, accumulating onto s0 / s1, which hold an additive bias of
+// the tile's scores on entry (the bias rides on the MFMAs' accumulator input
+// instead of costing one add per score).
+template <typename E>
+__device__ inline void qk_tile_acc(const uint16_t* __restrict__ Kt, const KOff& ko,
+                                   const u32x4_t (&q)[4], f32x16_t& s0, f32x16_t& s1) {
+  u32x4_t a0[4], a1[4];
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds) {
+    a0[ds] = lds_at<u32x4_t>(Kt, ko.o[ds]);
+    a1[ds] = lds_at<u32x4_t>(Kt, ko.o[ds] + 4096);
+  }
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds) s0 = E::mfma32(a0[ds], q[ds], s0);
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds) s1 = E::mfma32(a1[ds], q[ds], s1);
+}
+
 // Byte offsets of the transposed V reads: for 16-key step ks (+2048 bytes), d
 // block db and key half hf (keys 16ks + 8hf + 4h + v, v = source-lane row),
 // the lane addresses row 16ks + 8hf + 4h + v, columns d0 + 4r of its 16-lane
 // group.
 struct VOff {
   int o[2][2];  // [db][hf]
+  __device__ void refresh() {
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) lds_refresh(o[db][hf]);
+  }
 };
 __device__ inline void v_offsets(VOff& v) {
   const int l = threadIdx.x & 63;
@@ -501,11 +540,7 @@ __device__ inline s16x4_t lds_tr16(const uint16_t* base, int byte_off) {
 template <typename E>
 __device__ inline void pv_tile_sw(const uint16_t* __restrict__ Vt, const VOff& vo,
                                   const u32x4_t (&p)[4], f32x16_t& o0, f32x16_t& o1) {
-  int off[2][2];
-#pragma unroll
-  for (int db = 0; db < 2; ++db)
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) off[db][hf] = lds_opaque(vo.o[db][hf]);
+  const auto& off = vo.o;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     u32x4_t a[2];
@@ -538,8 +573,13 @@ __device__ inline void pv_tile_sw(const uint16_t* __restrict__ Vt, const VOff& v
 //   bool wave_active()                  the wave has a valid query row
 //   static constexpr bool kAllActive    every tile is active for such waves
 //   bool active(int i)                  the wave computes tile i
-//   bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot)   bias / masks;
-//                                       returns "exact" for softmax_exp
+//   bool init(f32x16_t& s0, f32x16_t& s1, int i, int slot)   writes an additive
+//                                       bias of tile i's scores into s0 / s1
+//                                       (the QK MFMAs accumulate onto it), or
+//                                       returns false (zero bias, s0 / s1
+//                                       untouched)
+//   bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot)   further bias /
+//                                       masks; returns "exact" for softmax_exp
 // ---------------------------------------------------------------------------
 
 // Issues the loads and metadata of tiles 0 and 1; call before the Q set-up so
@@ -575,6 +615,8 @@ __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t*
   tile_barrier();
   auto step = [&](int i, uint16_t* __restrict__ Kc, uint16_t* __restrict__ Vc,
                   uint16_t* __restrict__ Kn, uint16_t* __restrict__ Vn, int b) {
+    ko.refresh();
+    vo.refresh();
     // tile 1's K and meta were issued with tile 0; the next tile's metadata is
     // loaded before its DMA and written to LDS after this tile's compute
     const bool meta_next = i + 1 < n && i > 0;
@@ -585,7 +627,10 @@ __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t*
     }
     if (wave_on && (P::kAllActive || __builtin_amdgcn_readfirstlane((int)pol.active(i)) != 0)) {
       f32x16_t s0, s1;
-      qk_tile_sw<E>(Kc, ko, qf, s0, s1);
+      if (pol.init(s0, s1, i, b))
+        qk_tile_acc<E>(Kc, ko, qf, s0, s1);
+      else
+        qk_tile_sw<E>(Kc, ko, qf, s0, s1);
       const bool exact = pol.modify(s0, s1, i, b);
       u32x4_t p[4];
       if (FIXED)

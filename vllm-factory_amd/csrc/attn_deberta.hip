@@ -539,6 +539,8 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
   if (C2P && wave_on) c_prefetch(0);
 
   auto step = [&](int i, const uint16_t* __restrict__ Kc, uint16_t* __restrict__ Kn) {
+    ko.refresh();
+    vo.refresh();
     const int key0 = i * kBN;
     tile_load_buf(vsrc, key0, Vs);
     const int wlo = __builtin_amdgcn_readfirstlane(lut[q0 - key0 - 63 - dmin]) >> 1;
@@ -553,7 +555,7 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
       for (int kb = 0; kb < 2; ++kb) {
         u32x4_t kf[4];
 #pragma unroll
-        for (int ds = 0; ds < 4; ++ds) kf[ds] = lds_at<u32x4_t>(Kc, lds_opaque(ko.o[ds]) + kb * 4096);
+        for (int ds = 0; ds < 4; ++ds) kf[ds] = lds_at<u32x4_t>(Kc, ko.o[ds] + kb * 4096);
         f32x16_t acc0 = {}, acc1 = {};
 #pragma unroll
         for (int ds = 0; ds < 4; ++ds) {

@@ -75,6 +75,7 @@ struct RpbPolicy {
   const int* tiles;      // live key tiles (MASK_KEY) or nullptr = all in order
   const int* tflag;      // MASK_KEY: per key tile, bit0 = some nonzero mask
   float* maskt;          // MASK_KEY: [2][kBN] mask values of the tile in slot i & 1
+  const float* tailm;    // [kBN]: 0 / -inf per key of the partial last key tile
   const float* lut;      // bias per relative position (raw score units) or nullptr
   int lut_base, b, h, t, hl, qrow, wq_lo, wq_hi;
   int Lq, Lk;            // query / key rows of this (batch, head) or sequence
@@ -102,6 +103,12 @@ struct RpbPolicy {
     if (wq_lo >= Lq) return false;
     return !CAUSAL || key0(i) <= wq_hi;
   }
+  // the relative-position bias enters as the QK MFMAs' accumulator input
+  __device__ bool init(f32x16_t& s0, f32x16_t& s1, int i, int) const {
+    if (!lut || (MASK == MASK_KEY && nolive)) return false;
+    load_by_key(s0, s1, lut + key0(i) + lut_base);
+    return true;
+  }
   __device__ bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot) const {
     const int k0 = key0(i);
     bool exact = false;
@@ -111,7 +118,6 @@ struct RpbPolicy {
       s0 = f32x16_t{};
       s1 = f32x16_t{};
     } else {
-      if (lut) add_by_key(s0, s1, lut + k0 + lut_base);
       // masked keys (-1e30) fall far below the row max of the live keys:
       // the fma exponent form underflows them to 0 without an exact path
       if (MASK == MASK_KEY && (tflag[tile(i)] & 1)) add_by_key(s0, s1, maskt + slot * kBN + 4 * hl);
@@ -128,7 +134,9 @@ struct RpbPolicy {
       }
       exact = true;
     }
-    if (k0 + kBN > Lk || (CAUSAL && k0 + kBN - 1 > wq_lo)) {
+    if (!CAUSAL) {
+      if (k0 + kBN > Lk) add_by_key(s0, s1, tailm + 4 * hl);
+    } else if (k0 + kBN > Lk || k0 + kBN - 1 > wq_lo) {
       map_scores(s0, s1, [&](int e, float v) {
         const int j = k0 + x_key(e, hl);
         return (j >= Lk || (CAUSAL && j > qrow)) ? -INFINITY : v;
@@ -145,6 +153,7 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   __shared__ __align__(16) uint16_t V0[kTileElems];
   __shared__ __align__(16) uint16_t V1[kTileElems];
   __shared__ float maskt[MASK == MASK_KEY ? 2 * kBN : 1];
+  __shared__ float tailm[kBN];
   __shared__ int ntl;
   __shared__ int nolive_s;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -175,6 +184,9 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   int* tiles = tflag + nt4_lds;               // [nt4]
   float* lut = reinterpret_cast<float*>(tiles + nt4_lds);
   (void)nt4;
+
+  // keys past Lk in the partial last tile (read before the first barrier)
+  if (t < kBN) tailm[t] = ((Lk - 1) / kBN) * kBN + t < Lk ? 0.f : -INFINITY;
 
   // ---- bias table over rel = key - query, rel in [-(q0+127), Lk-1-q0] ----
   // the step thresholds and the head's table column go to LDS first, so each
@@ -260,6 +272,7 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   pol.tiles = (MASK == MASK_KEY && !direct) ? tiles : nullptr;
   pol.tflag = tflag;
   pol.maskt = maskt;
+  pol.tailm = tailm;
   pol.lut = has_table ? lut : nullptr;
   pol.nolive = MASK == MASK_KEY && nolive_s != 0;
   pol.b = b; pol.h = h; pol.t = t; pol.hl = hl;

@@ -179,17 +179,35 @@ struct VarlenPolicy {
     const int k0 = key0(i);
     return k0 <= wq_hi + window && k0 + kBN - 1 >= wq_lo - window;
   }
-  __device__ bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot) const {
-    if (KVALID) {
-      if (kflag[slot]) add_by_key(s0, s1, kmask + slot * kBN + 4 * hl);
-    } else if (key0(i) == tail0) {
-      add_by_key(s0, s1, kmask + 4 * hl);
+  // the tile cuts through the sliding window of some row of the wave
+  __device__ bool pen_tile(int k0) const {
+    return LOCAL && (wq_hi - k0 > window || k0 + kBN - 1 - wq_lo > window);
+  }
+  // 0 / -inf per key of tile i (key_valid, or the partial last tile), or null
+  __device__ const float* key_tab(int i, int slot) const {
+    if (KVALID) return kflag[slot] ? kmask + slot * kBN + 4 * hl : nullptr;
+    return key0(i) == tail0 ? kmask + 4 * hl : nullptr;
+  }
+  // one of the tile's additive terms (window penalty, else the key mask)
+  // enters as the QK MFMAs' accumulator input; modify adds the other
+  __device__ bool init(f32x16_t& s0, f32x16_t& s1, int i, int slot) const {
+    const int k0 = key0(i);
+    if (pen_tile(k0)) {
+      // entry kPenOff + key - qrow, key = k0 + 4*hl + x_key(e, 0)
+      load_by_key(s0, s1, pen + (kPenOff + k0 + 4 * hl - qrow));
+      return true;
     }
-    if (LOCAL) {
-      const int k0 = key0(i);
-      if (wq_hi - k0 > window || k0 + kBN - 1 - wq_lo > window)
-        // entry kPenOff + key - qrow, key = k0 + 4*hl + x_key(e, 0)
-        add_by_key(s0, s1, pen + (kPenOff + k0 + 4 * hl - qrow));
+    const float* kt = key_tab(i, slot);
+    if (kt) {
+      load_by_key(s0, s1, kt);
+      return true;
+    }
+    return false;
+  }
+  __device__ bool modify(f32x16_t& s0, f32x16_t& s1, int i, int slot) const {
+    if (pen_tile(key0(i))) {
+      const float* kt = key_tab(i, slot);
+      if (kt) add_by_key(s0, s1, kt);
     }
     return false;
   }
