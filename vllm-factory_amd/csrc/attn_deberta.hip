@@ -32,13 +32,14 @@ struct DebArgs {
   const void* qr; int64_t qrs[2];   // fused: query_rel [H, 2S, 64] (p2c) or null
   StepFn step;                      // |bucket| as a function of |d| (log mode)
   int unit;                         // c(d) moves by at most 1 per unit of d
+  int lin_lo, lin_hi;               // c(d) = d + span for lin_lo <= d <= lin_hi
   // packed sequences (fused kernel; nullptr: the padded batch): "batch" b is
   // sequence b, tokens cu[b] .. cu[b + 1] - 1 of [T, H, D] tensors (strides
   // [.][1] = head, [.][2] = token); M = N = the longest sequence
   const int32_t* cu;
 };
 
-__device__ inline int deb_index(const DebArgs& a, int d) {
+__host__ __device__ inline int deb_index(const DebArgs& a, int d) {
   int bk;
   if (a.log_bucket) {
     const int mag = step_eval(a.step, d < 0 ? -d : d);
@@ -556,15 +557,17 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
         u32x4_t kf[4];
 #pragma unroll
         for (int ds = 0; ds < 4; ++ds) kf[ds] = lds_at<u32x4_t>(Kc, ko.o[ds] + kb * 4096);
-        f32x16_t acc0 = {}, acc1 = {};
-#pragma unroll
-        for (int ds = 0; ds < 4; ++ds) {
-          acc0 = E::mfma32(pa[0][ds], kf[ds], acc0);
-          if (two_i) acc1 = E::mfma32(pa[1][ds], kf[ds], acc1);
-        }
         // lane holds key kb*32 + cl, indices ib*32 + 8j + 4h + 0..3
-        store_runs<E>(PT, ((kb * 32 + cl) * kPTs + w * 32 + 4 * hl) * 2, acc0);
-        if (two_i) store_runs<E>(PT, ((kb * 32 + cl) * kPTs + (w + 4) * 32 + 4 * hl) * 2, acc1);
+        f32x16_t acc = E::mfma32(pa[0][0], kf[0], f32x16_t{});
+#pragma unroll
+        for (int ds = 1; ds < 4; ++ds) acc = E::mfma32(pa[0][ds], kf[ds], acc);
+        store_runs<E>(PT, ((kb * 32 + cl) * kPTs + w * 32 + 4 * hl) * 2, acc);
+        if (two_i) {
+          acc = E::mfma32(pa[1][0], kf[0], f32x16_t{});
+#pragma unroll
+          for (int ds = 1; ds < 4; ++ds) acc = E::mfma32(pa[1][ds], kf[ds], acc);
+          store_runs<E>(PT, ((kb * 32 + cl) * kPTs + (w + 4) * 32 + 4 * hl) * 2, acc);
+        }
       }
     }
     if (C2P && wave_on) {
@@ -580,16 +583,44 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
       if (P2C) pt_loads(i + 1);
       if (C2P && wave_on) c_prefetch(i + 1);
     }
-    if (wave_on) {
+    // the wave's relative distances qrow - key all lie where c(d) = d + span:
+    // the gather addresses are a lane base plus a per-score immediate
+    const bool lin = qw0 - key0 - (kBN - 1) >= a.lin_lo && qw0 + 31 - key0 <= a.lin_hi;
+    if (wave_on && lin) {
+      // 2 c(d) for d = qrow - key, key = key0 + 4 hl + x_key(e, 0)
+      const int rel2 = 2 * (qrow - 4 * hl - key0 + a.span);
+      const int cb = lds_opaque(c_row - 2 * cwl + rel2 - 2 * (kBN - 1));
+      const int pb = lds_opaque(pt_row - 2 * wlo + rel2);
+      map_scores(s0, s1, [&](int e, float v) {
+        const int xk = x_key(e, 0);
+        const int co = cb + 2 * (kBN - 1 - xk), po = pb + xk * (kPTs * 2 - 2);
+        if (C2P && P2C) {
+          const uint32_t cv = lds_at<uint16_t>(Cm, co);
+          const uint32_t pv = lds_at<uint16_t>(PT, po);
+          return E::dot2_ones(cv | (pv << 16), v);
+        }
+        if (C2P) v += E::to_f32(lds_at<uint16_t>(Cm, co));
+        if (P2C) v += E::to_f32(lds_at<uint16_t>(PT, po));
+        return v;
+      });
+    } else if (wave_on) {
       const int lb = lut_lane - key0;
       const int cb = lds_opaque(c_row - 2 * cwl), pb = lds_opaque(pt_row - 2 * wlo);
       map_scores(s0, s1, [&](int e, float v) {
         const int xk = x_key(e, 0);
         const int c2 = lut[lb - xk];
+        if (C2P && P2C) {
+          // both 16-bit terms in one register, added by one packed dot
+          const uint32_t cv = lds_at<uint16_t>(Cm, cb + c2);
+          const uint32_t pv = lds_at<uint16_t>(PT, pb + xk * (kPTs * 2) + c2);
+          return E::dot2_ones(cv | (pv << 16), v);
+        }
         if (C2P) v += E::to_f32(lds_at<uint16_t>(Cm, cb + c2));
         if (P2C) v += E::to_f32(lds_at<uint16_t>(PT, pb + xk * (kPTs * 2) + c2));
         return v;
       });
+    }
+    if (wave_on) {
       if (key0 + kBN > len) {
         map_scores(s0, s1, [&](int e, float v) { return key0 + x_key(e, hl) >= len ? -INFINITY : v; });
       }
@@ -715,6 +746,16 @@ static int setup_scalars(DebArgs& a, float sm_scale, int position_buckets, int m
     int rc;
     if ((rc = build_deberta_step(nb, maxd, max_abs, a.span, &a.step))) return rc;
     a.unit = step_is_unit(a.step) ? 1 : 0;
+  }
+  // the run of distances around 0 where c(d) = d + span (empty: lo > hi)
+  a.lin_lo = 1;
+  a.lin_hi = 0;
+  if (deb_index(a, 0) == a.span) {
+    int lo = 0, hi = 0;
+    while (hi + 1 < max_abs && deb_index(a, hi + 1) == hi + 1 + a.span) ++hi;
+    while (1 - lo < max_abs && deb_index(a, lo - 1) == lo - 1 + a.span) --lo;
+    a.lin_lo = lo;
+    a.lin_hi = hi;
   }
   return VFK_OK;
 }
