@@ -17,8 +17,8 @@ oracle timed on the host.
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
                        [--only headline|traffic|SECTION[,SECTION...]]
 SECTION names the extra figures to run after the headline (rpb, deberta,
-epilogues, mt5_layer, deberta_layer, deberta_v1_layer, encoder); the default
-runs all of them.
+epilogues, glu_linear, qkv_rope, mt5_layer, deberta_layer, deberta_v1_layer,
+encoder); the default runs all of them.
 """
 from __future__ import annotations
 
@@ -487,6 +487,64 @@ def glu_linear_config5(torch, args):
                 note="fused: one kernel writes [M, 1152]; unfused: [M, 2304] projection + GELU-gate pass")
 
 
+def qkv_rope_config5(torch, args):
+    """ModernBERT-base attention block input side over the 256-sequence pack
+    (x [163 736, 768] bf16, Wqkv [2304, 768], token-50284 key mask): the fused
+    q | k | v projection with the k rotation in the GEMM epilogue plus the
+    attention over its rotated k (qkv_rope_projection +
+    varlen_rope_attention_krot), against hipBLASLt F.linear plus the attention
+    call with its k pre-pass (varlen_rope_attention); global and local layers,
+    and the two projections alone."""
+    import math
+    import torch.nn.functional as F
+
+    import workloads
+    from kernels.varlen_attention import (qkv_rope_projection, token_positions,
+                                          varlen_rope_attention, varlen_rope_attention_krot)
+
+    dev = torch.device("cuda:0")
+    c = workloads.config5()
+    cu = c.cu_seqlens.to(dev)
+    M, K, H = int(c.ids.numel()), 768, 12
+    g = torch.Generator(device=dev).manual_seed(4)
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(3 * K, K, device=dev, generator=g) * 0.036).to(torch.bfloat16)
+    key_valid = (c.ids != 50284).to(dev)
+    pos = token_positions(cu, M)
+    scale = 1.0 / math.sqrt(64)
+    res = {}
+    for name, window, theta in (("global", -1, 160000.0), ("local", 64, 10000.0)):
+        def fused():
+            r = qkv_rope_projection(x, w, H, pos, c.max_seqlen, theta, scale)
+            return varlen_rope_attention_krot(r, cu, c.max_seqlen, window, key_valid)
+
+        def unfused():
+            qkv = F.linear(x, w).view(M, 3, H, 64)
+            return varlen_rope_attention(qkv[:, 0], qkv[:, 1], qkv[:, 2], cu, c.max_seqlen, window,
+                                         theta, scale, key_valid)
+        for _ in range(2):
+            for tag, fn in (("fused", fused), ("unfused", unfused)):
+                for _ in range(args.warmup):
+                    fn()
+                ms = device_ms(torch, fn, args.steps)
+                key = f"{name}_{tag}_ms"
+                res[key] = min(res.get(key, ms), ms)
+    proj = lambda: qkv_rope_projection(x, w, H, pos, c.max_seqlen, 160000.0, scale)
+    gemm = lambda: F.linear(x, w)
+    for _ in range(2):
+        for tag, fn in (("projection_fused_ms", proj), ("projection_hipblaslt_ms", gemm)):
+            for _ in range(args.warmup):
+                fn()
+            ms = device_ms(torch, fn, args.steps)
+            res[tag] = min(res.get(tag, ms), ms)
+    flop = 2.0 * M * K * 3 * K
+    res.update(gflop_projection=flop / 1e9,
+               projection_fused_tflops=flop / (res["projection_fused_ms"] * 1e-3) / 1e12,
+               note="fused: projection writes q, v and the rotated k, attention reads the rotated "
+                    "k; unfused: [M, 2304] projection, then k pre-pass + attention")
+    return res
+
+
 def mt5_layer_config4(torch, args):
     """One mT5-large encoder layer (RMSNorm, RPB attention, gated-GELU FFN) at
     config 4 (B=32, L=768, lengths U{512..768}); tokens/s over valid tokens."""
@@ -656,6 +714,7 @@ def main():
                 ("deberta", "deberta_v3_large_config3", lambda: deberta_config3(torch, args)),
                 ("epilogues", "epilogues", lambda: epilogue_bench(torch, args, c2)),
                 ("glu_linear", "glu_linear_modernbert_config5", lambda: glu_linear_config5(torch, args)),
+                ("qkv_rope", "qkv_rope_modernbert_config5", lambda: qkv_rope_config5(torch, args)),
                 ("mt5_layer", "mt5_large_layer_config4", lambda: mt5_layer_config4(torch, args)),
                 ("deberta_layer", "deberta_v3_large_layer_config3",
                  lambda: deberta_layer_config3(torch, args)),

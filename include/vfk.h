@@ -460,6 +460,44 @@ int vfk_glu_fwd(int32_t act, const vfk_tensor* a, const vfk_tensor* b,
 int vfk_glu_linear_fwd(int32_t act, const vfk_tensor* x, const vfk_tensor* w,
                        vfk_tensor* out, void* stream);
 
+/* The q | k | v projection with the K rotation in the GEMM epilogue: the
+ * Wqkv linear of models/modernbert/modernbert_encoder.py:236-242
+ * (ModernBertAttention: Wqkv, view [T, 3, H, 64], then the rotary step of
+ * kernels/fused_rope_global.py / fused_rope_local.py on q and k) without the
+ * [T, 3H*64] projection or a separate K pass.
+ *   x [M, K], w [3 * num_heads * 64, K] (q rows, k rows, v rows), bf16/fp16,
+ *     rows contiguous and 16-byte aligned, K a multiple of 64
+ *   positions: device int32 [M], the rotary position of each token (clamped
+ *     into the table)
+ *   rope_cos_sin: the fp32 table of vfk_rope_table, rope_positions rows
+ *   q_out, v_out [M, num_heads, 64]: x . w^T of the q and v heads, rounded
+ *     once (q is not rotated: vfk_varlen_attn_krot_fwd rotates it)
+ *   workspace (vfk_qkv_rope_workspace_bytes, 16-byte aligned): the k heads,
+ *     rotated in fp32, multiplied by softmax_scale * log2(e) and rounded once,
+ *     head-major [num_heads][M][64], then per head the largest row norm of
+ *     each 32-token block [num_heads][ceil(M / 32)] fp32: the input of
+ *     vfk_varlen_attn_krot_fwd with the same M, heads and softmax_scale. */
+int vfk_qkv_rope_linear_fwd(const vfk_tensor* x, const vfk_tensor* w,
+                            const int32_t* positions, const float* rope_cos_sin,
+                            int32_t rope_positions, int32_t num_heads, float softmax_scale,
+                            vfk_tensor* q_out, vfk_tensor* v_out, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of vfk_qkv_rope_linear_fwd for M tokens and num_heads
+ * heads: M * num_heads * 128 rounded up to 256, plus num_heads *
+ * ceil(M / 32) * 4. */
+int64_t vfk_qkv_rope_workspace_bytes(int64_t tokens, int32_t num_heads);
+
+/* vfk_varlen_attn_fwd with RoPE for K already rotated by
+ * vfk_qkv_rope_linear_fwd (krot = its workspace, same tokens, heads and
+ * softmax_scale; positions t - cu_seqlens[s]): no K pre-pass. q and v
+ * [T, H, 64] bf16/fp16; q is rotated in the kernel with rope_cos_sin. */
+int vfk_varlen_attn_krot_fwd(const vfk_tensor* q, const vfk_tensor* v, const void* krot,
+                             int64_t krot_bytes, const int32_t* cu_seqlens, int32_t num_seqs,
+                             int32_t max_seqlen, int32_t window, const float* rope_cos_sin,
+                             int32_t rope_positions, const uint8_t* key_valid,
+                             float softmax_scale, vfk_tensor* out, void* stream);
+
 /* Activation out = act(x) over [rows, n] (row strides). Replaces the
  * intermediate activation of models/deberta_v2/deberta_v2_encoder.py:535-550
  * (DebertaV2Intermediate, ACT2FN[hidden_act]) in inference. */

@@ -36,8 +36,10 @@ struct VarlenArgs {
   const float* rope;        // optional [positions][32][2] (cos, sin) table
   const uint8_t* key_valid; // optional, [T]
   const void* kr;           // RoPE: rotated, scaled K, head-major [H][T][64]
-  float* kmax;              // RoPE: max row norm of each key tile [H][nseq][nkt]
+  float* kmax;              // RoPE: max row norm of each key tile [H][nseq][nkt], or
+                            // (kblk32) of each 32-token block of the stream [H][ceil(T / 32)]
   int nkt;                  // key tiles per sequence slot: ceil(max_seqlen / 64)
+  int kblk32;               // kmax holds 32-token stream blocks (K from the fused projection)
   int64_t T;
 };
 
@@ -283,9 +285,16 @@ __global__ __launch_bounds__(256, 4) void varlen_fwd_kernel(VarlenArgs a) {
     // |score| <= |q| max|k| over the workgroup's key tiles (scores are in
     // log2 units: K carries c2); the margin covers the fp32 norms and the
     // MFMA's fp32 accumulation
-    const float* km = a.kmax + ((int64_t)h * a.nseq + s) * a.nkt;
     float kx = 0.f;
-    for (int j = kt_begin + lane; j < kt_end; j += 64) kx = fmaxf(kx, km[j]);
+    if (a.kblk32) {
+      // stream blocks covering the workgroup's keys (a superset: still a bound)
+      const float* km = a.kmax + (int64_t)h * ((a.T + 31) >> 5);
+      const int b0 = (tok0 + kt_begin * kBN) >> 5, b1 = (tok0 + min(kt_end * kBN, n) - 1) >> 5;
+      for (int j = b0 + lane; j <= b1; j += 64) kx = fmaxf(kx, km[j]);
+    } else {
+      const float* km = a.kmax + ((int64_t)h * a.nseq + s) * a.nkt;
+      for (int j = kt_begin + lane; j < kt_end; j += 64) kx = fmaxf(kx, km[j]);
+    }
     kx = wave_max(kx);
     float q2 = 0.f;
 #pragma unroll
@@ -416,6 +425,8 @@ static int check_thd(const vfk_tensor* t, const char* name, int dtype, int64_t T
 }
 
 static int64_t kr_bytes(int64_t T, int64_t H) { return (T * H * kHD * 2 + 255) / 256 * 256; }
+static int launch_varlen(VarlenArgs& a, int dt, bool rope, int max_seqlen, hipStream_t st,
+                         const char* nm);
 
 extern "C" int64_t vfk_varlen_attn_workspace_bytes(int32_t dtype, int64_t total_tokens,
                                                   int32_t num_heads, int32_t rope,
@@ -499,14 +510,71 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
     else
       hipLaunchKernelGGL(rope_k_pack_kernel<F16>, pgrid, dim3(256), 0, st, a, nkt);
   }
+  return launch_varlen(a, dt, rope, max_seqlen, st, "vfk_varlen_attn_fwd");
+}
+
+// Attention over K already rotated, scaled by c2 and laid out head-major by
+// the fused q | k | v projection (vfk_qkv_rope_linear_fwd): no pre-pass.
+extern "C" int vfk_varlen_attn_krot_fwd(const vfk_tensor* q, const vfk_tensor* v,
+                                        const void* krot, int64_t krot_bytes,
+                                        const int32_t* cu_seqlens, int32_t num_seqs,
+                                        int32_t max_seqlen, int32_t window,
+                                        const float* rope_cos_sin, int32_t rope_positions,
+                                        const uint8_t* key_valid, float softmax_scale,
+                                        vfk_tensor* out, void* stream) {
+  const char* nm = "vfk_varlen_attn_krot_fwd";
+  int rc = check_tensor(q, "q", 3);
+  if (rc) return rc;
+  const int dt = q->dtype;
+  const int64_t T = q->size[0], H = q->size[1];
+  if (dt != VFK_BF16 && dt != VFK_F16) return set_error(VFK_ERR_UNSUPPORTED, "%s: q must be bf16 or fp16", nm);
+  if ((rc = check_thd(q, "q", dt, T, H)) || (rc = check_thd(v, "v", dt, T, H)) ||
+      (rc = check_thd(out, "out", dt, T, H)))
+    return rc;
+  if (!cu_seqlens) return set_error(VFK_ERR_INVALID, "cu_seqlens is NULL");
+  if (num_seqs < 0 || max_seqlen < 0)
+    return set_error(VFK_ERR_INVALID, "num_seqs/max_seqlen must be >= 0");
+  if (T >= (1ll << 31) || H > 4096 || max_seqlen > (1 << 24))
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: sizes too large", nm);
+  if (num_seqs == 0 || max_seqlen == 0 || H == 0) return VFK_OK;
+  if (!(softmax_scale > 0.f) || !isfinite(softmax_scale))
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: softmax_scale must be > 0", nm);
+  if (!rope_cos_sin || rope_positions < max_seqlen || !aligned16(rope_cos_sin))
+    return set_error(VFK_ERR_INVALID, "%s: rope table missing, unaligned or shorter than max_seqlen", nm);
+  const int64_t need = kr_bytes(T, H) + H * ((T + 31) / 32) * 4;
+  if (!krot || krot_bytes < need || !aligned16(krot))
+    return set_error(VFK_ERR_INVALID, "%s: krot needs %lld 16-byte aligned bytes", nm, (long long)need);
+  VarlenArgs a = {};
+  a.q = q->data; a.k = nullptr; a.v = v->data; a.o = out->data;
+  for (int i = 0; i < 2; ++i) {
+    a.qs[i] = q->stride[i]; a.vs[i] = v->stride[i]; a.os[i] = out->stride[i];
+  }
+  a.cu = cu_seqlens; a.nseq = num_seqs; a.H = (int)H; a.T = T;
+  a.window = window < 0 ? -1 : window;
+  a.c2 = softmax_scale * VFK_LOG2E;
+  a.key_valid = key_valid;
+  a.rope = rope_cos_sin;
+  a.kr = krot;
+  a.kmax = reinterpret_cast<float*>(static_cast<char*>(const_cast<void*>(krot)) + kr_bytes(T, H));
+  a.kblk32 = 1;
+  const int64_t span = (int64_t)max_seqlen * 2;
+  if (span * 64 >= (1ll << 31) || span * a.vs[0] >= (1ll << 31))
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: max_seqlen x row stride too large", nm);
+  return launch_varlen(a, dt, true, max_seqlen, (hipStream_t)stream, nm);
+}
+
+// Launch of the 16-bit attention kernel for prepared arguments.
+static int launch_varlen(VarlenArgs& a, int dt, bool rope, int max_seqlen, hipStream_t st,
+                         const char* nm) {
+  const int64_t H = a.H, num_seqs = a.nseq;
   if (a.window >= 0 && a.window >= max_seqlen) a.window = -1;  // window covers every pair
   if (a.window > kPenOff - kBM)
-    return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: window %d > %d", a.window, kPenOff - kBM);
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: window %d > %d", nm, a.window, kPenOff - kBM);
   a.nqt = ceil_div(max_seqlen, kBM);
   const int64_t blocks = (int64_t)a.nqt * H * num_seqs;
   if (blocks >= (1ll << 31))
-    return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: grid too large");
-  const bool local = a.window >= 0, kv = key_valid != nullptr;
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: grid too large", nm);
+  const bool local = a.window >= 0, kv = a.key_valid != nullptr;
 #define VFK_VL(E, R, L, K) \
   hipLaunchKernelGGL((varlen_fwd_kernel<E, R, L, K>), dim3((unsigned)blocks), dim3(256), 0, st, a)
 #define VFK_VL_E(E)                                                   \
@@ -524,7 +592,7 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
   }
 #undef VFK_VL_E
 #undef VFK_VL
-  return launch_status("vfk_varlen_attn_fwd");
+  return launch_status(nm);
 }
 
 extern "C" int vfk_rope_table(float theta, int32_t max_positions, float* out, void* stream) {

@@ -76,12 +76,17 @@ _SIGNATURES = {
     "vfk_rmsnorm_fwd": [_P, _P, _P, _f32, _P, _P, _vp],
     "vfk_glu_fwd": [_i32, _P, _P, _P, _vp],
     "vfk_glu_linear_fwd": [_i32, _P, _P, _P, _vp],
+    "vfk_qkv_rope_linear_fwd": [_P, _P, _vp, _vp, _i32, _i32, _f32, _P, _P, _vp, _i64, _vp],
+    "vfk_qkv_rope_workspace_bytes": [_i64, _i32],
+    "vfk_varlen_attn_krot_fwd": [_P, _P, _vp, _i64, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32,
+                                 _P, _vp],
     "vfk_act_fwd": [_i32, _P, _P, _vp],
     "vfk_residual_add": [_P, _P, _P, _vp],
     "vfk_colbert_head_fwd": [_P, _P, _P, _P, _f32, _P, _P, _P, _P, _vp],
 }
 
 _RESTYPES = {"vfk_varlen_attn_workspace_bytes": ctypes.c_int64,
+             "vfk_qkv_rope_workspace_bytes": ctypes.c_int64,
              "vfk_varlen_meta_workspace_bytes": ctypes.c_int64,
              "vfk_gliner_class_workspace_bytes": ctypes.c_int64}
 

@@ -20,7 +20,7 @@ Rows that see no key at all are returned as zeros.
 from __future__ import annotations
 
 import math
-from typing import Dict, Optional, Tuple
+from typing import Dict, NamedTuple, Optional, Tuple
 
 import torch
 
@@ -85,4 +85,82 @@ def varlen_rope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         ws.data_ptr() if ws is not None else None, ws_bytes,
         _lib.ref(_lib.desc(out)),
     )
+    return out
+
+
+def token_positions(cu_seqlens: torch.Tensor, total_tokens: int) -> torch.Tensor:
+    """int32 [T]: t - cu_seqlens[s] for token t of sequence s (the rotary
+    position varlen_rope_attention gives it), computed on the device."""
+    t = torch.arange(total_tokens, dtype=torch.int32, device=cu_seqlens.device)
+    s = torch.searchsorted(cu_seqlens[1:].contiguous(), t, right=True)
+    return (t - cu_seqlens.index_select(0, s)).to(torch.int32)
+
+
+class RotatedQKV(NamedTuple):
+    """Output of qkv_rope_projection: q and v [T, H, 64] as projected, and the
+    workspace holding k rotated, scaled by softmax_scale * log2(e) and laid out
+    head-major, with per-head norm bounds of each 32-token block."""
+    q: torch.Tensor
+    v: torch.Tensor
+    krot: torch.Tensor
+    rope_theta: float
+    softmax_scale: float
+
+
+def qkv_rope_projection(x: torch.Tensor, wqkv: torch.Tensor, num_heads: int,
+                        positions: torch.Tensor, max_seqlen: int, rope_theta: float,
+                        softmax_scale: Optional[float] = None) -> RotatedQKV:
+    """The Wqkv linear of models/modernbert/modernbert_encoder.py:236-242 with the
+    rotary step of k in the GEMM epilogue (vfk_qkv_rope_linear_fwd): x [T, K],
+    wqkv [3 H 64, K] (q, k, v rows) in bf16 / fp16, positions int32 [T] (the
+    rotary position of each token, < max_seqlen). The projection sums stay in
+    fp32 through the rotation and are rounded once. Use the result with
+    varlen_rope_attention_krot."""
+    dev = _lib.require_gpu(x, wqkv, positions)
+    T, K = x.shape
+    if wqkv.shape != (3 * num_heads * 64, K) or wqkv.dtype != x.dtype:
+        raise ValueError(f"qkv_rope_projection: wqkv must be [{3 * num_heads * 64}, {K}] {x.dtype}")
+    if positions.dtype != torch.int32 or positions.shape != (T,):
+        raise ValueError("qkv_rope_projection: positions must be int32 [T]")
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(64)
+    tab = rope_table(rope_theta, int(max_seqlen), dev)
+    x2 = _lib.rows_aligned(x)
+    w2 = _lib.rows_aligned(wqkv)
+    q = torch.empty(T, num_heads, 64, dtype=x.dtype, device=x.device)
+    v = torch.empty_like(q)
+    ws_bytes = int(_lib.load().vfk_qkv_rope_workspace_bytes(int(T), int(num_heads)))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    _lib.on_device("vfk_qkv_rope_linear_fwd", dev, _lib.ref(_lib.desc(x2)), _lib.ref(_lib.desc(w2)),
+                   positions.contiguous().data_ptr(), tab.data_ptr(), int(tab.shape[0]),
+                   int(num_heads), float(scale), _lib.ref(_lib.desc(q)), _lib.ref(_lib.desc(v)),
+                   ws.data_ptr(), ws_bytes)
+    return RotatedQKV(q, v, ws, float(rope_theta), float(scale))
+
+
+def varlen_rope_attention_krot(qkv: RotatedQKV, cu_seqlens: torch.Tensor, max_seqlen: int,
+                               window: int = -1, key_valid: Optional[torch.Tensor] = None,
+                               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """varlen_rope_attention for the output of qkv_rope_projection (k already
+    rotated: no k pass); positions t - cu_seqlens[s] must be the ones the
+    projection was given. Returns [T, H, 64]."""
+    q, v = qkv.q, qkv.v
+    dev = _lib.require_gpu(q, v, qkv.krot, cu_seqlens, key_valid)
+    if cu_seqlens.dtype != torch.int32 or cu_seqlens.dim() != 1:
+        raise ValueError("cu_seqlens must be a 1-D int32 tensor")
+    if not cu_seqlens.is_contiguous():
+        cu_seqlens = cu_seqlens.contiguous()
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    kv_ptr = None
+    if key_valid is not None:
+        if key_valid.numel() != q.shape[0]:
+            raise ValueError("key_valid must have one entry per token")
+        key_valid = key_valid.to(torch.uint8).contiguous()
+        kv_ptr = key_valid.data_ptr()
+    tab = rope_table(qkv.rope_theta, int(max_seqlen), dev)
+    _lib.on_device(
+        "vfk_varlen_attn_krot_fwd", dev, _lib.ref(_lib.desc(q)), _lib.ref(_lib.desc(v)),
+        qkv.krot.data_ptr(), int(qkv.krot.numel()), cu_seqlens.data_ptr(),
+        int(cu_seqlens.numel() - 1), int(max_seqlen), int(window), tab.data_ptr(),
+        int(tab.shape[0]), kv_ptr, float(qkv.softmax_scale), _lib.ref(_lib.desc(out)))
     return out
