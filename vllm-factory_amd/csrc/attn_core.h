@@ -148,19 +148,66 @@ __device__ inline int x_key(int i, int h) {
   return kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
 }
 
+// Row sums of the softmax probabilities, two forms:
+//  * RowSumAdd: fp32 adds of the fp32 probabilities; each lane sums its 32
+//    keys and total() adds the partner lane's (l ^ 32) share.
+//  * RowSumMfma: the 16-bit probabilities P (the PV operand) summed on the
+//    matrix core, which takes 31 adds per tile off the vector ALU and makes
+//    the denominator the sum of exactly the weights the numerator uses. The
+//    P registers are read as the B operand of a 16x16x32 MFMA: lane l gives
+//    column n = l % 16 and k = 8 (l / 16) .. +7, i.e. query n + 16 ((l/16) & 1)
+//    and 8 of its keys. The A operand selects k-groups by parity:
+//    A[m][k] = 1 when (k / 8) % 2 == m % 2, so row m of the product is the
+//    16-key sum of query n + 16 (m % 2). Lane l holds rows 4 (l / 16) .. +3:
+//    acc[0] = sum of query l % 16, acc[1] = sum of query l % 16 + 16.
+struct RowSumAdd {
+  float l = 0.f;
+  static constexpr bool kF32 = true;
+  __device__ void scale(float a) { l *= a; }
+  __device__ void add_f32(const f32x16_t& s0, const f32x16_t& s1) {
+    float la = s0[0] + s0[1], lb = s1[0] + s1[1];
+#pragma unroll
+    for (int i = 2; i < 16; ++i) {
+      la += s0[i];
+      lb += s1[i];
+    }
+    l += la + lb;
+  }
+  __device__ void add_p(const u32x4_t (&)[4]) {}
+  __device__ float total() const { return half_swap_sum(l); }
+};
+
+template <typename E>
+struct RowSumMfma {
+  f32x4_t acc = {};
+  static constexpr bool kF32 = false;
+  __device__ void scale(float a) { acc *= a; }
+  __device__ void add_f32(const f32x16_t&, const f32x16_t&) {}
+  __device__ void add_p(const u32x4_t (&p)[4]) {
+    const int l = threadIdx.x & 63;
+    const uint32_t s = (((l >> 4) ^ l) & 1) ? 0u : E::kOnePair;
+    const u32x4_t sel = {s, s, s, s};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = E::mfma16(sel, p[ks], acc);
+  }
+  // the row sum of this lane's query c = l % 32
+  __device__ float total() const { return (threadIdx.x & 16) ? acc[1] : acc[0]; }
+};
+
 // Online softmax over one tile of raw scores (bias already added, -inf =
 // masked), held in the two S^T accumulators s0 (keys 0..31) and s1 (32..63).
 // c = softmax scale * log2(e), so p = exp2(c * (x - m)) is one FMA and one
-// exp2 per score. m: running reference max in raw units; l: this lane's
-// partial row sum. The step is split in two so that a pipelined loop can
-// place the parts apart: softmax_ref (row max, O rescale) and softmax_exp
+// exp2 per score. m: running reference max in raw units; l: the row sum
+// (RowSumAdd / RowSumMfma). The step is split in two so that a pipelined loop
+// can place the parts apart: softmax_ref (row max, O rescale) and softmax_exp
 // (probabilities, row sum, 16-bit packing).
 
 // m := max(m, row max of the tile), but only when the max grew by more than
 // 2^kRescaleSlack (otherwise the old reference is kept and probabilities may
 // reach 256, harmless); O and l are rescaled to the new reference.
+template <typename RS>
 __device__ inline void softmax_ref(const f32x16_t& s0, const f32x16_t& s1, float c, float& m,
-                                   float& l, f32x16_t& o0, f32x16_t& o1) {
+                                   RS& l, f32x16_t& o0, f32x16_t& o1) {
   // IEEE maximum (NaN-propagating) maps to v_maximum3_f32 without the
   // canonicalising moves fmaxf needs: 17 instructions for 32 scores.
   float ma = fmax_ieee(s0[0], s1[0]), mb = fmax_ieee(s0[1], s1[1]);
@@ -176,21 +223,31 @@ __device__ inline void softmax_ref(const f32x16_t& s0, const f32x16_t& s1, float
       const float alpha = fast_exp2((m - m_new) * c);  // m = -inf -> 0
       o0 *= alpha;
       o1 *= alpha;
-      l *= alpha;
+      l.scale(alpha);
       m = m_new;
     }
   }
 }
 
 // p := 16-bit exp2((s - m) c) (0 where m = -inf; s is overwritten with the
-// fp32 probabilities), l += their fp32 sum. The sum uses plain fp32 adds:
-// they co-issue with the matrix cores, the packed dot instructions do not.
+// fp32 probabilities), and their sum added to l.
 // exact: (x - m) * c instead of fma(x, c, -m*c). Needed when x may carry a
 // huge finite additive mask (|x| ~ 1e30): the rounding of m*c alone would
 // then exceed the whole exponent range, while x - m stays exact.
 template <typename E>
+__device__ inline void pack_p(const f32x16_t& s0, const f32x16_t& s1, u32x4_t (&p)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    p[0][j] = E::pack2(s0[2 * j], s0[2 * j + 1]);
+    p[1][j] = E::pack2(s0[8 + 2 * j], s0[8 + 2 * j + 1]);
+    p[2][j] = E::pack2(s1[2 * j], s1[2 * j + 1]);
+    p[3][j] = E::pack2(s1[8 + 2 * j], s1[8 + 2 * j + 1]);
+  }
+}
+
+template <typename E, typename RS>
 __device__ inline void softmax_exp(f32x16_t& s0, f32x16_t& s1, float c, float m, bool exact,
-                                   u32x4_t (&p)[4], float& l) {
+                                   u32x4_t (&p)[4], RS& l) {
   const float ms = (m == -INFINITY) ? 0.f : m;
   if (exact) {
 #pragma unroll
@@ -206,51 +263,29 @@ __device__ inline void softmax_exp(f32x16_t& s0, f32x16_t& s1, float c, float m,
       s1[i] = fast_exp2(__builtin_fmaf(s1[i], c, nmc));
     }
   }
-  float la = s0[0] + s0[1], lb = s1[0] + s1[1];
-#pragma unroll
-  for (int i = 2; i < 16; ++i) {
-    la += s0[i];
-    lb += s1[i];
-  }
-  l += la + lb;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    p[0][j] = E::pack2(s0[2 * j], s0[2 * j + 1]);
-    p[1][j] = E::pack2(s0[8 + 2 * j], s0[8 + 2 * j + 1]);
-    p[2][j] = E::pack2(s1[2 * j], s1[2 * j + 1]);
-    p[3][j] = E::pack2(s1[8 + 2 * j], s1[8 + 2 * j + 1]);
-  }
+  l.add_f32(s0, s1);
+  pack_p<E>(s0, s1, p);
+  l.add_p(p);
 }
 
 // Probabilities without a reference: p = exp2(s) for scores already in log2
 // units and known to satisfy |s| <= log2(E::kPMax) (a bound computed from
 // |q| and max |k| before the loop), so p can neither overflow the fp32
 // accumulators nor underflow the 16-bit P operand; no row max, no rescale.
-template <typename E>
-__device__ inline void softmax_fixed(f32x16_t& s0, f32x16_t& s1, u32x4_t (&p)[4], float& l) {
+template <typename E, typename RS>
+__device__ inline void softmax_fixed(f32x16_t& s0, f32x16_t& s1, u32x4_t (&p)[4], RS& l) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     s0[i] = fast_exp2(s0[i]);
     s1[i] = fast_exp2(s1[i]);
   }
-  float la = s0[0] + s0[1], lb = s1[0] + s1[1];
-#pragma unroll
-  for (int i = 2; i < 16; ++i) {
-    la += s0[i];
-    lb += s1[i];
-  }
-  l += la + lb;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    p[0][j] = E::pack2(s0[2 * j], s0[2 * j + 1]);
-    p[1][j] = E::pack2(s0[8 + 2 * j], s0[8 + 2 * j + 1]);
-    p[2][j] = E::pack2(s1[2 * j], s1[2 * j + 1]);
-    p[3][j] = E::pack2(s1[8 + 2 * j], s1[8 + 2 * j + 1]);
-  }
+  l.add_f32(s0, s1);
+  pack_p<E>(s0, s1, p);
+  l.add_p(p);
 }
 
-template <typename E>
-__device__ inline void softmax_tile(f32x16_t& s0, f32x16_t& s1, float c, float& m, float& l,
+template <typename E, typename RS>
+__device__ inline void softmax_tile(f32x16_t& s0, f32x16_t& s1, float c, float& m, RS& l,
                                     f32x16_t& o0, f32x16_t& o1,
                                     u32x4_t (&p)[4], bool exact = false) {
   softmax_ref(s0, s1, c, m, l, o0, o1);
@@ -601,10 +636,10 @@ __device__ inline void attn_pipe_start(P& pol, int n, uint16_t* __restrict__ K0,
 
 // FIXED: scores arrive in log2 units within +-log2(E::kPMax) (softmax_fixed);
 // otherwise the online softmax with running max m and scale c.
-template <typename E, bool FIXED = false, typename P>
+template <typename E, bool FIXED = false, typename P, typename RS>
 __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t* __restrict__ K1,
                                     uint16_t* __restrict__ V0, uint16_t* __restrict__ V1, int n,
-                                    const u32x4_t (&qf)[4], float c, float& m, float& l,
+                                    const u32x4_t (&qf)[4], float c, float& m, RS& l,
                                     f32x16_t& o0, f32x16_t& o1) {
   if (n <= 0) return;
   KOff ko;
@@ -653,14 +688,19 @@ __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t*
 // Rotates the Q operand in registers (non-interleaved RoPE halves): the lane's
 // chunks ds and ds+2 hold d and d+32. cs = table row of this position:
 // cs[2f] = cos(pos * inv_freq[f]), cs[2f+1] = sin(...), f < 32.
+// Returns the lane's sum of squares of q before the rotation (the rotation
+// keeps each pair's norm; callers bounding |rotated q| allow for the rounding).
 template <typename E>
-__device__ inline void rope_q_table(u32x4_t (&q)[4], const float* __restrict__ cs) {
+__device__ inline float rope_q_table(u32x4_t (&q)[4], const float* __restrict__ cs) {
   const int h = (threadIdx.x & 63) >> 5;
+  float ss = 0.f;
 #pragma unroll
   for (int dl = 0; dl < 2; ++dl) {
     float a[8], b[8];
     unpack8<E>(q[dl], a);
     unpack8<E>(q[dl + 2], b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(b[i], b[i], __builtin_fmaf(a[i], a[i], ss));
     const f32x4_t* t = reinterpret_cast<const f32x4_t*>(cs + 2 * (16 * dl + 8 * h));
 #pragma unroll
     for (int i2 = 0; i2 < 4; ++i2) {
@@ -677,6 +717,7 @@ __device__ inline void rope_q_table(u32x4_t (&q)[4], const float* __restrict__ c
     q[dl] = pack8<E>(a);
     q[dl + 2] = pack8<E>(b);
   }
+  return ss;
 }
 
 // Rotates a staged K tile row (thread t holds key t>>2, d chunks cp and cp+4

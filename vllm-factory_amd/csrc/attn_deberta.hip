@@ -96,7 +96,8 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_kernel(DebArgs a) {
 
   u32x4_t qf[4];
   load_q(qf, Qp + (int64_t)qrow * a.qs[2], qvalid);
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY;
+  RowSumMfma<E> l;
   f32x16_t o0 = {}, o1 = {};
   // lut index of element e in tile kt: qrow - key - dmin
   const int lut_lane = qrow - 4 * hl - dmin;
@@ -128,7 +129,7 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_kernel(DebArgs a) {
     pv_tile<E>(Vt, p, o0, o1);
     __syncthreads();
   }
-  const float l_tot = half_swap_sum(l);
+  const float l_tot = l.total();
   if (qstore) {
     if (!qvalid) {
       f32x16_t z = {};
@@ -205,7 +206,8 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_staged_kernel(DebArgs a
 
   u32x4_t qf[4];
   load_q(qf, Qp + (int64_t)qrow * a.qs[2], qvalid);
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY;
+  RowSumMfma<E> l;
   f32x16_t o0 = {}, o1 = {};
   const int lut_lane = qrow - 4 * hl - dmin;
   const int prow = w * 32 + (lane & 31);  // this lane's staged pos_key row
@@ -282,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void deberta_gather_staged_kernel(DebArgs a
     pv_tile<E>(Vt, p, o0, o1);
     __syncthreads();
   }
-  const float l_tot = half_swap_sum(l);
+  const float l_tot = l.total();
   if (qstore) {
     if (!qvalid) {
       f32x16_t z = {};
@@ -494,7 +496,8 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
 
   u32x4_t qf[4];
   load_q(qf, Qp + (int64_t)qrow * a.qs[2], qvalid);
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY;
+  RowSumMfma<E> l;
   f32x16_t o0 = {}, o1 = {};
   KOff ko;
   VOff vo;
@@ -637,7 +640,7 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
   }
   if (i < kt_end) step(i, K0, K1);
 
-  const float l_tot = half_swap_sum(l);
+  const float l_tot = l.total();
   if (qstore) {
     if (!qvalid) {
       f32x16_t z = {};

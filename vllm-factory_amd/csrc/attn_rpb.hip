@@ -134,9 +134,11 @@ struct RpbPolicy {
       }
       exact = true;
     }
-    if (!CAUSAL) {
+    // the partial tile's keys from the LDS table (with a full mask the
+    // compare form keeps the kernel within its registers)
+    if (!CAUSAL && MASK != MASK_FULL) {
       if (k0 + kBN > Lk) add_by_key(s0, s1, tailm + 4 * hl);
-    } else if (k0 + kBN > Lk || k0 + kBN - 1 > wq_lo) {
+    } else if (k0 + kBN > Lk || (CAUSAL && k0 + kBN - 1 > wq_lo)) {
       map_scores(s0, s1, [&](int e, float v) {
         const int j = k0 + x_key(e, hl);
         return (j >= Lk || (CAUSAL && j > qrow)) ? -INFINITY : v;
@@ -288,10 +290,11 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   load_q(qf, reinterpret_cast<const uint16_t*>(a.q) + qo + h * a.qs[1] + (int64_t)pol.qrow * a.qs[2],
          qvalid);
 
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY;
+  RowSumAdd l;
   f32x16_t o0 = {}, o1 = {};
   attn_loop_db<E>(pol, K0, K1, V0, V1, n, qf, a.c2, m, l, o0, o1);
-  const float l_tot = half_swap_sum(l);
+  const float l_tot = l.total();
   // whole-row stores through this wave's half of K0 / K1 (free after the loop)
   uint16_t* ob = reinterpret_cast<uint16_t*>(a.o) + oo + h * a.os[1];
   const int wq_lo = pol.wq_lo;

@@ -22,6 +22,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "attn_core.h"
 #include "launch_util.h"
@@ -275,10 +276,15 @@ __global__ __launch_bounds__(256, 4) void varlen_fwd_kernel(VarlenArgs a) {
 
   u32x4_t qf[4];
   load_q(qf, Qp + (int64_t)qrow * a.qs[0], qvalid);
-  // rows past n rotate zeros with the table row of position n - 1
-  if (ROPE) rope_q_table<E>(qf, a.rope + (int64_t)min(qrow, n - 1) * 64);
+  // rows past n rotate zeros with the table row of position n - 1; q2: the
+  // lane's share of |q|^2 before the rotation
+  float q2 = 0.f;
+  if (ROPE) q2 = rope_q_table<E>(qf, a.rope + (int64_t)min(qrow, n - 1) * 64);
 
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY;
+  // row sums on the matrix core where the 8 extra registers fit (global
+  // layers); the sliding-window variants would spill
+  typename std::conditional<LOCAL, RowSumAdd, RowSumMfma<E>>::type l;
   f32x16_t o0 = {}, o1 = {};
   const int ntiles = kt_end - kt_begin;
   if (ROPE) {
@@ -296,11 +302,10 @@ __global__ __launch_bounds__(256, 4) void varlen_fwd_kernel(VarlenArgs a) {
       for (int j = kt_begin + lane; j < kt_end; j += 64) kx = fmaxf(kx, km[j]);
     }
     kx = wave_max(kx);
-    float q2 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) q2 += sumsq8<E>(qf[i]);
+    // the rotation keeps |q|; rounding the rotated q to 16 bits grows each
+    // element, and so |q|, by at most 2^-8 relative
     q2 = half_swap_sum(q2);
-    const float ub = sqrtf(q2) * kx * 1.0078125f + 0.0625f;
+    const float ub = sqrtf(q2) * 1.00390625f * kx * 1.0078125f + 0.0625f;
     if (__builtin_amdgcn_ballot_w64(ub > E::kLog2PMax) == 0ull)
       attn_loop_db<E, true>(pol, K0, K1, V0, V1, ntiles, qf, 1.f, m, l, o0, o1);
     else
@@ -309,7 +314,7 @@ __global__ __launch_bounds__(256, 4) void varlen_fwd_kernel(VarlenArgs a) {
     attn_loop_db<E, false>(pol, K0, K1, V0, V1, ntiles, qf, a.c2, m, l, o0, o1);
   }
 
-  const float l_tot = half_swap_sum(l);
+  const float l_tot = l.total();
   // whole-row stores through this wave's half of K0 / K1 (free after the
   // loop's last barrier; a workgroup with no key tile never touched them)
   uint16_t* ob = reinterpret_cast<uint16_t*>(a.o) + (int64_t)tok0 * a.os[0] + h * a.os[1];

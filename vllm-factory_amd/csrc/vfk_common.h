@@ -58,6 +58,12 @@ struct BF16 {
         __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
         0, 0, 0);
   }
+  __device__ static inline f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+        0, 0, 0);
+  }
+  static constexpr uint32_t kOnePair = 0x3f803f80u;  // (1.0, 1.0)
 };
 
 struct F16 {
@@ -86,6 +92,12 @@ struct F16 {
         __builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
         0, 0);
   }
+  __device__ static inline f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        __builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
+        0, 0);
+  }
+  static constexpr uint32_t kOnePair = 0x3c003c00u;  // (1.0, 1.0)
 };
 
 // Unpack eight 16-bit values held in a u32x4 into floats.
