@@ -209,3 +209,53 @@ def test_gliner_front_end_argument_checks():
     with pytest.raises(RuntimeError, match="GPU only"):
         gliner_reps_packed(torch.zeros(4, 8), torch.zeros(4), torch.zeros(4), torch.tensor([0, 4]),
                            [1], 5)
+
+
+def test_qkv_rope_argument_checks():
+    """The fused q|k|v projection and the attention over its rotated k reject
+    bad arguments before any HIP call (CPU tensors serve as descriptors and
+    are never dereferenced)."""
+    from kernels import _lib
+    lib = _lib.load()
+    kr = (100 * 12 * 128 + 255) // 256 * 256
+    assert lib.vfk_qkv_rope_workspace_bytes(100, 12) == kr + 12 * 4 * 4
+    assert lib.vfk_qkv_rope_workspace_bytes(0, 12) == 0
+    T, H, K = 100, 12, 768
+    bf = torch.bfloat16
+    x, w = torch.zeros(T, K, dtype=bf), torch.zeros(3 * H * 64, K, dtype=bf)
+    q, v = torch.zeros(T, H, 64, dtype=bf), torch.zeros(T, H, 64, dtype=bf)
+    d = lambda t: _lib.ref(_lib.desc(t))
+    fake = 1 << 20
+    ws = lib.vfk_qkv_rope_workspace_bytes(T, H)
+    proj = lambda *a: _lib.call("vfk_qkv_rope_linear_fwd", *a)
+    with pytest.raises(ValueError, match="w must be"):
+        proj(d(x), d(torch.zeros(3 * H * 64 + 64, K, dtype=bf)), fake, fake, 512, H, 0.125, d(q), d(v),
+             fake, ws, None)
+    with pytest.raises(NotImplementedError, match="multiple of 64"):
+        proj(d(torch.zeros(T, 96, dtype=bf)), d(torch.zeros(3 * H * 64, 96, dtype=bf)), fake, fake,
+             512, H, 0.125, d(q), d(v), fake, ws, None)
+    with pytest.raises(NotImplementedError, match="bf16 or fp16"):
+        proj(d(x.float()), d(w.float()), fake, fake, 512, H, 0.125, d(q.float()), d(v.float()), fake,
+             ws, None)
+    with pytest.raises(ValueError, match="positions"):
+        proj(d(x), d(w), None, fake, 512, H, 0.125, d(q), d(v), fake, ws, None)
+    with pytest.raises(ValueError, match="rope table"):
+        proj(d(x), d(w), fake, None, 512, H, 0.125, d(q), d(v), fake, ws, None)
+    with pytest.raises(ValueError, match="workspace"):
+        proj(d(x), d(w), fake, fake, 512, H, 0.125, d(q), d(v), fake, ws - 4, None)
+    with pytest.raises(ValueError, match="q_out / v_out"):
+        proj(d(x), d(w), fake, fake, 512, H, 0.125, d(torch.zeros(T, H - 1, 64, dtype=bf)), d(v), fake,
+             ws, None)
+    att = lambda *a: _lib.call("vfk_varlen_attn_krot_fwd", *a)
+    o = torch.zeros(T, H, 64, dtype=bf)
+    with pytest.raises(NotImplementedError, match="bf16 or fp16"):
+        att(d(q.float()), d(v.float()), fake, ws, fake, 2, 64, -1, fake, 512, None, 0.125,
+            d(o.float()), None)
+    with pytest.raises(ValueError, match="krot"):
+        att(d(q), d(v), fake, ws - 4, fake, 2, 64, -1, fake, 512, None, 0.125, d(o), None)
+    with pytest.raises(ValueError, match="rope table"):
+        att(d(q), d(v), fake, ws, fake, 2, 64, -1, None, 512, None, 0.125, d(o), None)
+    with pytest.raises(ValueError, match="rope table"):
+        att(d(q), d(v), fake, ws, fake, 2, 640, -1, fake, 512, None, 0.125, d(o), None)
+    with pytest.raises(ValueError, match="cu_seqlens"):
+        att(d(q), d(v), fake, ws, None, 2, 64, -1, fake, 512, None, 0.125, d(o), None)
