@@ -627,12 +627,18 @@ def deberta_v1_layer_config3(torch, args):
     sl = lens.to(dev)
     w = random_weights_v1(num_layers=1).to(dev)
     fn = lambda: deberta_v1_layer_forward(x, sl, w.layers[0], w)
-    for _ in range(args.warmup):
-        fn()
-    ms = device_ms(torch, fn, args.steps)
+    fu = lambda: deberta_v1_layer_forward(x, sl, w.layers[0], w, fuse_dense_ln=False)
+    res = {}
+    for name, f in (("fused", fn), ("unfused", fu)):
+        for _ in range(args.warmup):
+            f()
+        res[name] = device_ms(torch, f, args.steps)
+    ms = res["fused"]
     tv = int(lens.sum())
     return dict(ms_per_layer=ms, valid_tokens_per_s=tv / (ms * 1e-3), valid_tokens=tv,
-                padded_tokens=32 * 512)
+                padded_tokens=32 * 512, unfused_dense_ln_ms=res["unfused"],
+                note="unfused_dense_ln_ms: the attention output's dense + residual + LayerNorm "
+                     "as GEMM + LayerNorm pass instead of one kernel")
 
 
 def cpu_baseline(torch, c2, min_seconds=10.0):

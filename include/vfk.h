@@ -460,6 +460,44 @@ int vfk_glu_fwd(int32_t act, const vfk_tensor* a, const vfk_tensor* b,
 int vfk_glu_linear_fwd(int32_t act, const vfk_tensor* x, const vfk_tensor* w,
                        vfk_tensor* out, void* stream);
 
+/* Dense projection, bias, residual add and LayerNorm in one kernel:
+ *   out = LayerNorm(round(x w^T + bias) + residual) * ln_weight + ln_bias,
+ * DeBERTa's post-LN output blocks (DebertaV2SelfOutput.forward and
+ * DebertaV2Output.forward, models/deberta_v2/deberta_v2_encoder.py:504-508 and
+ * :563-567: dense -> dropout (identity) -> LayerNorm(. + input_tensor)). The
+ * projection is rounded to the storage type once, after the bias, as the
+ * unfused Linear writes it, and the statistics are fp32 over that value plus
+ * the residual, as in vfk_layernorm_fwd; the [M, N] projection is never
+ * written.
+ *   x [M, K], residual and out [M, N]: one dtype, bf16 or fp16, rows
+ *     contiguous, base pointers and row strides 16-byte aligned
+ *   w_packed [N / 32, K / 16, 64, 8]: the dense weight [N, K] packed by
+ *     vfk_dense_ln_pack_weight (same dtype, contiguous)
+ *   bias, ln_weight, ln_bias: contiguous 16-byte aligned [N] of that dtype, or
+ *     NULL (zeros, ones, zeros)
+ *   N in {256, 512, 768, 1024}; K a positive multiple of 64
+ *   residual_out [M, N] or NULL: the sum round(x w^T + bias) + residual,
+ *     rounded once, as vfk_layernorm_fwd's residual_out: ModernBERT's
+ *     pre-LN layers carry it on as the residual stream (Wo at
+ *     models/modernbert/modernbert_encoder.py:258 and :177, the residual
+ *     adds at :338-342 and :349-353, then mlp_norm :345 or the next
+ *     layer's attn_norm)
+ *   out and residual_out may each be the residual itself (same rows: updated
+ *     in place), must not overlap x or each other. */
+int vfk_dense_residual_layernorm_fwd(const vfk_tensor* x, const vfk_tensor* w_packed,
+                                     const vfk_tensor* bias, const vfk_tensor* residual,
+                                     const vfk_tensor* ln_weight, const vfk_tensor* ln_bias,
+                                     float eps, vfk_tensor* out, vfk_tensor* residual_out,
+                                     void* stream);
+
+/* The weight layout vfk_dense_residual_layernorm_fwd reads: w [N, K] (rows
+ * contiguous and 16-byte aligned) -> packed [N / 32, K / 16, 64, 8] with
+ * packed[f][s][l][i] = w[32 f + l % 32][16 s + 8 (l / 32) + i], the operand
+ * order of the 32x32x16 matrix instruction, so that each wave's operand load
+ * is one contiguous KiB. Done once per weight (no counterpart in the
+ * reference, whose Linear reads w as stored). Same N and K limits. */
+int vfk_dense_ln_pack_weight(const vfk_tensor* w, vfk_tensor* packed, void* stream);
+
 /* The q | k | v projection with the K rotation in the GEMM epilogue: the
  * Wqkv linear of models/modernbert/modernbert_encoder.py:236-242
  * (ModernBertAttention: Wqkv, view [T, 3, H, 64], then the rotary step of

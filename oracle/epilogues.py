@@ -99,6 +99,19 @@ def residual_dense(x, weight, bias=None, residual_weight=None, use_residual=Fals
     return y
 
 
+def dense_residual_layernorm(x, weight, bias, residual, ln_weight=None, ln_bias=None, eps=1e-7,
+                             round_dtype=None, dtype=torch.float32):
+    """DeBERTa's post-LN output block, DebertaV2SelfOutput.forward and
+    DebertaV2Output.forward (models/deberta_v2/deberta_v2_encoder.py:504-508 and
+    :563-567, dropout the identity at inference): LayerNorm(x W^T + b + residual).
+    round_dtype: the storage type the unfused Linear writes its output in
+    (rounded once, after the bias); None keeps the projection unrounded."""
+    y = residual_dense(x, weight, bias, dtype=dtype)
+    if round_dtype is not None:
+        y = y.to(round_dtype).to(dtype)
+    return layernorm(y + residual.to(dtype), ln_weight, ln_bias, eps, dtype)
+
+
 def colbert_head(hidden, layers, norm_weight=None, norm_bias=None, eps=1e-5, residual=None,
                  layer_norm=True, dtype=torch.float32):
     """The encoder's final LayerNorm (models/modernbert/modernbert_encoder.py:412-415,

@@ -34,6 +34,41 @@ def test_deberta_layers_match_oracle(batch, layers):
         assert err <= 6e-2 and cs >= 0.9999, (b, err, cs)
 
 
+def test_deberta_layer_dense_ln_paths_agree_and_match_oracle():
+    """DeBERTa-v3-base widths (hidden 768, 12 heads, intermediate 3072), where
+    the attention output's dense + residual + LayerNorm runs as one kernel by
+    default: that path and the GEMM + LayerNorm pass (fuse_dense_ln=False)
+    both match the oracle on the valid rows of the padded layer, and the
+    packed layer's two paths agree with each other."""
+    from encoders.deberta import (deberta_layer_forward, deberta_layer_packed,
+                                  deberta_rel_embeddings, random_weights)
+    from kernels.packing import unpad_packed
+    from oracle import encoders as oe
+    _, lens = workloads.config3_hidden(3)
+    hidden = torch.randn(3, 512, 768, generator=torch.Generator().manual_seed(71))
+    w = random_weights(num_layers=1, hidden=768, heads=12, inter=3072, dtype=torch.bfloat16)
+    dev = torch.device("cuda:0")
+    wd = w.to(dev)
+    x, sl = hidden.to(dev, torch.bfloat16), lens.to(dev)
+    rel = deberta_rel_embeddings(wd)
+    want = oe.deberta_encoder(hidden.to(torch.bfloat16).float(), lens, w)
+    outs = {}
+    for fuse in (True, False):
+        got = deberta_layer_forward(x, sl, rel, wd.layers[0], wd, fuse_dense_ln=fuse).float().cpu()
+        for b in range(3):
+            n = int(lens[b])
+            err = (got[b, :n] - want[b, :n]).abs().max().item()
+            cs = cosine(got[b, :n], want[b, :n])
+            assert err <= 6e-2 and cs >= 0.9999, (fuse, b, err, cs)
+        cu = torch.cat([lens.new_zeros(1), lens.cumsum(0)]).to(device=dev, dtype=torch.int32)
+        xf = unpad_packed(x, cu, int(lens.sum()))
+        outs[fuse] = deberta_layer_packed(xf, cu, x.shape[1], rel, wd.layers[0], wd,
+                                          fuse_dense_ln=fuse).float().cpu()
+    assert "wo" in wd.layers[0].packed
+    d = (outs[True] - outs[False]).abs()
+    assert d.max().item() <= 6e-2 and cosine(outs[True], outs[False]) >= 0.9999, d.max().item()
+
+
 def test_deberta_layer_wide_bucket_steps_match_oracle():
     """position_buckets 256 with max_relative_positions 256: the log bucket
     moves by 2 per unit of distance in places, so the layer takes the
@@ -124,7 +159,8 @@ def test_deberta_v1_layers_match_oracle(layers, max_rel):
     for lw in w.layers:
         want = oe.deberta_v1_layer(want, lens, w.rel_emb.float(),
                                    ed.DebertaV1LayerWeights(*(getattr(lw, f).float() for f in
-                                                              ed.DebertaV1LayerWeights.__dataclass_fields__)),
+                                                              ed.DebertaV1LayerWeights.__dataclass_fields__
+                                                              if f != "packed")),
                                    12, max_rel, w.eps)
     assert torch.isfinite(got).all()
     for b in range(B):

@@ -32,7 +32,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     from kernels import _lib
-    assert _lib.load().vfk_abi_version() == 14
+    assert _lib.load().vfk_abi_version() == 15
 
 
 def _host_t5(rel, bidirectional, nb, md):
@@ -259,3 +259,56 @@ def test_qkv_rope_argument_checks():
         att(d(q), d(v), fake, ws, fake, 2, 640, -1, fake, 512, None, 0.125, d(o), None)
     with pytest.raises(ValueError, match="cu_seqlens"):
         att(d(q), d(v), fake, ws, None, 2, 64, -1, fake, 512, None, 0.125, d(o), None)
+
+
+def test_dense_layernorm_argument_checks():
+    """The dense + residual + LayerNorm entry point rejects unsupported widths,
+    reduction lengths, dtypes, parameter shapes and an output overlapping x
+    before any HIP call (CPU tensors serve as descriptors, never read)."""
+    from kernels import _lib
+    bf = torch.bfloat16
+    M, N, K = 100, 1024, 1024
+    x, w = torch.zeros(M, K, dtype=bf), torch.zeros(N // 32, K // 16, 64, 8, dtype=bf)
+    r, o, p = torch.zeros(M, N, dtype=bf), torch.zeros(M, N, dtype=bf), torch.zeros(N, dtype=bf)
+    d = lambda t: _lib.ref(_lib.desc(t))
+    g = lambda *a: _lib.call("vfk_dense_residual_layernorm_fwd", *a, None)
+    f = lambda *a: g(*a, None)
+    with pytest.raises(NotImplementedError, match="N must be"):
+        f(d(x), d(torch.zeros(20, K // 16, 64, 8, dtype=bf)), None, d(torch.zeros(M, 640, dtype=bf)),
+          None, None, 1e-7, d(torch.zeros(M, 640, dtype=bf)))
+    with pytest.raises(NotImplementedError, match="multiple of 64"):
+        f(d(torch.zeros(M, 96, dtype=bf)), d(torch.zeros(N // 32, 6, 64, 8, dtype=bf)), None, d(r),
+          None, None, 1e-7, d(o))
+    with pytest.raises(NotImplementedError, match="bf16 or fp16"):
+        f(d(x.float()), d(w.float()), None, d(r.float()), None, None, 1e-7, d(o.float()))
+    with pytest.raises(ValueError, match="share one dtype"):
+        f(d(x), d(w.half()), None, d(r), None, None, 1e-7, d(o))
+    with pytest.raises(ValueError, match="w_packed must be"):
+        f(d(x), d(torch.zeros(N // 32, K // 16 + 4, 64, 8, dtype=bf)), None, d(r), None, None, 1e-7, d(o))
+    with pytest.raises(ValueError, match="expected 4 dims"):
+        f(d(x), d(torch.zeros(N, K, dtype=bf)), None, d(r), None, None, 1e-7, d(o))
+    pk = lambda *a: _lib.call("vfk_dense_ln_pack_weight", *a, None)
+    with pytest.raises(ValueError, match="packed must be"):
+        pk(d(torch.zeros(N, K, dtype=bf)), d(torch.zeros(N // 32, K // 16, 64, 4, dtype=bf)))
+    with pytest.raises(NotImplementedError, match="N must be"):
+        pk(d(torch.zeros(N + 32, K, dtype=bf)), d(torch.zeros(N // 32 + 1, K // 16, 64, 8, dtype=bf)))
+    with pytest.raises(ValueError, match="residual and out"):
+        f(d(x), d(w), None, d(r[:50]), None, None, 1e-7, d(o))
+    with pytest.raises(ValueError, match="ln_weight"):
+        f(d(x), d(w), None, d(r), d(torch.zeros(N - 8, dtype=bf)), None, 1e-7, d(o))
+    with pytest.raises(ValueError, match="bias"):
+        f(d(x), d(w), d(p.float()), d(r), None, None, 1e-7, d(o))
+    big = torch.zeros(M, N + K, dtype=bf)
+    with pytest.raises(ValueError, match="output overlaps"):
+        f(d(big[:, :K]), d(w), None, d(r), None, None, 1e-7, d(big[:, K:]))
+    with pytest.raises(ValueError, match="output overlaps"):
+        g(d(big[:, :K]), d(w), None, d(r), None, None, 1e-7, d(o), d(big[:, K:]))
+    with pytest.raises(ValueError, match="out and residual_out overlap"):
+        g(d(x), d(w), None, d(r), None, None, 1e-7, d(o), d(o))
+    with pytest.raises(ValueError, match="residual_out must be"):
+        g(d(x), d(w), None, d(r), None, None, 1e-7, d(o), d(torch.zeros(M, N, dtype=torch.float16)))
+    with pytest.raises(ValueError, match="eps"):
+        f(d(x), d(w), None, d(r), None, None, -1.0, d(o))
+    # M = 0 returns before any launch
+    d0 = lambda t: _lib.ref(_lib.desc(t, shape=[0, t.shape[1]]))
+    f(d0(x), d(w), d(p), d0(r), d(p), d(p), 1e-7, d0(o))

@@ -165,3 +165,40 @@ def test_colbert_head_residual_stack_and_zero_rows():
     z = oep.colbert_head(torch.zeros(3, 256, dtype=torch.float64), [(w3, None, None, False)],
                          layer_norm=False, dtype=torch.float64)
     assert torch.equal(z, torch.zeros(3, 64, dtype=torch.float64))
+
+
+# ------------------------------------------------ DeBERTa dense + residual + LN
+def test_dense_residual_layernorm_matches_torch_modules():
+    """LayerNorm(dense(h) + input) built from torch.nn.Linear and
+    torch.nn.LayerNorm (DebertaV2SelfOutput's modules, eps 1e-7) in float64;
+    unit-gamma rows have mean 0 and variance 1; dropping the bias or the
+    residual fails."""
+    from oracle import epilogues as oep
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(40, 512, generator=g, dtype=D64)
+    res = torch.randn(40, 256, generator=g, dtype=D64)
+    lin = torch.nn.Linear(512, 256).double()
+    ln = torch.nn.LayerNorm(256, eps=1e-7).double()
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(256, 512, generator=g, dtype=D64) * 0.05)
+        lin.bias.copy_(torch.randn(256, generator=g, dtype=D64))
+        ln.weight.copy_(1 + 0.1 * torch.randn(256, generator=g, dtype=D64))
+        ln.bias.copy_(0.1 * torch.randn(256, generator=g, dtype=D64))
+        want = ln(lin(x) + res)
+    got = oep.dense_residual_layernorm(x, lin.weight, lin.bias, res, ln.weight, ln.bias, 1e-7,
+                                       dtype=D64)
+    torch.testing.assert_close(got, want, rtol=0, atol=1e-12)
+    unit = oep.dense_residual_layernorm(x, lin.weight, lin.bias, res, eps=0.0, dtype=D64)
+    torch.testing.assert_close(unit.mean(-1), torch.zeros(40, dtype=D64), rtol=0, atol=1e-12)
+    torch.testing.assert_close(unit.var(-1, unbiased=False), torch.ones(40, dtype=D64), rtol=0, atol=1e-10)
+    no_bias = oep.dense_residual_layernorm(x, lin.weight, None, res, ln.weight, ln.bias, 1e-7, dtype=D64)
+    no_res = oep.layernorm(lin(x).detach(), ln.weight, ln.bias, 1e-7, dtype=D64)
+    assert (no_bias - want).abs().max() > 1e-2 and (no_res - want).abs().max() > 1e-2
+    # round_dtype rounds the projection once: equal to the unrounded form on
+    # inputs whose projection is exactly representable in bf16
+    xi = torch.randint(-2, 3, (8, 64), generator=g).to(D64)
+    wi = torch.randint(-2, 3, (256, 64), generator=g).to(D64)
+    ri = torch.randn(8, 256, generator=g, dtype=D64)
+    torch.testing.assert_close(
+        oep.dense_residual_layernorm(xi, wi, None, ri, round_dtype=torch.bfloat16, dtype=D64),
+        oep.dense_residual_layernorm(xi, wi, None, ri, dtype=D64), rtol=0, atol=0)

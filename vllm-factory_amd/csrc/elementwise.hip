@@ -85,32 +85,6 @@ __device__ inline float ld_any(const void* base, int dt, int64_t i) {
   return F16::to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
 }
 
-template <int CTRL>
-__device__ inline float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over aligned groups of LANES (4..64) lanes, every lane gets the sum:
-// DPP quad permutes and row mirrors inside 16 lanes, then the gfx950
-// permlane16/32 swaps across rows; no LDS round trips.
-template <int LANES>
-__device__ inline float group_sum(float v) {
-  static_assert(LANES >= 4 && LANES <= 64 && (LANES & (LANES - 1)) == 0, "group size");
-  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
-  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
-  if (LANES >= 8) v += dpp_f<0x141>(v);   // row_half_mirror: other quad of 8
-  if (LANES >= 16) v += dpp_f<0x140>(v);  // row_mirror: other 8 of 16
-  if (LANES >= 32) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
-    v = __int_as_float(r[0]) + __int_as_float(r[1]);  // lane ^ 16
-  }
-  if (LANES >= 64) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
-    v = __int_as_float(r[0]) + __int_as_float(r[1]);  // lane ^ 32
-  }
-  return v;
-}
-
 // ---------------------------------------------------------------------------
 // LayerNorm / RMSNorm (one group of LANES lanes per row)
 // ---------------------------------------------------------------------------

@@ -30,6 +30,7 @@ import torch
 import torch.nn.functional as F
 
 from kernels.activation import activation
+from kernels.dense_layernorm import dense_add_layernorm, pack_dense_weight
 from kernels.flash_deberta_attention import (flash_deberta_attention,
                                              flash_deberta_attention_fused, unit_steps)
 from kernels.fused_layernorm import fused_add_layernorm, fused_layernorm
@@ -50,6 +51,9 @@ class DebertaLayerWeights:
     bo2: torch.Tensor
     ln2_w: torch.Tensor  # output.LayerNorm
     ln2_b: torch.Tensor
+    # dense weights in the fused dense + LayerNorm kernel's layout, made on
+    # first use (name -> ((data_ptr, version), packed))
+    packed: dict = field(default_factory=dict, repr=False, compare=False)
 
 
 @dataclass
@@ -71,7 +75,8 @@ class DebertaWeights:
         return DebertaWeights(
             self.hidden, self.heads, self.inter, mv(self.rel_emb), mv(self.rel_ln_w),
             mv(self.rel_ln_b),
-            [DebertaLayerWeights(*(mv(getattr(l, f)) for f in DebertaLayerWeights.__dataclass_fields__))
+            [DebertaLayerWeights(*(mv(getattr(l, f)) for f in DebertaLayerWeights.__dataclass_fields__
+                                   if f != "packed"))
              for l in self.layers],
             self.position_buckets, self.max_relative_positions, self.eps)
 
@@ -106,10 +111,40 @@ def deberta_rel_embeddings(w: DebertaWeights) -> torch.Tensor:
     return fused_layernorm(w.rel_emb, w.hidden, w.rel_ln_w, w.rel_ln_b, w.eps)
 
 
+def _dense_ln_fits(wt: torch.Tensor) -> bool:
+    """Where the fused dense + residual + LayerNorm kernel is used: widths N
+    up to 768 with K <= N (the attention output's square projection of the
+    base-size models), where it beats the library GEMM plus the LayerNorm
+    pass by ~11 us per layer at B=32, L=512. At N = 1024 the two take the same
+    time, and for the FFN output (K = 4 N) the library GEMM is faster."""
+    N, K = wt.shape
+    return (wt.dtype in (torch.bfloat16, torch.float16) and N in (256, 512, 768)
+            and K % 64 == 0 and K <= N)
+
+
+def _attn_output(ctx: torch.Tensor, x: torch.Tensor, lw, eps: float,
+                 fuse: bool = True) -> torch.Tensor:
+    """attention.output (deberta_v2_encoder.py:504-508): LayerNorm(dense(ctx) +
+    x) over [..., hidden], in one kernel when the shape allows it."""
+    if fuse and _dense_ln_fits(lw.wo):
+        key = (lw.wo.data_ptr(), lw.wo._version)
+        cached = lw.packed.get("wo")
+        if cached is None or cached[0] != key:
+            cached = (key, pack_dense_weight(lw.wo))
+            lw.packed["wo"] = cached
+        return dense_add_layernorm(ctx, None, lw.bo, x, lw.ln1_w, lw.ln1_b, eps,
+                                   packed_weight=cached[1])
+    return fused_add_layernorm(F.linear(ctx, lw.wo, lw.bo), x, lw.ln1_w, lw.ln1_b, eps,
+                               return_sum=False)
+
+
 def deberta_layer_forward(x: torch.Tensor, seq_lengths: torch.Tensor, rel: torch.Tensor,
-                          lw: DebertaLayerWeights, w: DebertaWeights) -> torch.Tensor:
+                          lw: DebertaLayerWeights, w: DebertaWeights,
+                          fuse_dense_ln: bool = True) -> torch.Tensor:
     """One DebertaV2Layer on x [B, L, hidden]; seq_lengths int32 [B] on the
-    device; rel = deberta_rel_embeddings(w)."""
+    device; rel = deberta_rel_embeddings(w). fuse_dense_ln: the attention
+    output's dense + residual + LayerNorm in one kernel where the shape
+    allows it (_dense_ln_fits); False keeps the GEMM and the LayerNorm pass."""
     B, L, D = x.shape
     H = w.heads
     d = D // H
@@ -133,8 +168,7 @@ def deberta_layer_forward(x: torch.Tensor, seq_lengths: torch.Tensor, rel: torch
         pos_query = torch.matmul(k, query_rel.transpose(-1, -2).contiguous().unsqueeze(0))
         ctx.copy_(flash_deberta_attention(q, k, v, seq_lengths, pos_key, pos_query, False, sm, pb,
                                           w.max_relative_positions, log).transpose(1, 2))
-    h = fused_add_layernorm(F.linear(ctx.view(B, L, D), lw.wo, lw.bo), x, lw.ln1_w, lw.ln1_b,
-                            w.eps, return_sum=False)
+    h = _attn_output(ctx.view(B, L, D), x, lw, w.eps, fuse_dense_ln)
     inter = activation(F.linear(h, lw.wi, lw.bi), "gelu")
     return fused_add_layernorm(F.linear(inter, lw.wo2, lw.bo2), h, lw.ln2_w, lw.ln2_b, w.eps,
                                return_sum=False)
@@ -142,7 +176,7 @@ def deberta_layer_forward(x: torch.Tensor, seq_lengths: torch.Tensor, rel: torch
 
 def deberta_layer_packed(x: torch.Tensor, cu_seqlens: torch.Tensor, max_len: int,
                          rel: torch.Tensor, lw: DebertaLayerWeights,
-                         w: DebertaWeights) -> torch.Tensor:
+                         w: DebertaWeights, fuse_dense_ln: bool = True) -> torch.Tensor:
     """deberta_layer_forward on packed sequences, without padding: x [T,
     hidden], sequence s owns rows cu_seqlens[s] .. cu_seqlens[s + 1] - 1
     (int32 on the device), max_len >= every sequence length. The projections,
@@ -162,8 +196,7 @@ def deberta_layer_packed(x: torch.Tensor, cu_seqlens: torch.Tensor, max_len: int
     ctx = flash_deberta_attention_varlen(qkv[:, 0], qkv[:, 1], qkv[:, 2], cu_seqlens, max_len,
                                          key_rel, query_rel, 1.0 / math.sqrt(3 * d), pb,
                                          w.max_relative_positions, log)
-    h = fused_add_layernorm(F.linear(ctx.view(T, D), lw.wo, lw.bo), x, lw.ln1_w, lw.ln1_b,
-                            w.eps, return_sum=False)
+    h = _attn_output(ctx.view(T, D), x, lw, w.eps, fuse_dense_ln)
     inter = activation(F.linear(h, lw.wi, lw.bi), "gelu")
     return fused_add_layernorm(F.linear(inter, lw.wo2, lw.bo2), h, lw.ln2_w, lw.ln2_b, w.eps,
                                return_sum=False)
@@ -201,6 +234,7 @@ class DebertaV1LayerWeights:
     bo2: torch.Tensor
     ln2_w: torch.Tensor
     ln2_b: torch.Tensor
+    packed: dict = field(default_factory=dict, repr=False, compare=False)
 
 
 @dataclass
@@ -219,7 +253,8 @@ class DebertaV1Weights:
         return DebertaV1Weights(
             self.hidden, self.heads, self.inter, mv(self.rel_emb),
             [DebertaV1LayerWeights(*(mv(getattr(l, f))
-                                     for f in DebertaV1LayerWeights.__dataclass_fields__))
+                                     for f in DebertaV1LayerWeights.__dataclass_fields__
+                                     if f != "packed"))
              for l in self.layers],
             self.max_relative_positions, self.eps)
 
@@ -251,7 +286,8 @@ def random_weights_v1(num_layers: int = 12, hidden: int = 768, heads: int = 12, 
 
 
 def deberta_v1_layer_forward(x: torch.Tensor, seq_lengths: torch.Tensor,
-                             lw: DebertaV1LayerWeights, w: DebertaV1Weights) -> torch.Tensor:
+                             lw: DebertaV1LayerWeights, w: DebertaV1Weights,
+                             fuse_dense_ln: bool = True) -> torch.Tensor:
     """One DeBERTa v1 DebertaLayer (models/deberta/deberta_encoder.py:528-548) on
     x [B, L, hidden] with seq_lengths int32 [B] on the device: in_proj (rows
     per head q, k, v) with q_bias / v_bias folded into the GEMM's bias, the
@@ -275,8 +311,7 @@ def deberta_v1_layer_forward(x: torch.Tensor, seq_lengths: torch.Tensor,
     ctx = torch.empty(B, L, H, d, dtype=x.dtype, device=x.device)
     flash_deberta_attention_fused(q, k, v, seq_lengths, key_rel, query_rel, 1.0 / math.sqrt(3 * d),
                                   span, mr, False, out=ctx.transpose(1, 2))
-    h = fused_add_layernorm(F.linear(ctx.view(B, L, D), lw.wo, lw.bo), x, lw.ln1_w, lw.ln1_b,
-                            w.eps, return_sum=False)
+    h = _attn_output(ctx.view(B, L, D), x, lw, w.eps, fuse_dense_ln)
     inter = activation(F.linear(h, lw.wi, lw.bi), "gelu")
     return fused_add_layernorm(F.linear(inter, lw.wo2, lw.bo2), h, lw.ln2_w, lw.ln2_b, w.eps,
                                return_sum=False)
