@@ -17,8 +17,8 @@ oracle timed on the host.
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
                        [--only headline|traffic|SECTION[,SECTION...]]
 SECTION names the extra figures to run after the headline (rpb, deberta,
-epilogues, glu_linear, qkv_rope, mt5_layer, deberta_layer, deberta_v1_layer,
-encoder); the default runs all of them.
+epilogues, glu_linear, qkv_rope, dense_ln, mt5_layer, deberta_layer,
+deberta_v1_layer, encoder); the default runs all of them.
 """
 from __future__ import annotations
 
@@ -487,6 +487,49 @@ def glu_linear_config5(torch, args):
                 note="fused: one kernel writes [M, 1152]; unfused: [M, 2304] projection + GELU-gate pass")
 
 
+def dense_ln_config3(torch, args):
+    """DeBERTa post-LN output block at the config-3 batch shape (32 x 512 =
+    16 384 rows): LayerNorm(x W^T + b + residual) as one kernel
+    (dense_add_layernorm, packed weight) against hipBLASLt F.linear plus the
+    residual + LayerNorm pass, at the attention output's square projection of
+    DeBERTa-base (768) and -large (1024) and the -large FFN output (K 4096)."""
+    import torch.nn.functional as F
+    from kernels.dense_layernorm import dense_add_layernorm, pack_dense_weight
+    from kernels.fused_layernorm import fused_add_layernorm
+
+    dev = torch.device("cuda:0")
+    M = 32 * 512
+    out = {}
+    for tag, N, K in (("base_attn_out", 768, 768), ("large_attn_out", 1024, 1024),
+                      ("large_ffn_out", 1024, 4096)):
+        g = torch.Generator(device=dev).manual_seed(N + K)
+        x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+        w = (torch.randn(N, K, device=dev, generator=g) / K ** 0.5).to(torch.bfloat16)
+        b = (0.1 * torch.randn(N, device=dev, generator=g)).to(torch.bfloat16)
+        r = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
+        lw = torch.ones(N, device=dev, dtype=torch.bfloat16)
+        lb = torch.zeros(N, device=dev, dtype=torch.bfloat16)
+        wp = pack_dense_weight(w)
+        o = torch.empty_like(r)
+        fused = lambda: dense_add_layernorm(x, None, b, r, lw, lb, 1e-7, out=o, packed_weight=wp)
+        unfused = lambda: fused_add_layernorm(F.linear(x, w, b), r, lw, lb, 1e-7, return_sum=False)
+        res = {}
+        for _ in range(3):
+            for name, fn in (("fused", fused), ("unfused", unfused)):
+                for _ in range(args.warmup):
+                    fn()
+                ms = device_ms(torch, fn, args.steps)
+                res[name] = min(res.get(name, ms), ms)
+        flop = 2.0 * M * N * K
+        out[tag] = dict(N=N, K=K, fused_ms=res["fused"], unfused_ms=res["unfused"],
+                        fused_tflops=flop / (res["fused"] * 1e-3) / 1e12,
+                        fused_frac=flop / (res["fused"] * 1e-3) / 2.5e15)
+    out["note"] = ("fused: vfk_dense_residual_layernorm_fwd (the [M, N] projection never written); "
+                   "unfused: hipBLASLt GEMM with bias, then the residual + LayerNorm pass; "
+                   "best of 3 interleaved rounds")
+    return out
+
+
 def qkv_rope_config5(torch, args):
     """ModernBERT-base attention block input side over the 256-sequence pack
     (x [163 736, 768] bf16, Wqkv [2304, 768], token-50284 key mask): the fused
@@ -721,6 +764,7 @@ def main():
                 ("epilogues", "epilogues", lambda: epilogue_bench(torch, args, c2)),
                 ("glu_linear", "glu_linear_modernbert_config5", lambda: glu_linear_config5(torch, args)),
                 ("qkv_rope", "qkv_rope_modernbert_config5", lambda: qkv_rope_config5(torch, args)),
+                ("dense_ln", "dense_ln_deberta_config3", lambda: dense_ln_config3(torch, args)),
                 ("mt5_layer", "mt5_large_layer_config4", lambda: mt5_layer_config4(torch, args)),
                 ("deberta_layer", "deberta_v3_large_layer_config3",
                  lambda: deberta_layer_config3(torch, args)),
