@@ -390,7 +390,9 @@ int vfk_rope_table(float theta, int32_t max_positions, float* out, void* stream)
  *   ln_weight, ln_bias [D] or NULL; without ln_weight the rows are projected
  *     as given (no LayerNorm)
  *   weight [N, D] (nn.Linear layout; N = 32, 64, 96 or 128; rows 16-byte
- *     aligned), bias [N] or NULL
+ *     aligned) or the same weight packed by vfk_pack_weight_mfma32
+ *     ([N / 32, D / 16, 64, 8]: each wave's weight load is then one
+ *     contiguous KiB), bias [N] or NULL
  *   hidden_out [T, D] or NULL: receives the LayerNorm output
  *   out [T, N] = y / max(|y|, 1e-8) per row, y = LN(x + residual) W^T + bias
  * x, weight and outputs share one 16-bit dtype; statistics, products and
@@ -472,7 +474,7 @@ int vfk_glu_linear_fwd(int32_t act, const vfk_tensor* x, const vfk_tensor* w,
  *   x [M, K], residual and out [M, N]: one dtype, bf16 or fp16, rows
  *     contiguous, base pointers and row strides 16-byte aligned
  *   w_packed [N / 32, K / 16, 64, 8]: the dense weight [N, K] packed by
- *     vfk_dense_ln_pack_weight (same dtype, contiguous)
+ *     vfk_pack_weight_mfma32 (same dtype, contiguous)
  *   bias, ln_weight, ln_bias: contiguous 16-byte aligned [N] of that dtype, or
  *     NULL (zeros, ones, zeros)
  *   N in {256, 512, 768, 1024}; K a positive multiple of 64
@@ -490,13 +492,14 @@ int vfk_dense_residual_layernorm_fwd(const vfk_tensor* x, const vfk_tensor* w_pa
                                      float eps, vfk_tensor* out, vfk_tensor* residual_out,
                                      void* stream);
 
-/* The weight layout vfk_dense_residual_layernorm_fwd reads: w [N, K] (rows
- * contiguous and 16-byte aligned) -> packed [N / 32, K / 16, 64, 8] with
- * packed[f][s][l][i] = w[32 f + l % 32][16 s + 8 (l / 32) + i], the operand
- * order of the 32x32x16 matrix instruction, so that each wave's operand load
- * is one contiguous KiB. Done once per weight (no counterpart in the
- * reference, whose Linear reads w as stored). Same N and K limits. */
-int vfk_dense_ln_pack_weight(const vfk_tensor* w, vfk_tensor* packed, void* stream);
+/* The weight layout vfk_dense_residual_layernorm_fwd and
+ * vfk_colbert_head_fwd read: w [N, K] (rows contiguous and 16-byte aligned,
+ * N a multiple of 32, K a multiple of 16) -> packed [N / 32, K / 16, 64, 8]
+ * with packed[f][s][l][i] = w[32 f + l % 32][16 s + 8 (l / 32) + i], the
+ * operand order of the 32x32x16 matrix instruction, so that each wave's
+ * operand load is one contiguous KiB. Done once per weight (no counterpart
+ * in the reference, whose Linear reads w as stored). */
+int vfk_pack_weight_mfma32(const vfk_tensor* w, vfk_tensor* packed, void* stream);
 
 /* The q | k | v projection with the K rotation in the GEMM epilogue: the
  * Wqkv linear of models/modernbert/modernbert_encoder.py:236-242

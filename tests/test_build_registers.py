@@ -48,7 +48,7 @@ def _spills(src: str, tmp_path) -> dict:
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
 @pytest.mark.parametrize("src", ["attn_varlen.hip", "attn_rpb.hip", "attn_deberta.hip",
-                                 "gemm_glu.hip", "gemm_ln.hip"])
+                                 "gemm_glu.hip", "gemm_ln.hip", "colbert_head.hip"])
 def test_no_new_register_spills(src, tmp_path):
     spills = _spills(os.path.join(CSRC, src), tmp_path)
     assert spills, "no kernels found"

@@ -218,22 +218,40 @@ def _colbert_rows_close(got, want, what):
     torch.testing.assert_close(got.norm(dim=-1), torch.ones(got.shape[0]), atol=5e-3, rtol=0)
 
 
+@pytest.mark.parametrize("pack", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("T,D,N", [(1000, 768, 128), (1, 768, 128), (33, 1024, 96), (64, 256, 32)])
-def test_colbert_head_with_final_layernorm(dev, dtype, T, D, N):
+def test_colbert_head_with_final_layernorm(dev, dtype, T, D, N, pack):
     """ModernBERT final LayerNorm (weight, no bias, eps 1e-5) of x + residual,
     projection [N, D] without bias, L2 normalisation; the LayerNorm output
-    that comes back equals the LayerNorm oracle."""
+    that comes back equals the LayerNorm oracle. Both weight layouts: operand
+    order (packed) and [N, D] rows."""
     from kernels.colbert_head import colbert_head
     x, r = _rand((T, D), dtype, 41), _rand((T, D), dtype, 42)
     lw = (1 + 0.1 * _rand((D,), torch.float32, 43)).to(dtype)
     w = _rand((N, D), dtype, 44, 0.05)
     want = oe.colbert_head(x, [(w, None, None, False)], lw, None, 1e-5, residual=r)
     got, h = colbert_head(x.to(dev), w.to(dev), None, lw.to(dev), None, 1e-5, residual=r.to(dev),
-                          return_hidden=True)
-    _colbert_rows_close(got, want, f"colbert {dtype} {T}x{D}->{N}")
+                          return_hidden=True, pack=pack)
+    _colbert_rows_close(got, want, f"colbert {dtype} {T}x{D}->{N} pack={pack}")
     assert_elem_close(h, oe.layernorm(x.float() + r.float(), lw, None, 1e-5), dtype,
                       f"colbert hidden {dtype}")
+
+
+def test_colbert_head_repacks_an_updated_weight(dev):
+    """The packed copy is cached per weight tensor and version: an in-place
+    update of the weight is seen by the next call."""
+    from kernels.colbert_head import colbert_head
+    x = _rand((100, 768), torch.bfloat16, 61)
+    w = _rand((128, 768), torch.bfloat16, 62, 0.05)
+    wd = w.to(dev)
+    got1 = colbert_head(x.to(dev), wd)
+    _colbert_rows_close(got1, oe.colbert_head(x, [(w, None, None, False)], layer_norm=False), "before")
+    delta = _rand((128, 768), torch.bfloat16, 63, 0.05)
+    wd.add_(delta.to(dev))
+    w2 = wd.cpu()
+    got2 = colbert_head(x.to(dev), wd)
+    _colbert_rows_close(got2, oe.colbert_head(x, [(w2, None, None, False)], layer_norm=False), "after")
 
 
 def test_colbert_head_projection_only_with_bias(dev):

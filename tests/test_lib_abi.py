@@ -32,7 +32,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     from kernels import _lib
-    assert _lib.load().vfk_abi_version() == 15
+    assert _lib.load().vfk_abi_version() == 16
 
 
 def _host_t5(rel, bidirectional, nb, md):
@@ -287,11 +287,11 @@ def test_dense_layernorm_argument_checks():
         f(d(x), d(torch.zeros(N // 32, K // 16 + 4, 64, 8, dtype=bf)), None, d(r), None, None, 1e-7, d(o))
     with pytest.raises(ValueError, match="expected 4 dims"):
         f(d(x), d(torch.zeros(N, K, dtype=bf)), None, d(r), None, None, 1e-7, d(o))
-    pk = lambda *a: _lib.call("vfk_dense_ln_pack_weight", *a, None)
+    pk = lambda *a: _lib.call("vfk_pack_weight_mfma32", *a, None)
     with pytest.raises(ValueError, match="packed must be"):
         pk(d(torch.zeros(N, K, dtype=bf)), d(torch.zeros(N // 32, K // 16, 64, 4, dtype=bf)))
-    with pytest.raises(NotImplementedError, match="N must be"):
-        pk(d(torch.zeros(N + 32, K, dtype=bf)), d(torch.zeros(N // 32 + 1, K // 16, 64, 8, dtype=bf)))
+    with pytest.raises(NotImplementedError, match="multiple of 32"):
+        pk(d(torch.zeros(N + 16, K, dtype=bf)), d(torch.zeros(N // 32, K // 16, 64, 8, dtype=bf)))
     with pytest.raises(ValueError, match="residual and out"):
         f(d(x), d(w), None, d(r[:50]), None, None, 1e-7, d(o))
     with pytest.raises(ValueError, match="ln_weight"):

@@ -11,7 +11,9 @@
 // LayerNorm) into a 16-bit LDS tile [32][D]. Phase 2: wave w computes output
 // columns 32w .. 32w+31 for the 32 tokens with v_mfma_f32_32x32x16 (A = rows
 // of W, streamed from L2, where the whole [N, D] matrix stays resident,
-// through a register ring, each lane reading whole 64-byte runs of its row;
+// through a register ring: from W in operand order, as vfk_pack_weight_mfma32
+// lays it out, each load of a wave is one contiguous KiB; from the [N, D]
+// rows, each lane reads whole 64-byte runs of its row;
 // B = the tokens' normalised rows from LDS;
 // all of a wave's row loads are issued before any row is reduced), so lane (c, h) ends
 // with token c and 16 of the wave's columns. Phase 3: per-token sums of
@@ -58,8 +60,9 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
-// NCH = D / 256: 4-element chunks per lane and row.
-template <typename E, int NCH>
+// NCH = D / 256: 4-element chunks per lane and row. PACKED: a.w is the weight
+// in operand order [N/32][D/16][64][8].
+template <typename E, int NCH, bool PACKED>
 __global__ __launch_bounds__(256) void colbert_head_kernel(HeadArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int D = NCH * 256;
@@ -139,31 +142,35 @@ __global__ __launch_bounds__(256) void colbert_head_kernel(HeadArgs a) {
   const bool on = 32 * w < a.N;
   f32x16_t acc = {};
   if (on) {
-    // The reduction order over k is free as long as both operands follow it:
-    // in each 64-wide chunk, MFMA step j gives lane half hh the k values
-    // 32 hh + 8 j .. +7, so a lane reads one contiguous 64-byte run of its W
-    // row per chunk and the two halves cover the row's 128-byte line once.
-    const uint16_t* wrow = a.w + (int64_t)(32 * w + c) * a.ws + 32 * hh;
-    const uint16_t* arow = At + c * ld + 32 * hh;
+    // Packed: k-step s of the wave's 32 rows is the KiB block w * D/16 + s,
+    // lane half hh holding k = 16 s + 8 hh .. +7 (the standard operand order).
+    // Rows: the reduction order over k is free as long as both operands
+    // follow it: in each 64-wide chunk, MFMA step j gives lane half hh the k
+    // values 32 hh + 8 j .. +7, so a lane reads one contiguous 64-byte run of
+    // its W row per chunk and the two halves cover the row's 128-byte line.
+    const uint16_t* wrow = PACKED ? a.w + ((int64_t)w * (D / 16) * 64 + lane) * 8
+                                  : a.w + (int64_t)(32 * w + c) * a.ws + 32 * hh;
+    const uint16_t* arow = At + c * ld + (PACKED ? 8 : 32) * hh;
+    auto wsrc = [&](int m, int j) { return PACKED ? wrow + (4 * m + j) * 512 : wrow + 64 * m + 8 * j; };
+    auto asrc = [&](int m, int j) { return PACKED ? arow + 64 * m + 16 * j : arow + 64 * m + 8 * j; };
     // W streams from L2 through a ring of kWC chunks (4 MFMA steps each)
     constexpr int kWC = 4, NK = NCH * 4;  // chunks in flight, chunks in D
     u32x4_t wq[kWC][4];
 #pragma unroll
     for (int m = 0; m < kWC; ++m)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) wq[m][j] = *reinterpret_cast<const u32x4_t*>(wrow + 64 * m + 8 * j);
+      for (int j = 0; j < 4; ++j) wq[m][j] = *reinterpret_cast<const u32x4_t*>(wsrc(m, j));
 #pragma unroll
     for (int m = 0; m < NK; ++m) {
       __builtin_amdgcn_sched_barrier(0);
       u32x4_t xb[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xb[j] = *reinterpret_cast<const u32x4_t*>(arow + 64 * m + 8 * j);
+      for (int j = 0; j < 4; ++j) xb[j] = *reinterpret_cast<const u32x4_t*>(asrc(m, j));
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc = E::mfma32(wq[m % kWC][j], xb[j], acc);
       if (m + kWC < NK) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          wq[m % kWC][j] = *reinterpret_cast<const u32x4_t*>(wrow + 64 * (m + kWC) + 8 * j);
+        for (int j = 0; j < 4; ++j) wq[m % kWC][j] = *reinterpret_cast<const u32x4_t*>(wsrc(m + kWC, j));
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -203,7 +210,7 @@ __global__ __launch_bounds__(256) void colbert_head_kernel(HeadArgs a) {
   }
 }
 
-template <typename E, int NCH>
+template <typename E, int NCH, bool PACKED>
 static void launch_head(const HeadArgs& a, hipStream_t st) {
   const size_t lds = (size_t)kHeadRows * (NCH * 256 + kHeadPad) * 2 + 4 * 32 * sizeof(float);
   const unsigned grid = (unsigned)((a.T + kHeadRows - 1) / kHeadRows);
@@ -214,12 +221,12 @@ static void launch_head(const HeadArgs& a, hipStream_t st) {
     (void)hipGetDevice(&dev);
     const uint64_t bit = 1ull << (dev & 63);
     if (!(raised.load() & bit)) {
-      (void)hipFuncSetAttribute((const void*)colbert_head_kernel<E, NCH>,
+      (void)hipFuncSetAttribute((const void*)colbert_head_kernel<E, NCH, PACKED>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       raised.fetch_or(bit);
     }
   }
-  hipLaunchKernelGGL((colbert_head_kernel<E, NCH>), dim3(grid), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((colbert_head_kernel<E, NCH, PACKED>), dim3(grid), dim3(256), lds, st, a);
 }
 
 }  // namespace vfk
@@ -263,17 +270,27 @@ extern "C" int vfk_colbert_head_fwd(const vfk_tensor* x, const vfk_tensor* resid
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_colbert_head_fwd: x must be bf16 or fp16");
   const int64_t T = x->size[0], D = x->size[1];
   if (!present(weight)) return set_error(VFK_ERR_INVALID, "vfk_colbert_head_fwd: weight is NULL");
-  rc = check_tensor(weight, "weight", 2);
+  const bool packed = weight->ndim == 4;
+  rc = check_tensor(weight, "weight", packed ? 4 : 2);
   if (rc) return rc;
-  const int64_t N = weight->size[0];
+  const int64_t N = packed ? 32 * weight->size[0] : weight->size[0];
   if (D % 256 || D < 256 || D > 1024)
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_colbert_head_fwd: hidden size %lld (needs a multiple "
                      "of 256 up to 1024)", (long long)D);
   if (N % 32 || N < 32 || N > 128)
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_colbert_head_fwd: output size %lld (needs 32, 64, 96 "
                      "or 128)", (long long)N);
-  if ((rc = check_rows(x, "x", dt, T, D, 4)) || (rc = check_rows(weight, "weight", dt, N, D, 8)) ||
-      (rc = check_rows(out, "out", dt, T, N, 4)))
+  if (packed) {
+    if (weight->dtype != dt || weight->size[1] != D / 16 || weight->size[2] != 64 || weight->size[3] != 8 ||
+        weight->stride[3] != 1 || weight->stride[2] != 8 || weight->stride[1] != 512 ||
+        weight->stride[0] != 512 * (D / 16) || (reinterpret_cast<uintptr_t>(weight->data) & 15))
+      return set_error(VFK_ERR_INVALID,
+                       "vfk_colbert_head_fwd: a packed weight must be a contiguous, 16-byte aligned "
+                       "[N / 32, %lld, 64, 8] of x's dtype (vfk_pack_weight_mfma32)", (long long)(D / 16));
+  } else if ((rc = check_rows(weight, "weight", dt, N, D, 8))) {
+    return rc;
+  }
+  if ((rc = check_rows(x, "x", dt, T, D, 4)) || (rc = check_rows(out, "out", dt, T, N, 4)))
     return rc;
   if (present(residual) && (rc = check_rows(residual, "residual", dt, T, D, 4))) return rc;
   if (present(hidden_out) && (rc = check_rows(hidden_out, "hidden_out", dt, T, D, 4))) return rc;
@@ -292,24 +309,24 @@ extern "C" int vfk_colbert_head_fwd(const vfk_tensor* x, const vfk_tensor* resid
   if (present(ln_weight)) a.lnw = static_cast<const uint16_t*>(ln_weight->data);
   if (present(ln_bias)) a.lnb = static_cast<const uint16_t*>(ln_bias->data);
   a.eps = eps;
-  a.w = static_cast<const uint16_t*>(weight->data); a.ws = weight->stride[0];
+  a.w = static_cast<const uint16_t*>(weight->data); a.ws = packed ? 0 : weight->stride[0];
   if (present(bias)) a.bias = static_cast<const uint16_t*>(bias->data);
   if (present(hidden_out)) { a.h = static_cast<uint16_t*>(hidden_out->data); a.hs = hidden_out->stride[0]; }
   a.y = static_cast<uint16_t*>(out->data); a.ys = out->stride[0];
   a.T = T; a.D = (int)D; a.N = (int)N;
   hipStream_t st = (hipStream_t)stream;
   const int nch = (int)(D / 256);
-#define VFK_HEAD(E)                                   \
+#define VFK_HEAD(E, P)                                \
   switch (nch) {                                      \
-    case 1: launch_head<E, 1>(a, st); break;          \
-    case 2: launch_head<E, 2>(a, st); break;          \
-    case 3: launch_head<E, 3>(a, st); break;          \
-    default: launch_head<E, 4>(a, st); break;         \
+    case 1: launch_head<E, 1, P>(a, st); break;       \
+    case 2: launch_head<E, 2, P>(a, st); break;       \
+    case 3: launch_head<E, 3, P>(a, st); break;       \
+    default: launch_head<E, 4, P>(a, st); break;      \
   }
   if (dt == VFK_BF16) {
-    VFK_HEAD(BF16)
+    if (packed) { VFK_HEAD(BF16, true) } else { VFK_HEAD(BF16, false) }
   } else {
-    VFK_HEAD(F16)
+    if (packed) { VFK_HEAD(F16, true) } else { VFK_HEAD(F16, false) }
   }
 #undef VFK_HEAD
   return launch_status("vfk_colbert_head_fwd");

@@ -19,7 +19,7 @@
 // Every workgroup streams the whole weight, and an MFMA operand puts a
 // different row in every lane: loaded from [N, K] rows, each 1 KiB wave load
 // would touch 32 cache lines. The weight is therefore packed once
-// (vfk_dense_ln_pack_weight) into operand order, [N/32][K/16][64 lanes][8]:
+// (vfk_pack_weight_mfma32) into operand order, [N/32][K/16][64 lanes][8]:
 // block (F, s) holds rows 32 F .. +32 and k = 16 s .. +16, lane c + 32 h's
 // 16 bytes being row 32 F + c, k = 16 s + 8 h .. +8. A wave's operand load is
 // then one contiguous KiB, straight into registers (a weight row is used by
@@ -315,29 +315,32 @@ int check_dense_dims(int64_t N, int64_t K) {
 
 using namespace vfk;
 
-extern "C" int vfk_dense_ln_pack_weight(const vfk_tensor* w, vfk_tensor* packed, void* stream) {
+extern "C" int vfk_pack_weight_mfma32(const vfk_tensor* w, vfk_tensor* packed, void* stream) {
   int rc;
   if ((rc = check_tensor(w, "w", 2)) || (rc = check_tensor(packed, "packed", 4))) return rc;
   const int dt = w->dtype;
   if (dt != VFK_BF16 && dt != VFK_F16)
-    return set_error(VFK_ERR_UNSUPPORTED, "dense_ln_pack_weight: w must be bf16 or fp16");
+    return set_error(VFK_ERR_UNSUPPORTED, "pack_weight_mfma32: w must be bf16 or fp16");
   const int64_t N = w->size[0], K = w->size[1];
-  if ((rc = check_dense_dims(N, K))) return rc;
+  if (N < 32 || N % 32 || K < 16 || K % 16)
+    return set_error(VFK_ERR_UNSUPPORTED,
+                     "pack_weight_mfma32: w [%lld, %lld] needs rows a multiple of 32 and columns a "
+                     "multiple of 16", (long long)N, (long long)K);
   if (packed->dtype != dt || packed->size[0] != N / 32 || packed->size[1] != K / 16 ||
       packed->size[2] != 64 || packed->size[3] != 8)
-    return set_error(VFK_ERR_INVALID, "dense_ln_pack_weight: packed must be [%lld, %lld, 64, 8] of w's dtype",
+    return set_error(VFK_ERR_INVALID, "pack_weight_mfma32: packed must be [%lld, %lld, 64, 8] of w's dtype",
                      (long long)(N / 32), (long long)(K / 16));
   if (packed->stride[3] != 1 || packed->stride[2] != 8 || packed->stride[1] != 512 ||
       packed->stride[0] != 512 * (K / 16) || !aligned16(packed->data))
-    return set_error(VFK_ERR_INVALID, "dense_ln_pack_weight: packed must be contiguous and 16-byte aligned");
+    return set_error(VFK_ERR_INVALID, "pack_weight_mfma32: packed must be contiguous and 16-byte aligned");
   if (w->stride[1] != 1 || w->stride[0] < K || w->stride[0] % 8 || !aligned16(w->data))
     return set_error(VFK_ERR_UNSUPPORTED,
-                     "dense_ln_pack_weight: w rows must be contiguous and 16-byte aligned");
+                     "pack_weight_mfma32: w rows must be contiguous and 16-byte aligned");
   const int64_t n16 = N * K / 8;
   hipLaunchKernelGGL(dense_ln_pack_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w->data),
                      w->stride[0], (int)K, n16, static_cast<uint16_t*>(packed->data));
-  return launch_status("dense_ln_pack_weight");
+  return launch_status("pack_weight_mfma32");
 }
 
 extern "C" int vfk_dense_residual_layernorm_fwd(const vfk_tensor* x, const vfk_tensor* w_packed,

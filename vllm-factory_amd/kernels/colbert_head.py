@@ -16,24 +16,27 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
+from .weight_pack import packed_weight
 
 
 def colbert_head(hidden: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
                  norm_weight: Optional[torch.Tensor] = None,
                  norm_bias: Optional[torch.Tensor] = None, eps: float = 1e-5,
                  residual: Optional[torch.Tensor] = None,
-                 return_hidden: bool = False):
+                 return_hidden: bool = False, pack: bool = True):
     """hidden [T, D] (+ residual) -> LayerNorm (if norm_weight) -> @ weight^T
     (+ bias) -> rows scaled to unit L2 norm (norm clamped at 1e-8).
     weight [N, D] with N in {32, 64, 96, 128}, D a multiple of 256 up to 1024.
+    pack: the kernel reads the weight in MFMA operand order, packed once per
+    weight tensor (weight_pack.packed_weight); False reads the [N, D] rows.
     Returns the [T, N] embeddings, and the LayerNorm output if return_hidden."""
     dev = _lib.require_gpu(hidden, weight, bias, norm_weight, norm_bias, residual)
     if hidden.dim() != 2 or weight.dim() != 2 or weight.shape[1] != hidden.shape[1]:
         raise ValueError("hidden must be [T, D] and weight [N, D]")
     x = _lib.rows_aligned(hidden)
     r = _lib.rows_aligned(residual) if residual is not None else None
-    wt = _lib.rows_aligned(weight)
-    T, N = x.shape[0], wt.shape[0]
+    wt = packed_weight(weight) if pack else _lib.rows_aligned(weight)
+    T, N = x.shape[0], weight.shape[0]
     out = torch.empty(T, N, dtype=x.dtype, device=dev)
     h = torch.empty_like(x) if return_hidden else None
     vec = lambda t: None if t is None else t.contiguous()

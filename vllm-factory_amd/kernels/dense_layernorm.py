@@ -22,21 +22,13 @@ from typing import Optional
 import torch
 
 from . import _lib
+from .weight_pack import pack_weight
 
 
 def pack_dense_weight(weight: torch.Tensor) -> torch.Tensor:
     """The [N, K] projection weight in the kernel's operand order,
-    [N / 32, K / 16, 64, 8] (vfk_dense_ln_pack_weight); pack once per weight."""
-    dev = _lib.require_gpu(weight)
-    if weight.dim() != 2:
-        raise ValueError(f"weight must be [N, K], got {tuple(weight.shape)}")
-    N, K = weight.shape
-    w2 = _lib.rows_aligned(weight)
-    packed = torch.empty(max(N // 32, 1), max(K // 16, 1), 64, 8, dtype=weight.dtype,
-                         device=weight.device)
-    _lib.on_device("vfk_dense_ln_pack_weight", dev, _lib.ref(_lib.desc(w2)),
-                   _lib.ref(_lib.desc(packed)))
-    return packed
+    [N / 32, K / 16, 64, 8] (vfk_pack_weight_mfma32); pack once per weight."""
+    return pack_weight(weight)
 
 
 def dense_add_layernorm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor],
