@@ -243,3 +243,33 @@ def test_fused_varlen_equals_padded_call(dev, log_bucket):
         gb = got[a:a + n].transpose(0, 1)
         assert torch.equal(gb, pad[b, :, :n]), f"sequence {b}"
         assert_attn_close(gb, want[b, :, :n], f"varlen b={b}")
+
+
+@pytest.mark.parametrize("which", ["both", "c2p", "p2c"])
+@pytest.mark.parametrize("log_bucket", [True, False])
+def test_chunk_major_tables_equal_row_tables(dev, which, log_bucket):
+    """The fused kernels read key_rel / query_rel either as [H, 2S, 64] rows
+    or in the chunk-major layout [H, 8, 2S, 8]: the same products in the same
+    order, so the outputs are equal bit for bit (padded and packed calls),
+    including windows that run past the table's last row."""
+    lens = [300, 77, 512]
+    B, H, S, L = len(lens), 3, 256, max(lens)
+    q, k, v, kr, qr, ln = _case(B, H, L, S, torch.bfloat16, 91, lens=lens)
+    kr = kr if which != "p2c" else None
+    qr = qr if which != "c2p" else None
+    mv = lambda t: t.to(dev) if t is not None else None
+    print(f"deberta chunk-major {which} log={log_bucket}", flush=True)
+    rows = _k().flash_deberta_attention_fused(q.to(dev), k.to(dev), v.to(dev), ln.to(dev), mv(kr), mv(qr),
+                                              SM, S, 512, log_bucket, chunk_major=False)
+    cm = lambda t: _k().rel_chunk_major(t.to(dev), S) if t is not None else None
+    chunk = _k().flash_deberta_attention_fused(q.to(dev), k.to(dev), v.to(dev), ln.to(dev), cm(kr), cm(qr),
+                                               SM, S, 512, log_bucket)
+    assert torch.equal(rows, chunk)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    qkv = torch.stack([torch.cat([t[b, :, :n].transpose(0, 1) for b, n in enumerate(lens)])
+                       for t in (q, k, v)], 1).to(dev)
+    vr = _k().flash_deberta_attention_varlen(qkv[:, 0], qkv[:, 1], qkv[:, 2], cu.to(dev), L, mv(kr), mv(qr),
+                                             SM, S, 512, log_bucket, chunk_major=False)
+    vc = _k().flash_deberta_attention_varlen(qkv[:, 0], qkv[:, 1], qkv[:, 2], cu.to(dev), L, cm(kr), cm(qr),
+                                             SM, S, 512, log_bucket)
+    assert torch.equal(vr, vc)

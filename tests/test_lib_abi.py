@@ -312,3 +312,33 @@ def test_dense_layernorm_argument_checks():
     # M = 0 returns before any launch
     d0 = lambda t: _lib.ref(_lib.desc(t, shape=[0, t.shape[1]]))
     f(d0(x), d(w), d(p), d0(r), d(p), d(p), 1e-7, d0(o))
+
+
+def test_rel_chunk_major_layout_and_checks():
+    """rel_chunk_major: out[h][c][r][i] = rel[h][r][8 c + i] for r < 2S (a
+    torch view-and-copy, checked on the CPU); the fused entry point rejects
+    mixed layouts, a wrong chunk-major shape and chunk-major fp32 tables
+    before any HIP call."""
+    from kernels import _lib
+    from kernels.flash_deberta_attention import rel_chunk_major
+    rel = torch.arange(3 * 600 * 64, dtype=torch.float32).view(3, 600, 64)
+    cm = rel_chunk_major(rel, 256)
+    assert cm.shape == (3, 8, 512, 8) and cm.is_contiguous()
+    for h, c, r, i in [(0, 0, 0, 0), (2, 7, 511, 7), (1, 3, 200, 5)]:
+        assert cm[h, c, r, i] == rel[h, r, 8 * c + i]
+    assert rel_chunk_major(cm, 256) is cm
+    bf = torch.bfloat16
+    B, H, L = 2, 3, 64
+    q = torch.zeros(B, H, L, 64, dtype=bf)
+    d = lambda t: _lib.ref(_lib.desc(t))
+    fake = 1 << 20
+    f = lambda kr, qr, qq=q: _lib.call("vfk_deberta_fused_fwd", d(qq), d(qq), d(qq), fake, kr, qr,
+                                       0.07, 256, 512, 1, d(qq), None)
+    rows = torch.zeros(H, 512, 64, dtype=bf)
+    cmt = torch.zeros(H, 8, 512, 8, dtype=bf)
+    with pytest.raises(ValueError, match="one layout"):
+        f(d(rows), d(cmt))
+    with pytest.raises(ValueError, match="chunk-major"):
+        f(d(torch.zeros(H, 8, 500, 8, dtype=bf)), None)
+    with pytest.raises(NotImplementedError, match="16-bit"):
+        f(d(cmt.float()), None, q.float())

@@ -30,6 +30,7 @@ struct DebArgs {
   int lut_len;                      // ntiles_k*64 + kBM
   const void* kr; int64_t krs[2];   // fused: key_rel [H, 2S, 64] (c2p) or null
   const void* qr; int64_t qrs[2];   // fused: query_rel [H, 2S, 64] (p2c) or null
+  int rel_cm;                       // both tables chunk-major [H][8][2S][8] (head stride in [0])
   StepFn step;                      // |bucket| as a function of |d| (log mode)
   int unit;                         // c(d) moves by at most 1 per unit of d
   int lin_lo, lin_hi;               // c(d) = d + span for lin_lo <= d <= lin_hi
@@ -391,11 +392,34 @@ constexpr int kPTElems = kBN * kPTs;
 constexpr int kCElems = 32 * kCs;       // per wave
 constexpr int kFusedStaticLds = (3 * kTileElems + kPTElems + 4 * kCElems) * 2;
 
-// Rel-table MFMA operand through a buffer resource over the table's 2S rows
-// (rows past the table read as zeros; their products are never used): lane
-// byte offset voff = row-in-block * rs2 + 16 h, block row offset in soff.
-__device__ inline u32x4_t rel_ld(rsrc_t r, int voff, int soff, int ds) {
-  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 32 * ds, soff, 0));
+// Rel-table MFMA operand (rows row0 .. row0 + 31, k-step ds) through a buffer
+// resource over one head's table. Row-major [2S][64] rows: lane byte offset
+// voff = row-in-block * rs2 + 16 h, soff = row0 * rs2, dsb = 32, and each
+// wave load touches 32 rows' lines. Chunk-major [8][2S][8] (chunk q = k / 8
+// holds 16 bytes of every row): voff = (h * 2S + row-in-block) * 16,
+// soff = row0 * 16, dsb = 2 * 2S * 16, so a wave load reads two contiguous
+// 512-byte runs whatever row0 is. Rows past the table read as zeros, or (chunk
+// major) as rows of the next chunk; their products are never used.
+struct RelSrc {
+  rsrc_t r;
+  int lane, rowb, dsb;  // lane byte offset, bytes per row step, bytes per k-step
+};
+
+__device__ inline u32x4_t rel_ld(const RelSrc& t, int row0, int ds) {
+  return __builtin_bit_cast(u32x4_t,
+                            __builtin_amdgcn_raw_buffer_load_b128(t.r, t.lane, row0 * t.rowb + ds * t.dsb, 0));
+}
+
+__device__ inline RelSrc rel_src(const void* base, int64_t hstride, int64_t rs, int cm, int span, int cl,
+                                 int hl) {
+  RelSrc t;
+  const int rowb = cm ? 16 : (int)rs * 2;
+  t.r = uniform_rsrc(base ? reinterpret_cast<const uint16_t*>(base) + hstride : nullptr,
+                     base ? 2 * span * (cm ? 128 : rowb) : 0);
+  t.lane = cm ? (hl * 2 * span + cl) * 16 : cl * rowb + 16 * hl;
+  t.rowb = rowb;
+  t.dsb = cm ? 64 * span : 32;
+  return t;
 }
 
 // Writes the lane's four 4-element runs of an MFMA output block (rows
@@ -414,11 +438,11 @@ __device__ inline void store_runs(uint16_t* __restrict__ base, int off, const f3
 
 // C blocks ib < NB of one wave: C[row][idx] = Kr[cwl + idx] . q[row].
 template <int NB>
-__device__ inline void c_loads(rsrc_t kr_r, int kr_lane, int cwl, int kr_rs2, u32x4_t (&ca)[3][4]) {
+__device__ inline void c_loads(const RelSrc& kr, int cwl, u32x4_t (&ca)[3][4]) {
 #pragma unroll
   for (int ib = 0; ib < NB; ++ib)
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) ca[ib][ds] = rel_ld(kr_r, kr_lane, (cwl + ib * 32) * kr_rs2, ds);
+    for (int ds = 0; ds < 4; ++ds) ca[ib][ds] = rel_ld(kr, cwl + ib * 32, ds);
 }
 template <typename E, int NB>
 __device__ inline void c_blocks(const u32x4_t (&ca)[3][4], const u32x4_t (&qf)[4],
@@ -487,12 +511,8 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
   tile_src_init(ksrc, reinterpret_cast<const uint16_t*>(a.k) + kb + h * a.ks[1], (int)a.ks[2], len);
   tile_src_init(vsrc, reinterpret_cast<const uint16_t*>(a.v) + vb + h * a.vs[1], (int)a.vs[2], len);
   tile_load_buf(ksrc, 0, K0);
-  const int kr_rs2 = C2P ? (int)a.krs[1] * 2 : 0, qr_rs2 = P2C ? (int)a.qrs[1] * 2 : 0;
-  const rsrc_t kr_r = uniform_rsrc(
-      C2P ? reinterpret_cast<const uint16_t*>(a.kr) + h * a.krs[0] : nullptr, 2 * a.span * kr_rs2);
-  const rsrc_t qr_r = uniform_rsrc(
-      P2C ? reinterpret_cast<const uint16_t*>(a.qr) + h * a.qrs[0] : nullptr, 2 * a.span * qr_rs2);
-  const int kr_lane = cl * kr_rs2 + 16 * hl, qr_lane = cl * qr_rs2 + 16 * hl;
+  const RelSrc krt = rel_src(C2P ? a.kr : nullptr, h * a.krs[0], a.krs[1], a.rel_cm, a.span, cl, hl);
+  const RelSrc qrt = rel_src(P2C ? a.qr : nullptr, h * a.qrs[0], a.qrs[1], a.rel_cm, a.span, cl, hl);
 
   u32x4_t qf[4];
   load_q(qf, Qp + (int64_t)qrow * a.qs[2], qvalid);
@@ -524,11 +544,11 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
     const int nbp = pt_blocks(i);
     if (w < nbp) {
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds) pa[0][ds] = rel_ld(qr_r, qr_lane, (wl + w * 32) * qr_rs2, ds);
+      for (int ds = 0; ds < 4; ++ds) pa[0][ds] = rel_ld(qrt, wl + w * 32, ds);
     }
     if (two && w + 4 < nbp) {
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds) pa[1][ds] = rel_ld(qr_r, qr_lane, (wl + (w + 4) * 32) * qr_rs2, ds);
+      for (int ds = 0; ds < 4; ++ds) pa[1][ds] = rel_ld(qrt, wl + (w + 4) * 32, ds);
     }
   };
   if (P2C) pt_loads(0);
@@ -538,7 +558,7 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
   u32x4_t ca[3][4];
   auto c_prefetch = [&](int i) {
     const int cwl = __builtin_amdgcn_readfirstlane(lut[qw0 - i * kBN - 63 - dmin]) >> 1;
-    c_loads<3>(kr_r, kr_lane, cwl, kr_rs2, ca);
+    c_loads<3>(krt, cwl, ca);
   };
   if (C2P && wave_on) c_prefetch(0);
 
@@ -870,19 +890,37 @@ static int deb_fused_launch(DebArgs& a, int dt, const vfk_tensor* key_rel, const
   int rc;
   const vfk_tensor* rel[2] = {key_rel, query_rel};
   const char* names[2] = {"key_rel", "query_rel"};
+  a.rel_cm = -1;
   for (int i = 0; i < 2; ++i) {
     if (!present(rel[i])) continue;
     const vfk_tensor* r = rel[i];
-    if ((rc = check_tensor(r, names[i], 3))) return rc;
+    const int cm = r->ndim == 4;
+    if (a.rel_cm >= 0 && a.rel_cm != cm)
+      return set_error(VFK_ERR_INVALID, "%s: key_rel and query_rel must share one layout", name);
+    a.rel_cm = cm;
+    if ((rc = check_tensor(r, names[i], cm ? 4 : 3))) return rc;
     if (r->dtype != dt) return set_error(VFK_ERR_INVALID, "%s: dtype differs from q", names[i]);
-    if (r->size[0] != a.H || r->size[1] < 2 * a.span || r->size[2] != kHD || r->stride[2] != 1)
-      return set_error(VFK_ERR_INVALID, "%s: expected [H, >= %d, 64] with unit last stride", names[i],
-                       2 * a.span);
-    if (dt != VFK_F32 && (!aligned16(r->data) || r->stride[0] % 8 || r->stride[1] % 8))
-      return set_error(VFK_ERR_INVALID, "%s: rows must be 16-byte aligned", names[i]);
-    if (i == 0) { a.kr = r->data; a.krs[0] = r->stride[0]; a.krs[1] = r->stride[1]; }
-    else { a.qr = r->data; a.qrs[0] = r->stride[0]; a.qrs[1] = r->stride[1]; }
+    if (cm) {
+      // chunk-major [H, 8, 2S, 8]: chunk c holds k = 8 c .. 8 c + 7 of every row
+      if (dt == VFK_F32)
+        return set_error(VFK_ERR_UNSUPPORTED, "%s: the chunk-major layout is for 16-bit types", names[i]);
+      if (r->size[0] != a.H || r->size[1] != 8 || r->size[2] != 2 * a.span || r->size[3] != 8 ||
+          r->stride[3] != 1 || r->stride[2] != 8 || r->stride[1] != 16 * a.span ||
+          r->stride[0] < 128 * (int64_t)a.span || r->stride[0] % 8 || !aligned16(r->data))
+        return set_error(VFK_ERR_INVALID,
+                         "%s: expected a chunk-major [H, 8, %d, 8], contiguous per head and 16-byte "
+                         "aligned", names[i], 2 * a.span);
+    } else {
+      if (r->size[0] != a.H || r->size[1] < 2 * a.span || r->size[2] != kHD || r->stride[2] != 1)
+        return set_error(VFK_ERR_INVALID, "%s: expected [H, >= %d, 64] with unit last stride", names[i],
+                         2 * a.span);
+      if (dt != VFK_F32 && (!aligned16(r->data) || r->stride[0] % 8 || r->stride[1] % 8))
+        return set_error(VFK_ERR_INVALID, "%s: rows must be 16-byte aligned", names[i]);
+    }
+    if (i == 0) { a.kr = r->data; a.krs[0] = r->stride[0]; a.krs[1] = cm ? 0 : r->stride[1]; }
+    else { a.qr = r->data; a.qrs[0] = r->stride[0]; a.qrs[1] = cm ? 0 : r->stride[1]; }
   }
+  if (a.rel_cm < 0) a.rel_cm = 0;
   if (a.B == 0 || a.H == 0 || a.M == 0) return VFK_OK;
   if (dt == VFK_F32) {
     const int nqt = ceil_div(a.M, 64);

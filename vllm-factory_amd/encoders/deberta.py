@@ -14,7 +14,8 @@ Differences from the reference, by construction: the three projections are
 one GEMM with concatenated weights; pos_key / pos_query are not materialised
 as [B, H, L, 2S] tensors: the attention kernel computes q.key_rel and
 k.query_rel per tile from the per-head projections of the relative table
-(one [2S, hidden] x [hidden, 2 hidden] GEMM per layer); the attention writes
+(one [2S, hidden] x [hidden, 2 hidden] GEMM per layer, whose output is
+copied once into the kernel's chunk-major table layout); the attention writes
 its [B, L, H, d] context in place, so no permute copy precedes the dense
 projection; the residual add is folded into each LayerNorm pass. Query rows
 at or beyond a sequence's length attend nowhere and hold zeros after the
@@ -111,6 +112,15 @@ def deberta_rel_embeddings(w: DebertaWeights) -> torch.Tensor:
     return fused_layernorm(w.rel_emb, w.hidden, w.rel_ln_w, w.rel_ln_b, w.eps)
 
 
+def _rel_pair_chunk_major(pr: torch.Tensor, span: int):
+    """(query_rel, key_rel) of the relative table's projection pr [2S, 2, H,
+    64] (query_proj rows, key_proj rows) in the fused kernels' chunk-major
+    layout [H, 8, 2S, 8], with one copy for both tables."""
+    H = pr.shape[2]
+    t = pr.view(2 * span, 2, H, 8, 8).permute(1, 2, 3, 0, 4).contiguous()
+    return t[0], t[1]
+
+
 def _dense_ln_fits(wt: torch.Tensor) -> bool:
     """Where the fused dense + residual + LayerNorm kernel is used: widths N
     up to 768 with K <= N (the attention output's square projection of the
@@ -159,7 +169,8 @@ def deberta_layer_forward(x: torch.Tensor, seq_lengths: torch.Tensor, rel: torch
     log = w.position_buckets > 0
     sm = 1.0 / math.sqrt(3 * d)
     if unit_steps(pb, w.max_relative_positions, log, L):
-        flash_deberta_attention_fused(q, k, v, seq_lengths, key_rel, query_rel, sm, pb,
+        query_cm, key_cm = _rel_pair_chunk_major(pr, span)
+        flash_deberta_attention_fused(q, k, v, seq_lengths, key_cm, query_cm, sm, pb,
                                       w.max_relative_positions, log, out=ctx.transpose(1, 2))
     else:
         # bucket steps above 1: the reference interface with materialised
@@ -190,11 +201,11 @@ def deberta_layer_packed(x: torch.Tensor, cu_seqlens: torch.Tensor, max_len: int
     span = w.position_buckets if w.position_buckets > 0 else w.max_relative_positions
     qkv = F.linear(x, lw.wqkv, lw.bqkv).view(T, 3, H, d)
     pr = F.linear(rel[:2 * span], lw.wqkv[:2 * D], lw.bqkv[:2 * D]).view(2 * span, 2, H, d)
-    query_rel, key_rel = pr[:, 0].transpose(0, 1), pr[:, 1].transpose(0, 1)
+    query_cm, key_cm = _rel_pair_chunk_major(pr, span)
     pb = w.position_buckets if w.position_buckets > 0 else span
     log = w.position_buckets > 0
     ctx = flash_deberta_attention_varlen(qkv[:, 0], qkv[:, 1], qkv[:, 2], cu_seqlens, max_len,
-                                         key_rel, query_rel, 1.0 / math.sqrt(3 * d), pb,
+                                         key_cm, query_cm, 1.0 / math.sqrt(3 * d), pb,
                                          w.max_relative_positions, log)
     h = _attn_output(ctx.view(T, D), x, lw, w.eps, fuse_dense_ln)
     inter = activation(F.linear(h, lw.wi, lw.bi), "gelu")

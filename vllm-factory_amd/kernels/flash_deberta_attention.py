@@ -97,6 +97,35 @@ def flash_deberta_attention(
     return out
 
 
+def rel_chunk_major(rel: torch.Tensor, att_span: int) -> torch.Tensor:
+    """A per-head relative table [H, >= 2 att_span, 64] in the fused kernels'
+    chunk-major layout [H, 8, 2 att_span, 8] (chunk c holds k = 8c .. 8c + 7
+    of every row), so that each wave's operand load reads contiguous runs.
+    A 4-D table is returned as given."""
+    if rel.dim() == 4:
+        return rel
+    H, R, D = rel.shape
+    if D != 64 or R < 2 * att_span:
+        raise ValueError(f"expected [H, >= {2 * att_span}, 64], got {tuple(rel.shape)}")
+    return rel[:, :2 * att_span].reshape(H, 2 * att_span, 8, 8).permute(0, 2, 1, 3).contiguous()
+
+
+def _rel_tables(key_rel, query_rel, dtype, att_span, chunk_major):
+    """Both tables in one layout: chunk-major (16-bit types, by default) or
+    [H, 2S, 64] rows with aligned rows."""
+    out = []
+    for t in (key_rel, query_rel):
+        if t is None:
+            out.append(None)
+        elif chunk_major and dtype != torch.float32:
+            out.append(rel_chunk_major(t.to(dtype), att_span))
+        elif t.dim() == 4:
+            raise ValueError("a chunk-major table needs a 16-bit dtype and chunk_major=True")
+        else:
+            out.append(_lib.rows_aligned(t.to(dtype)))
+    return out
+
+
 def flash_deberta_attention_fused(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -109,11 +138,15 @@ def flash_deberta_attention_fused(
     max_relative_distance: int = 512,
     use_log_bucket: bool = True,
     out: Optional[torch.Tensor] = None,
+    chunk_major: bool = True,
 ) -> torch.Tensor:
     """Disentangled attention with c2p / p2c computed inside the kernel.
 
     key_rel, query_rel: [H, 2*ATT_SPAN, D] per-head projections of the
-    relative-position embeddings. Equivalent to flash_deberta_attention with
+    relative-position embeddings, or the same in the chunk-major layout of
+    `rel_chunk_major` (which the kernel reads with contiguous loads; 3-D
+    tables are converted unless chunk_major is False). Equivalent to
+    flash_deberta_attention with
     pos_key = q @ key_rel^T and pos_query = k @ query_rel^T. Raises
     NotImplementedError where `unit_steps` is False (flash_deberta_attention
     covers those bucket settings). `out` may be a
@@ -123,8 +156,8 @@ def flash_deberta_attention_fused(
     dev = _lib.require_gpu(q, k, v, key_rel, query_rel)
     B = q.shape[0]
     qq, kk, vv = (_lib.rows_aligned(t) for t in (q, k, v))
-    kr = _lib.rows_aligned(key_rel.to(q.dtype)) if key_rel is not None else None
-    qr = _lib.rows_aligned(query_rel.to(q.dtype)) if query_rel is not None else None
+    span = position_buckets if position_buckets > 0 else max_relative_distance
+    kr, qr = _rel_tables(key_rel, query_rel, q.dtype, span, chunk_major)
     sl = _seq_lengths(seq_lengths, B, dev)
     if out is None:
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -155,6 +188,7 @@ def flash_deberta_attention_varlen(
     max_relative_distance: int = 512,
     use_log_bucket: bool = True,
     out: Optional[torch.Tensor] = None,
+    chunk_major: bool = True,
 ) -> torch.Tensor:
     """flash_deberta_attention_fused over packed sequences, without padding.
 
@@ -168,8 +202,8 @@ def flash_deberta_attention_varlen(
     if q.dim() != 3 or k.shape != q.shape or v.shape != q.shape:
         raise ValueError("q, k, v must be [T, H, D] of one shape")
     qq, kk, vv = (_lib.rows_aligned(t) for t in (q, k, v))
-    kr = _lib.rows_aligned(key_rel.to(q.dtype)) if key_rel is not None else None
-    qr = _lib.rows_aligned(query_rel.to(q.dtype)) if query_rel is not None else None
+    span = position_buckets if position_buckets > 0 else max_relative_distance
+    kr, qr = _rel_tables(key_rel, query_rel, q.dtype, span, chunk_major)
     if out is None:
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     elif (out.shape != q.shape or out.dtype != q.dtype or out.device != q.device
@@ -188,5 +222,5 @@ def flash_deberta_attention_varlen(
 
 
 __all__ = ["flash_deberta_attention", "flash_deberta_attention_fused",
-           "flash_deberta_attention_varlen", "unit_steps",
+           "flash_deberta_attention_varlen", "rel_chunk_major", "unit_steps",
            "clear_config_cache", "HAS_TRITON"]
