@@ -142,6 +142,10 @@ int vfk_flash_deberta_fwd(const vfk_tensor* q, const vfk_tensor* k,
  * followed by flash_deberta_attention).
  *   key_rel   [H, 2*att_span, D]  = key_proj(rel_emb) per head   (c2p) or NULL
  *   query_rel [H, 2*att_span, D]  = query_proj(rel_emb) per head (p2c) or NULL
+ *   either both as given ([H, >= 2 att_span, 64], any strides) or both
+ *   chunk-major [H, 8, 2*att_span, 8], contiguous per head (bf16 / fp16 only):
+ *   element [h][c][r][i] = table[h][r][8c + i]; the kernel's operand loads
+ *   are then contiguous runs, outputs are identical.
  * score(i,j) = (q_i.k_j + q_i.key_rel[c(i-j)] + k_j.query_rel[c(i-j)]) * sm_scale
  * with c(d) = clamp(bucket(d) + att_span, 0, 2*att_span - 1). */
 int vfk_deberta_fused_fwd(const vfk_tensor* q, const vfk_tensor* k,
