@@ -28,21 +28,24 @@ def _case():
     return w, ids, cu, max(lens)
 
 
-@pytest.mark.parametrize("fuse_qkv_rope", [False, True])
+@pytest.mark.parametrize("fuse_qkv_rope,fuse_dense_ln", [(False, False), (True, False), (False, True)])
 @pytest.mark.parametrize("layers,max_abs,min_cos", [(1, 5e-2, 0.9999), (4, 1e-1, 0.9999)])
-def test_modernbert_encoder_matches_oracle(layers, max_abs, min_cos, fuse_qkv_rope):
+def test_modernbert_encoder_matches_oracle(layers, max_abs, min_cos, fuse_qkv_rope, fuse_dense_ln):
     """Also with Wqkv and the k rotation as one kernel (qkv_rope_projection),
-    which rounds k once after the rotation instead of before and after it."""
+    which rounds k once after the rotation instead of before and after it,
+    and with the attention output's Wo + residual + mlp_norm as one kernel
+    (fuse_dense_ln=True, dense_add_layernorm with the sum output)."""
     import encoders.modernbert as em
     from oracle import encoders as oe
     w, ids, cu, mx = _case()
     dev = torch.device("cuda:0")
     got = em.modernbert_forward(ids.to(dev), cu.to(dev), mx, w.to(dev), num_layers=layers,
-                                fuse_qkv_rope=fuse_qkv_rope)
+                                fuse_qkv_rope=fuse_qkv_rope, fuse_dense_ln=fuse_dense_ln)
     want = oe.modernbert_encoder(ids, cu, w, dtype=torch.float32, num_layers=layers)
     err = (got.float().cpu() - want).abs().max().item()
     cs = cosine(got.float().cpu(), want)
-    print(f"layers {layers} fused qkv {fuse_qkv_rope}: max-abs {err:.3e} cosine {cs:.6f}")
+    print(f"layers {layers} fused qkv {fuse_qkv_rope} dense-ln {fuse_dense_ln}: max-abs {err:.3e} "
+          f"cosine {cs:.6f}")
     assert err <= max_abs and cs >= min_cos, (err, cs)
 
 
