@@ -175,6 +175,16 @@ int vfk_deberta_fused_varlen_fwd(const vfk_tensor* q, const vfk_tensor* k,
                                  int32_t max_relative_distance, int32_t use_log_bucket,
                                  vfk_tensor* out, void* stream);
 
+/* Copies key_rel and / or query_rel ([H, >= 2 att_span, 64], 16-byte aligned
+ * rows, bf16 / fp16; either pair may be NULL) into the chunk-major layout the
+ * two fused entry points read fastest, out [H, 8, 2 att_span, 8] with
+ * out[h][c][r][i] = rel[h][r][8c + i], in one launch. No counterpart in the
+ * reference (its pos_key / pos_query matmuls read the projections as
+ * stored). */
+int vfk_deberta_rel_chunk_major(const vfk_tensor* key_rel, vfk_tensor* key_out,
+                                const vfk_tensor* query_rel, vfk_tensor* query_out,
+                                int32_t att_span, void* stream);
+
 /* Varlen (packed) bidirectional attention with optional RoPE and sliding
  * window, for ModernBERT (no counterpart kernel in the reference: it replaces
  * the rotary step and F.scaled_dot_product_attention with the dense O(T^2)

@@ -245,6 +245,27 @@ def test_fused_varlen_equals_padded_call(dev, log_bucket):
         assert_attn_close(gb, want[b, :, :n], f"varlen b={b}")
 
 
+@pytest.mark.parametrize("present", ["both", "key", "query"])
+def test_rel_chunk_major_kernel_equals_torch_layout(dev, present):
+    """vfk_deberta_rel_chunk_major (the calls' one-launch conversion) writes
+    exactly rel_chunk_major's layout, from strided views of one [2S, 2, H,
+    64] projection with extra rows past 2S, bit for bit."""
+    from kernels import _lib
+    S, H = 256, 16
+    g = torch.Generator().manual_seed(12)
+    pr = torch.randn(2 * S + 8, 2, H, 64, generator=g).to(torch.bfloat16).to(dev)
+    qrel, krel = pr[:, 0].transpose(0, 1), pr[:, 1].transpose(0, 1)   # [H, 2S + 8, 64] views
+    kr = krel if present != "query" else None
+    qr = qrel if present != "key" else None
+    out = [torch.full((H, 8, 2 * S, 8), 7.0, dtype=torch.bfloat16, device=dev) if t is not None else None
+           for t in (kr, qr)]
+    _lib.on_device("vfk_deberta_rel_chunk_major", dev, _lib.ref(_lib.desc(kr)), _lib.ref(_lib.desc(out[0])),
+                   _lib.ref(_lib.desc(qr)), _lib.ref(_lib.desc(out[1])), S)
+    for t, o in zip((kr, qr), out):
+        if t is not None:
+            assert torch.equal(o, _k().rel_chunk_major(t, S))
+
+
 @pytest.mark.parametrize("which", ["both", "c2p", "p2c"])
 @pytest.mark.parametrize("log_bucket", [True, False])
 def test_chunk_major_tables_equal_row_tables(dev, which, log_bucket):

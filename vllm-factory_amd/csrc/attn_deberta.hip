@@ -734,9 +734,86 @@ __global__ __launch_bounds__(64) void deberta_fused_f32_kernel(DebArgs a) {
   for (int d = 0; d < kHD; ++d) op[d] = acc[d] * inv;
 }
 
+// Chunk-major copies of up to two relative tables in one launch: thread i
+// of table j moves the 16 bytes of (head h, row r, chunk c), reading them at
+// row r of the [H, R, 64] source and writing them to [h][c][r] of the
+// [H, 8, 2S, 8] destination; a row's eight chunks come from consecutive
+// threads, so the reads are whole rows.
+struct RelCmArgs {
+  const uint16_t* src[2];
+  int64_t ss[2][2];  // head and row strides of each source, in elements
+  uint16_t* dst[2];
+  int64_t ds[2];     // head stride of each destination, in elements
+  int span, H;
+  int64_t n0;        // 16-byte items of table 0 (H * 2S * 8); table 1 follows
+};
+
+__global__ __launch_bounds__(256) void rel_cm_kernel(RelCmArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int j = i >= a.n0 ? 1 : 0;
+  const int64_t e = i - (j ? a.n0 : 0);
+  if (e >= a.n0 || !a.src[j]) return;
+  const int rows = 2 * a.span;
+  const int c = (int)(e & 7);
+  const int64_t hr = e >> 3;
+  const int r = (int)(hr % rows);
+  const int h = (int)(hr / rows);
+  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.src[j] + h * a.ss[j][0] + r * a.ss[j][1] + 8 * c);
+  *reinterpret_cast<u32x4_t*>(a.dst[j] + h * a.ds[j] + ((int64_t)c * rows + r) * 8) = v;
+}
+
 }  // namespace vfk
 
 using namespace vfk;
+
+extern "C" int vfk_deberta_rel_chunk_major(const vfk_tensor* key_rel, vfk_tensor* key_out,
+                                           const vfk_tensor* query_rel, vfk_tensor* query_out,
+                                           int32_t att_span, void* stream) {
+  const vfk_tensor* src[2] = {key_rel, query_rel};
+  vfk_tensor* dst[2] = {key_out, query_out};
+  const char* names[2] = {"key_rel", "query_rel"};
+  if (att_span <= 0 || att_span > 8192)
+    return set_error(VFK_ERR_INVALID, "deberta_rel_chunk_major: att_span %d out of range", att_span);
+  RelCmArgs a = {};
+  a.span = att_span;
+  int dt = -1, H = -1;
+  for (int j = 0; j < 2; ++j) {
+    if (!present(src[j]) && !present(dst[j])) continue;
+    int rc;
+    if ((rc = check_tensor(src[j], names[j], 3)) || (rc = check_tensor(dst[j], "out", 4))) return rc;
+    const vfk_tensor* s = src[j];
+    const vfk_tensor* d = dst[j];
+    if (s->dtype != VFK_BF16 && s->dtype != VFK_F16)
+      return set_error(VFK_ERR_UNSUPPORTED, "deberta_rel_chunk_major: %s must be bf16 or fp16", names[j]);
+    if ((dt >= 0 && s->dtype != dt) || d->dtype != s->dtype || (H >= 0 && s->size[0] != H))
+      return set_error(VFK_ERR_INVALID, "deberta_rel_chunk_major: tables differ in dtype or heads");
+    dt = s->dtype;
+    H = (int)s->size[0];
+    if (s->size[1] < 2 * att_span || s->size[2] != kHD || s->stride[2] != 1 || !aligned16(s->data) ||
+        s->stride[0] % 8 || s->stride[1] % 8)
+      return set_error(VFK_ERR_INVALID,
+                       "deberta_rel_chunk_major: %s must be [H, >= %d, 64] with 16-byte aligned rows",
+                       names[j], 2 * att_span);
+    if (d->size[0] != H || d->size[1] != 8 || d->size[2] != 2 * att_span || d->size[3] != 8 ||
+        d->stride[3] != 1 || d->stride[2] != 8 || d->stride[1] != 16 * (int64_t)att_span ||
+        d->stride[0] < 128 * (int64_t)att_span || d->stride[0] % 8 || !aligned16(d->data))
+      return set_error(VFK_ERR_INVALID,
+                       "deberta_rel_chunk_major: out must be [H, 8, %d, 8], contiguous per head, "
+                       "16-byte aligned", 2 * att_span);
+    a.src[j] = static_cast<const uint16_t*>(s->data);
+    a.ss[j][0] = s->stride[0];
+    a.ss[j][1] = s->stride[1];
+    a.dst[j] = static_cast<uint16_t*>(d->data);
+    a.ds[j] = d->stride[0];
+  }
+  if (H <= 0) return VFK_OK;
+  a.H = H;
+  a.n0 = (int64_t)H * 2 * att_span * 8;
+  const int64_t n = 2 * a.n0;
+  hipLaunchKernelGGL(rel_cm_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launch_status("deberta_rel_chunk_major");
+}
 
 static int check_bhld_deb(const vfk_tensor* t, const char* name, int dtype) {
   int rc = check_tensor(t, name, 4);

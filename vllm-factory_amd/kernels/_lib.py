@@ -78,6 +78,7 @@ _SIGNATURES = {
     "vfk_glu_linear_fwd": [_i32, _P, _P, _P, _vp],
     "vfk_dense_residual_layernorm_fwd": [_P, _P, _P, _P, _P, _P, _f32, _P, _P, _vp],
     "vfk_pack_weight_mfma32": [_P, _P, _vp],
+    "vfk_deberta_rel_chunk_major": [_P, _P, _P, _P, _i32, _vp],
     "vfk_qkv_rope_linear_fwd": [_P, _P, _vp, _vp, _i32, _i32, _f32, _P, _P, _vp, _i64, _vp],
     "vfk_qkv_rope_workspace_bytes": [_i64, _i32],
     "vfk_varlen_attn_krot_fwd": [_P, _P, _vp, _i64, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32,

@@ -111,19 +111,26 @@ def rel_chunk_major(rel: torch.Tensor, att_span: int) -> torch.Tensor:
 
 
 def _rel_tables(key_rel, query_rel, dtype, att_span, chunk_major):
-    """Both tables in one layout: chunk-major (16-bit types, by default) or
-    [H, 2S, 64] rows with aligned rows."""
-    out = []
-    for t in (key_rel, query_rel):
-        if t is None:
-            out.append(None)
-        elif chunk_major and dtype != torch.float32:
-            out.append(rel_chunk_major(t.to(dtype), att_span))
-        elif t.dim() == 4:
-            raise ValueError("a chunk-major table needs a 16-bit dtype and chunk_major=True")
-        else:
-            out.append(_lib.rows_aligned(t.to(dtype)))
-    return out
+    """Both tables in one layout: chunk-major (16-bit types, by default; the
+    [H, 2S, 64] tables of a call are converted by one
+    vfk_deberta_rel_chunk_major launch) or [H, 2S, 64] rows with aligned
+    rows."""
+    tabs = [None if t is None else t.to(dtype) for t in (key_rel, query_rel)]
+    if chunk_major and dtype != torch.float32:
+        todo = [t is not None and t.dim() == 3 for t in tabs]
+        if any(todo):
+            src = [_lib.rows_aligned(t) if c else None for t, c in zip(tabs, todo)]
+            dst = [torch.empty(t.shape[0], 8, 2 * att_span, 8, dtype=dtype, device=t.device) if c else None
+                   for t, c in zip(tabs, todo)]
+            dev = _lib.require_gpu(*[t for t in src if t is not None])
+            _lib.on_device("vfk_deberta_rel_chunk_major", dev, _lib.ref(_lib.desc(src[0])),
+                           _lib.ref(_lib.desc(dst[0])), _lib.ref(_lib.desc(src[1])),
+                           _lib.ref(_lib.desc(dst[1])), int(att_span))
+            tabs = [d if c else t for t, d, c in zip(tabs, dst, todo)]
+        return tabs
+    if any(t is not None and t.dim() == 4 for t in tabs):
+        raise ValueError("a chunk-major table needs a 16-bit dtype and chunk_major=True")
+    return [None if t is None else _lib.rows_aligned(t) for t in tabs]
 
 
 def flash_deberta_attention_fused(
