@@ -31,7 +31,8 @@ import torch
 import torch.nn.functional as F
 
 from kernels.activation import activation
-from kernels.dense_layernorm import dense_add_layernorm, pack_dense_weight
+from kernels.dense_layernorm import dense_add_layernorm
+from kernels.weight_pack import packed_weight
 from kernels.flash_deberta_attention import (flash_deberta_attention,
                                              flash_deberta_attention_fused, unit_steps)
 from kernels.fused_layernorm import fused_add_layernorm, fused_layernorm
@@ -52,9 +53,6 @@ class DebertaLayerWeights:
     bo2: torch.Tensor
     ln2_w: torch.Tensor  # output.LayerNorm
     ln2_b: torch.Tensor
-    # dense weights in the fused dense + LayerNorm kernel's layout, made on
-    # first use (name -> ((data_ptr, version), packed))
-    packed: dict = field(default_factory=dict, repr=False, compare=False)
 
 
 @dataclass
@@ -76,8 +74,7 @@ class DebertaWeights:
         return DebertaWeights(
             self.hidden, self.heads, self.inter, mv(self.rel_emb), mv(self.rel_ln_w),
             mv(self.rel_ln_b),
-            [DebertaLayerWeights(*(mv(getattr(l, f)) for f in DebertaLayerWeights.__dataclass_fields__
-                                   if f != "packed"))
+            [DebertaLayerWeights(*(mv(getattr(l, f)) for f in DebertaLayerWeights.__dataclass_fields__))
              for l in self.layers],
             self.position_buckets, self.max_relative_positions, self.eps)
 
@@ -137,13 +134,9 @@ def _attn_output(ctx: torch.Tensor, x: torch.Tensor, lw, eps: float,
     """attention.output (deberta_v2_encoder.py:504-508): LayerNorm(dense(ctx) +
     x) over [..., hidden], in one kernel when the shape allows it."""
     if fuse and _dense_ln_fits(lw.wo):
-        key = (lw.wo.data_ptr(), lw.wo._version)
-        cached = lw.packed.get("wo")
-        if cached is None or cached[0] != key:
-            cached = (key, pack_dense_weight(lw.wo))
-            lw.packed["wo"] = cached
+        # the packed copy is made once per weight tensor and version
         return dense_add_layernorm(ctx, None, lw.bo, x, lw.ln1_w, lw.ln1_b, eps,
-                                   packed_weight=cached[1])
+                                   packed_weight=packed_weight(lw.wo))
     return fused_add_layernorm(F.linear(ctx, lw.wo, lw.bo), x, lw.ln1_w, lw.ln1_b, eps,
                                return_sum=False)
 
@@ -245,7 +238,6 @@ class DebertaV1LayerWeights:
     bo2: torch.Tensor
     ln2_w: torch.Tensor
     ln2_b: torch.Tensor
-    packed: dict = field(default_factory=dict, repr=False, compare=False)
 
 
 @dataclass
@@ -264,8 +256,7 @@ class DebertaV1Weights:
         return DebertaV1Weights(
             self.hidden, self.heads, self.inter, mv(self.rel_emb),
             [DebertaV1LayerWeights(*(mv(getattr(l, f))
-                                     for f in DebertaV1LayerWeights.__dataclass_fields__
-                                     if f != "packed"))
+                                     for f in DebertaV1LayerWeights.__dataclass_fields__))
              for l in self.layers],
             self.max_relative_positions, self.eps)
 

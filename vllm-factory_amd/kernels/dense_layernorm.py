@@ -9,7 +9,8 @@ LayerNorm statistics are fp32 over that value plus the residual, as in
 `fused_add_layernorm`; the [M, N] projection never reaches memory.
 
 The kernel reads the weight in its MFMA operand order; `pack_dense_weight`
-makes that copy once per weight (`SelfOutput` caches it).
+makes that copy (`SelfOutput` keeps one per weight tensor and version through
+`weight_pack.packed_weight`).
 
 `SelfOutput` keeps the reference module's parameter names (`dense.weight`,
 `dense.bias`, `LayerNorm.weight`, `LayerNorm.bias`), so a DeBERTa state dict
@@ -22,7 +23,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from .weight_pack import pack_weight
+from .weight_pack import pack_weight, packed_weight
 
 
 def pack_dense_weight(weight: torch.Tensor) -> torch.Tensor:
@@ -102,22 +103,12 @@ class SelfOutput(torch.nn.Module):
         super().__init__()
         self.dense = torch.nn.Linear(in_features, hidden_size, bias=True, dtype=dtype, device=device)
         self.LayerNorm = torch.nn.LayerNorm(hidden_size, eps=eps, dtype=dtype, device=device)
-        self._packed = None
-        self._packed_key = None
-
-    def packed_weight(self) -> torch.Tensor:
-        """The packed dense weight, re-packed when the weight changes."""
-        w = self.dense.weight
-        key = (w.data_ptr(), w._version, w.dtype, w.device)
-        if self._packed is None or self._packed_key != key:
-            self._packed = pack_dense_weight(w.detach())
-            self._packed_key = key
-        return self._packed
 
     def forward(self, hidden_states: torch.Tensor, input_tensor: torch.Tensor) -> torch.Tensor:
+        # the packed copy is made once per weight tensor and version
         return dense_add_layernorm(hidden_states, None, self.dense.bias, input_tensor,
                                    self.LayerNorm.weight, self.LayerNorm.bias, self.LayerNorm.eps,
-                                   packed_weight=self.packed_weight())
+                                   packed_weight=packed_weight(self.dense.weight))
 
 
 __all__ = ["pack_dense_weight", "dense_add_layernorm", "SelfOutput"]
