@@ -79,7 +79,7 @@ def gliner_reps_packed(hidden: torch.Tensor, input_ids: torch.Tensor, words_mask
     class_idx = torch.empty(T + 1, dtype=torch.int32, device=dev)
     aux = torch.zeros(n + 5, dtype=torch.int32, device=dev)
     class_cu, status = aux[:n + 1], aux[n + 1:n + 3]
-    aux[n + 3:] = cu[[0, n]]  # endpoints, checked with the same read-back
+    aux[n + 3:].copy_(cu[::n])  # endpoints cu[0], cu[n], checked with the same read-back
     meta = torch.empty(4, dtype=torch.int32, device=dev)
     ws_bytes = int(lib.vfk_gliner_class_workspace_bytes(T))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
@@ -89,7 +89,8 @@ def gliner_reps_packed(hidden: torch.Tensor, input_ids: torch.Tensor, words_mask
                    status.data_ptr(), ws.data_ptr(), ws_bytes)
     word_src = torch.zeros(max(W, 1), dtype=torch.int32, device=dev)
     if W:
-        wcu = we_cu.to(device=dev, dtype=torch.int32)
+        # from pinned memory: the copy does not wait for the kernels above
+        wcu = we_cu.to(torch.int32).pin_memory().to(dev, non_blocking=True)
         _lib.on_device("vfk_gliner_word_index", dev, wm.data_ptr(), T, cu.data_ptr(), n,
                        wcu.data_ptr(), word_src.data_ptr(), status.data_ptr() + 4)
     host = aux.cpu()
