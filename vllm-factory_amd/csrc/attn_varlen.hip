@@ -80,11 +80,7 @@ constexpr int kPenLen = 2 * kPenOff;
 // kmax[h][s][kt].
 constexpr int kPackHeads = 6;
 
-__device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
+__device__ inline float wave_max(float v) { return group_max<64>(v); }
 
 template <typename E>
 __device__ inline float sumsq8(u32x4_t v) {
@@ -136,9 +132,7 @@ __global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int nkt)
       }
     }
     // squared row norm (the row's 4 threads form a quad), then the wave's max
-    nrm += __shfl_xor(nrm, 1);
-    nrm += __shfl_xor(nrm, 2);
-    nrm = wave_max(nrm);
+    nrm = wave_max(group_sum<4>(nrm));
     if (lane == 0) part[w][u] = nrm;
   }
   __syncthreads();

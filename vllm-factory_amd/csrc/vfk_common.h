@@ -160,6 +160,25 @@ __device__ inline float group_sum(float v) {
   return v;
 }
 
+// Max over aligned groups of LANES lanes, by the same exchange pattern.
+template <int LANES>
+__device__ inline float group_max(float v) {
+  static_assert(LANES >= 4 && LANES <= 64 && (LANES & (LANES - 1)) == 0, "group size");
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  if (LANES >= 8) v = fmaxf(v, dpp_f<0x141>(v));
+  if (LANES >= 16) v = fmaxf(v, dpp_f<0x140>(v));
+  if (LANES >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+  }
+  if (LANES >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+  }
+  return v;
+}
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
