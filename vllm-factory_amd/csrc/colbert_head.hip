@@ -54,11 +54,7 @@ __device__ inline void load4(const uint16_t* p, float (&f)[4]) {
   f[3] = E::to_f32((uint16_t)(v[1] >> 16));
 }
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ inline float wave_sum(float v) { return group_sum<64>(v); }
 
 // NCH = D / 256: 4-element chunks per lane and row. PACKED: a.w is the weight
 // in operand order [N/32][D/16][64][8].
