@@ -423,9 +423,12 @@ int vfk_colbert_head_fwd(const vfk_tensor* x, const vfk_tensor* residual,
 
 /* RoPE with a cos/sin table. Replaces kernels/fused_rope_global.py:18-142
  * (_fused_rope_kernel / fused_rope_apply).
- *   x, out [B,S,H,D]; cos, sin [B,S,D] (stride 0 broadcasts)
+ *   x, out [B,S,H,D], any strides, any even D; cos, sin [B,S,D] (stride 0
+ *   broadcasts) in x's dtype or fp32 (then used at fp32)
  * out[..d] = x[d] cos[d] - x[d+D/2] sin[d]        (d <  D/2)
- *          = x[d] cos[d] + x[d-D/2] sin[d]        (d >= D/2)            */
+ *          = x[d] cos[d] + x[d-D/2] sin[d]        (d >= D/2)
+ * The Python mirror uses it where vfk_rope_qk_fwd's D / alignment limits
+ * are not met (e.g. D = 36, 40 or 72 in 16 bits).                       */
 int vfk_rope_fwd(const vfk_tensor* x, const vfk_tensor* cos,
                  const vfk_tensor* sin, vfk_tensor* out, void* stream);
 

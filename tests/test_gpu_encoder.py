@@ -83,6 +83,8 @@ def test_modernbert_colbert_head_matches_unfused():
 
 # ---------------------------------------------------------------- config 5
 DEPTHS = (1, 4, 11, 22)
+# 1.25x the max-abs measured on MI355X at each depth (see the test below)
+MAX_ABS_BOUND = {1: 5.3e-2, 4: 9.8e-2, 11: 1.49e-1, 22: 1.69e-1}
 
 
 def _config5_subset(nseq=4):
@@ -117,8 +119,9 @@ def test_modernbert_config5_22_layers_match_oracle():
     rounds every activation; its error grows with depth roughly like the
     square root of the number of layers. Measured on MI355X at depths 1 / 4 /
     11 / 22: max-abs 4.2e-2 / 7.8e-2 / 1.19e-1 / 1.35e-1, cosine 0.999996 /
-    0.999987 / 0.999964 / 0.999925. Bound: max-abs 4e-2 * sqrt(depth) + 4e-2
-    (0.228 at 22) and cosine 0.9998 at every depth."""
+    0.999987 / 0.999964 / 0.999925. Bound: 1.25x the measured max-abs at each
+    depth (5.3e-2 / 9.8e-2 / 1.49e-1 / 1.69e-1), so a change that adds a
+    fifth to the error fails, and cosine 0.9998 at every depth."""
     import encoders.modernbert as em
     ids, cu, mx, _ = _config5_subset()
     w = em.random_weights()
@@ -130,7 +133,7 @@ def test_modernbert_config5_22_layers_match_oracle():
         assert torch.isfinite(got).all()
         err = (got - want[k]).abs().max().item()
         cs = cosine(got, want[k])
-        bound = 4e-2 * k ** 0.5 + 4e-2
+        bound = MAX_ABS_BOUND[k]
         print(f"config 5, {k} layers: max-abs {err:.3e} (bound {bound:.3e}) cosine {cs:.6f}",
               flush=True)
         assert err <= bound and cs >= 0.9998, (k, err, cs)

@@ -283,3 +283,64 @@ def test_colbert_project_residual_stack(dev):
     # the intermediate GEMM outputs are rounded to bf16 twice per layer
     assert min(cosine(got[i], want[i]) for i in range(257)) >= 0.9995
     torch.testing.assert_close(got.norm(dim=-1), torch.ones(257), atol=5e-3, rtol=0)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 40), (torch.bfloat16, 72),
+                                     (torch.bfloat16, 36), (torch.float16, 40),
+                                     (torch.float32, 36)])
+@pytest.mark.parametrize("table", ["fp32", "same"])
+def test_rope_head_dims_outside_chunking(dev, dtype, D, table):
+    """Head dims the one-launch q/k kernel does not chunk (D not a multiple of
+    16 in 16 bits, of 8 in fp32) still work as in the reference, which takes
+    any even D: the drop-ins route them through the general kernel. q as a
+    strided view of a fused projection, k contiguous; fp32 tables are used at
+    fp32, tables in the input's dtype as given. Every element equals the
+    oracle's fp32 result rounded once."""
+    from kernels.fused_rope_global import fused_rope_apply, fused_rope_global_apply
+    from kernels.fused_rope_local import fused_rope_local_apply
+    from oracle.attention import rope_cos_sin
+    B, S = 2, 131
+    qkv = _rand((B, S, 3, 5, D), dtype, 31)
+    k = _rand((B, S, 7, D), dtype, 32)
+    cos, sin = rope_cos_sin(torch.arange(S) * 3 + 2, 10000.0, D)
+    if table == "same":
+        cos, sin = cos.to(dtype), sin.to(dtype)
+    q = qkv[:, :, 0]
+    for fn in (fused_rope_global_apply, fused_rope_local_apply):
+        gq, gk = fn(qkv.to(dev)[:, :, 0], k.to(dev), cos.to(dev), sin.to(dev))
+        for got, x in ((gq, q), (gk, k)):
+            want = oe.rope_table(x, cos[None], sin[None]).to(dtype)
+            assert got.is_contiguous() and got.shape == x.shape
+            assert torch.equal(got.cpu(), want), f"{fn.__name__} {dtype} D={D} {table}"
+    one = fused_rope_apply(k.to(dev), cos[None].to(dev), sin[None].to(dev))
+    assert torch.equal(one.cpu(), oe.rope_table(k, cos[None], sin[None]).to(dtype))
+
+
+def test_packed_weights_under_inference_mode(dev):
+    """Weights built under torch.inference_mode() (as a model loaded and run
+    by vLLM has them) through the packed-weight paths, called inside
+    inference mode twice: colbert_head (pack=True) and SelfOutput."""
+    from kernels.colbert_head import colbert_head
+    from kernels.dense_layernorm import SelfOutput
+    from oracle.epilogues import dense_residual_layernorm
+    from _tol import cosine
+    x = _rand((200, 768), torch.bfloat16, 71)
+    w = _rand((128, 768), torch.bfloat16, 72, 0.05)
+    with torch.inference_mode():
+        wd = w.to(dev)
+        mod = SelfOutput(768, 768, eps=1e-7, dtype=torch.bfloat16, device=dev)
+        mod.dense.weight.copy_(_rand((768, 768), torch.bfloat16, 73, 768 ** -0.5).to(dev))
+        mod.dense.bias.copy_(_rand((768,), torch.bfloat16, 74, 0.5).to(dev))
+    assert wd.is_inference()
+    want = oe.colbert_head(x, [(w, None, None, False)], layer_norm=False)
+    r = _rand((200, 768), torch.bfloat16, 75)
+    for _ in range(2):
+        with torch.inference_mode():
+            got = colbert_head(x.to(dev), wd)
+            y = mod(x.to(dev), r.to(dev))
+        _colbert_rows_close(got, want, "colbert head, inference-mode weight")
+        ref = dense_residual_layernorm(x, mod.dense.weight.cpu(), mod.dense.bias.cpu(), r,
+                                       mod.LayerNorm.weight.cpu(), mod.LayerNorm.bias.cpu(), 1e-7,
+                                       round_dtype=torch.bfloat16)
+        err = (y.float().cpu() - ref).abs().max().item()
+        assert err <= 6e-2 and cosine(y.float().cpu(), ref) >= 0.9999, err

@@ -38,22 +38,27 @@ def test_config1_16bit(dev, dtype):
     assert_attn_close(got, want, f"cfg1 {dtype}")
 
 
-def test_config4_attention_subset(dev):
-    """mT5-large shapes: 4 of the 32 sequences at L=768 against the oracle."""
-    g = torch.Generator().manual_seed(4)
-    B, H, L = 4, 16, 768
-    lengths = torch.tensor([768, 512, 700, 601])
-    q, k, v = (torch.randn(B, H, L, 64, generator=g) * 0.64 for _ in range(3))
-    q, k, v = (t.bfloat16() for t in (q, k, v))
-    table = (torch.randn(32, H, generator=g) * 0.1).bfloat16()
-    keep = (torch.arange(L)[None] < lengths[:, None]).bfloat16()
-    mask = ((1.0 - keep) * torch.finfo(torch.bfloat16).min)[:, None, None, :]
-    want = oa.rpb_attention(q, k, v, table, 32, 128, False, mask, 1.0)
-    got = _rpb()(q.to(dev), k.to(dev), v.to(dev), table.to(dev), 32, 128, False,
-                 padding_mask=mask.to(dev))
-    for b in range(B):
-        n = int(lengths[b])
-        assert_attn_close(got[b, :, :n], want[b, :, :n], f"cfg4 batch {b}")
+def test_config4_attention_all_sequences(dev):
+    """Config 4 (mT5-large, B = 32, L = 768, lengths U{512..768}): q, k, v
+    projected from the config's hidden states and Wq / Wk / Wv, the config's
+    [32, 16] table and [B, 1, 1, L] key mask; every valid row of all 32
+    sequences against the oracle (four batch rows per oracle call)."""
+    c = workloads.config4(device=dev)
+    B, L, D = c.hidden.shape
+    H = c.table.shape[1]
+    q, k, v = ((c.hidden @ w).view(B, L, H, 64).transpose(1, 2) for w in (c.wq, c.wk, c.wv))
+    got = _rpb()(q, k, v, c.table, 32, 128, False, padding_mask=c.mask).cpu()
+    table, mask = c.table.cpu(), c.mask.cpu()
+    worst = 0.0
+    for b0 in range(0, B, 4):
+        sl = slice(b0, b0 + 4)
+        want = oa.rpb_attention(q[sl].cpu(), k[sl].cpu(), v[sl].cpu(), table, 32, 128, False,
+                                mask[sl], 1.0)
+        for i in range(want.shape[0]):
+            n = int(c.lengths[b0 + i])
+            err, _ = assert_attn_close(got[b0 + i, :, :n], want[i, :, :n], f"cfg4 batch {b0 + i}")
+            worst = max(worst, err)
+    print(f"config 4: {B} sequences, max-abs {worst:.3e}")
 
 
 def test_config4_full_size_properties(dev):

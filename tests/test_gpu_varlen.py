@@ -51,18 +51,23 @@ def test_varlen_key_valid_mask(dev, window):
 
 
 @pytest.mark.parametrize("window,theta", [(-1, 160000.0), (64, 10000.0)])
-def test_config2_subset(dev, window, theta):
-    """Config 2 (64 sequences, 512..768 tokens): 6 sequences checked exactly."""
+def test_config2_all_sequences(dev, window, theta):
+    """Config 2 (64 sequences, 512..768 tokens, T = 40 265), the benchmark's
+    own pack: every sequence against the oracle run on it alone."""
     c = workloads.config2(device=dev)
     qkv = c.qkv
-    got = _vl()(qkv[:, 0], qkv[:, 1], qkv[:, 2], c.cu_seqlens, c.max_seqlen, window, theta, 0.125)
+    got = _vl()(qkv[:, 0], qkv[:, 1], qkv[:, 2], c.cu_seqlens, c.max_seqlen, window, theta,
+                0.125).cpu()
     cu = c.cu_seqlens.cpu()
-    for s in (0, 1, 17, 31, 50, 63):
+    worst = 0.0
+    for s in range(len(cu) - 1):
         a, b = int(cu[s]), int(cu[s + 1])
         sub = qkv[a:b].cpu()
         want = oa.varlen_attention(sub[:, 0], sub[:, 1], sub[:, 2],
                                    torch.tensor([0, b - a], dtype=torch.int32), window, theta, None, 0.125)
-        assert_attn_close(got[a:b], want, f"cfg2 seq {s} w={window}")
+        err, _ = assert_attn_close(got[a:b], want, f"cfg2 seq {s} w={window}")
+        worst = max(worst, err)
+    print(f"config 2 window={window}: {len(cu) - 1} sequences, max-abs {worst:.3e}")
 
 
 def test_config2_full_properties(dev):

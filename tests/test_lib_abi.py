@@ -342,3 +342,52 @@ def test_rel_chunk_major_layout_and_checks():
         f(d(torch.zeros(H, 8, 500, 8, dtype=bf)), None)
     with pytest.raises(NotImplementedError, match="16-bit"):
         f(d(cmt.float()), None, q.float())
+
+
+def test_deberta_flash_flag_is_set():
+    """The reference's DeBERTa v2 and v1 models take their flash path only when
+    `HAS_TRITON` imported from kernels.flash_deberta_attention is true
+    (models/deberta_v2/deberta_v2_encoder.py:39-42, :201, :230;
+    models/deberta/deberta_encoder.py:35-38, :202, :227): the same import
+    here must give a true flag and the kernel entry point."""
+    from kernels.flash_deberta_attention import HAS_TRITON, flash_deberta_attention
+    assert HAS_TRITON is True
+    assert callable(flash_deberta_attention)
+
+
+def test_packed_weight_cache_with_inference_tensors(monkeypatch):
+    """packed_weight on a weight made under torch.inference_mode() (no version
+    counter) packs once and reuses the copy, also when called inside
+    inference mode; an ordinary weight re-packs after an in-place update; a
+    new tensor object packs again. The pack itself is a stand-in here (the
+    real one needs the GPU): only the cache logic is under test."""
+    from kernels import weight_pack as wp
+    calls = []
+
+    def fake_pack(w):
+        calls.append(w)
+        return w.clone()
+
+    monkeypatch.setattr(wp, "pack_weight", fake_pack)
+    wp.clear_cache()
+    with torch.inference_mode():
+        w_inf = torch.randn(64, 32)
+    assert w_inf.is_inference()
+    a = wp.packed_weight(w_inf)
+    with torch.inference_mode():
+        b = wp.packed_weight(w_inf)
+    assert a is b and len(calls) == 1
+    w = torch.randn(64, 32)
+    c = wp.packed_weight(w)
+    assert wp.packed_weight(w) is c and len(calls) == 2
+    w.add_(1.0)
+    d = wp.packed_weight(w)
+    assert d is not c and len(calls) == 3 and torch.equal(d, w)
+    with torch.inference_mode():
+        tmp = w_inf * 2            # a per-call temporary: its own entry
+        e = wp.packed_weight(tmp)
+    assert len(calls) == 4 and torch.equal(e, w_inf * 2)
+    wp.clear_cache()
+    wp.packed_weight(w_inf)
+    assert len(calls) == 5
+    wp.clear_cache()

@@ -287,3 +287,29 @@ def test_deberta_v1_oracle_matches_transformers(L, max_rel):
         # even in a float64 model, so outputs agree to ~1e-6; a missing c2p/p2c
         # term, a wrong clamp or span slice differs by O(1e-2)
         torch.testing.assert_close(got[b, :n], want[b, :n], rtol=0, atol=5e-6)
+
+
+def test_mt5_fused_layer_weights_cached():
+    """encoders.mt5.fused_layer_weights builds the q|k|v concatenation and the
+    stacked GLU weight once per weight set (same objects on the next call,
+    also for weights made under inference mode), rebuilds after an in-place
+    update, and equals the plain torch constructions."""
+    from encoders.mt5 import fused_layer_weights, stack_glu_weight
+    g = torch.Generator().manual_seed(5)
+    D, F_ = 128, 192
+    mk = lambda *s: (torch.randn(*s, generator=g) * 0.02).bfloat16()
+    lw = [mk(D, D), mk(D, D), mk(D, D), mk(D, D), mk(D, F_), mk(D, F_), mk(F_, D), None, None]
+    a = fused_layer_weights(lw)
+    assert torch.equal(a[0], torch.cat(lw[:3], 1))
+    assert torch.equal(a[1], torch.cat((lw[4].t(), lw[5].t()), 0))
+    assert torch.equal(a[1], stack_glu_weight(lw[4], lw[5]))
+    b = fused_layer_weights(lw)
+    assert b[0] is a[0] and b[1] is a[1]
+    lw[1].add_(1.0)
+    c = fused_layer_weights(lw)
+    assert c[0] is not a[0] and torch.equal(c[0], torch.cat(lw[:3], 1))
+    with torch.inference_mode():
+        li = [t.clone() if t is not None else None for t in lw]
+        d = fused_layer_weights(li)
+        e = fused_layer_weights(li)
+    assert d[0] is e[0] and torch.equal(d[0], c[0])

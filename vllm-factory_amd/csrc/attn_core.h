@@ -410,6 +410,16 @@ __device__ inline void store_out_rows(uint16_t* __restrict__ stage, f32x16_t o0,
   }
 }
 
+// Rows [from, to) of one 64-wide 16-bit output slice (row stride rs
+// elements, rows 16-byte aligned) written as zeros, eight lanes per 128-byte
+// row: the rows of a packed sequence longer than max_seqlen, which the
+// varlen kernels do not compute.
+__device__ inline void zero_rows_d64(uint16_t* __restrict__ base, int64_t rs, int from, int to) {
+  const u32x4_t z = {0u, 0u, 0u, 0u};
+  for (int r = from + (int)(threadIdx.x >> 3); r < to; r += (int)(blockDim.x >> 3))
+    *reinterpret_cast<u32x4_t*>(base + (int64_t)r * rs + 8 * (threadIdx.x & 7)) = z;
+}
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 

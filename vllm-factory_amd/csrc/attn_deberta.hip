@@ -482,9 +482,14 @@ __global__ __launch_bounds__(256, 2) void deberta_fused_kernel(DebArgs a) {
   int64_t qb, kb, vb, ob;
   if (a.cu) {
     const int tok0 = a.cu[b];
-    len = mrows = min(max(a.cu[b + 1] - tok0, 0), a.N);
+    const int nfull = a.cu[b + 1] - tok0;
+    len = mrows = min(max(nfull, 0), a.N);
     qb = (int64_t)tok0 * a.qs[2]; kb = (int64_t)tok0 * a.ks[2];
     vb = (int64_t)tok0 * a.vs[2]; ob = (int64_t)tok0 * a.os[2];
+    // rows past max_seqlen (a.N) are not computed: the last query tile
+    // writes them as zeros
+    if (qt == nqt - 1 && nfull > len)
+      zero_rows_d64(reinterpret_cast<uint16_t*>(a.o) + ob + h * a.os[1], a.os[2], len, nfull);
   } else {
     len = a.seq_lengths ? min(max(a.seq_lengths[b], 0), a.N) : a.N;
     mrows = a.M;

@@ -171,12 +171,15 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   int64_t qo = b * a.qs[0], ko = b * a.ks[0], vo = b * a.vs[0], oo = b * a.os[0];
   if (a.cu) {
     const int tok0 = a.cu[b];
-    // rows past max_seqlen (a.Lq) are not computed: the LDS tables are sized
-    // for a.Lk keys
-    Lq = Lk = min(a.cu[b + 1] - tok0, a.Lq);
-    if (q0 >= Lq) return;  // whole workgroup: uniform exit
+    // rows past max_seqlen (a.Lq) are not computed (the LDS tables are sized
+    // for a.Lk keys): the last query tile writes them as zeros
+    const int nfull = a.cu[b + 1] - tok0;
+    Lq = Lk = min(nfull, a.Lq);
     qo = (int64_t)tok0 * a.qs[2]; ko = (int64_t)tok0 * a.ks[2];
     vo = (int64_t)tok0 * a.vs[2]; oo = (int64_t)tok0 * a.os[2];
+    if (qt == nqt - 1 && nfull > Lq)
+      zero_rows_d64(reinterpret_cast<uint16_t*>(a.o) + oo + h * a.os[1], a.os[2], Lq, nfull);
+    if (q0 >= Lq) return;  // whole workgroup: uniform exit
   }
   // the host sizes the dynamic LDS for a.Lk keys, an upper bound of Lk
   const int ntiles_all = (Lk + kBN - 1) / kBN;

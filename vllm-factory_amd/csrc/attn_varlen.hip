@@ -41,6 +41,8 @@ struct VarlenArgs {
                             // (kblk32) of each 32-token block of the stream [H][ceil(T / 32)]
   int nkt;                  // key tiles per sequence slot: ceil(max_seqlen / 64)
   int kblk32;               // kmax holds 32-token stream blocks (K from the fused projection)
+  int maxlen;               // max_seqlen: longer sequences are cut there, their
+                            // rows past it written as zeros
   int64_t T;
 };
 
@@ -98,14 +100,22 @@ __global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int nkt)
   const int kt = blockIdx.x % nkt;
   const int s = blockIdx.x / nkt;
   const int tok0 = a.cu[s];
-  const int n = a.cu[s + 1] - tok0;
+  const int nfull = a.cu[s + 1] - tok0;
+  const int n = min(nfull, a.maxlen);
+  const int h0 = blockIdx.y * kPackHeads;
+  if (kt == nkt - 1 && nfull > n) {
+    // a sequence longer than max_seqlen: the attention computes its first
+    // max_seqlen rows; the rest of its output rows become zeros here
+    for (int u = 0; u < kPackHeads && h0 + u < a.H; ++u)
+      zero_rows_d64(reinterpret_cast<uint16_t*>(a.o) + (int64_t)tok0 * a.os[0] + (h0 + u) * a.os[1],
+                    a.os[0], n, nfull);
+  }
   if (kt * 64 >= n) return;  // uniform: no row of the sequence in this tile
   const int row = kt * 64 + (threadIdx.x >> 2);
   const bool valid = row < n;
   const int rr = valid ? row : kt * 64;  // tail threads load a valid row, store nothing
   const int cp = threadIdx.x & 3;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int h0 = blockIdx.y * kPackHeads;
   RopeK rk;
   rope_k_fetch(rk, a.rope, rr, true);
   const uint16_t* src = reinterpret_cast<const uint16_t*>(a.k) + (int64_t)(tok0 + rr) * a.ks[0] + 8 * cp;
@@ -141,6 +151,18 @@ __global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int nkt)
     const float m = fmaxf(fmaxf(part[0][t], part[1][t]), fmaxf(part[2][t], part[3][t]));
     a.kmax[((int64_t)(h0 + t) * a.nseq + s) * a.nkt + kt] = sqrtf(m);
   }
+}
+
+// Output rows past max_seqlen of every (sequence, head), as zeros: block
+// (s, h). Launched by the attention over the fused projection's K, where no
+// pre-pass runs.
+__global__ __launch_bounds__(256) void zero_cut_rows_kernel(VarlenArgs a) {
+  const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
+  const int tok0 = a.cu[s];
+  const int nfull = a.cu[s + 1] - tok0;
+  if (nfull > a.maxlen)
+    zero_rows_d64(reinterpret_cast<uint16_t*>(a.o) + (int64_t)tok0 * a.os[0] + h * a.os[1],
+                  a.os[0], a.maxlen, nfull);
 }
 
 template <typename E, bool ROPE, bool LOCAL, bool KVALID>
@@ -229,9 +251,18 @@ __global__ __launch_bounds__(256, (LOCAL && KVALID) ? 3 : 4) void varlen_fwd_ker
   const int h = (work / a.nqt) % a.H;
   const int s = work / (a.nqt * a.H);
   const int tok0 = a.cu[s];
-  const int n = a.cu[s + 1] - tok0;
+  const int nfull = a.cu[s + 1] - tok0;
+  const int n = min(nfull, a.maxlen);
   const int q0 = qt * kBM;
-  if (q0 >= n) return;  // whole workgroup: uniform exit
+  // rows past max_seqlen are written as zeros: without RoPE by the last
+  // query tile, with RoPE by the K pre-pass (or, after the fused projection,
+  // by zero_cut_rows_kernel), which keeps the RoPE kernels' registers free
+  if (q0 >= n) {  // whole workgroup: uniform exit
+    if (!ROPE && qt == a.nqt - 1 && nfull > n)
+      zero_rows_d64(reinterpret_cast<uint16_t*>(a.o) + (int64_t)tok0 * a.os[0] + h * a.os[1],
+                    a.os[0], n, nfull);
+    return;
+  }
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, hl = lane >> 5;
   const uint16_t* Qp = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)tok0 * a.qs[0] + h * a.qs[1];
@@ -319,6 +350,7 @@ __global__ __launch_bounds__(256, (LOCAL && KVALID) ? 3 : 4) void varlen_fwd_ker
   store_out_rows<E>((w < 2 ? K0 : K1) + (w & 1) * 2048, o0, o1, l_tot,
                     [&](int r) { return ob + (int64_t)(wq_lo + r) * a.os[0]; },
                     [&](int r) { return wq_lo + r < n; });
+  if (!ROPE && qt == a.nqt - 1 && nfull > n) zero_rows_d64(ob, a.os[0], n, nfull);
 }
 
 // fp32: one thread per query row, exact fp32 arithmetic, accurate sin/cos.
@@ -330,8 +362,14 @@ __global__ __launch_bounds__(64) void varlen_fwd_f32_kernel(VarlenArgs a) {
   const int h = (blockIdx.x / nqt64) % a.H;
   const int s = blockIdx.x / (nqt64 * a.H);
   const int tok0 = a.cu[s];
-  const int n = a.cu[s + 1] - tok0;
+  const int nfull = a.cu[s + 1] - tok0;
+  const int n = min(nfull, a.maxlen);
   const int q0 = qt * 64;
+  if (qt == nqt64 - 1 && nfull > n) {  // rows past max_seqlen: zeros
+    float* ob = reinterpret_cast<float*>(a.o) + (int64_t)tok0 * a.os[0] + h * a.os[1];
+    for (int e = threadIdx.x; e < (nfull - n) * kHD; e += 64)
+      ob[(int64_t)(n + e / kHD) * a.os[0] + e % kHD] = 0.f;
+  }
   if (q0 >= n) return;
   const int qrow = q0 + threadIdx.x;
   const bool qvalid = qrow < n;
@@ -467,7 +505,7 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
     a.qs[i] = q->stride[i]; a.ks[i] = k->stride[i];
     a.vs[i] = v->stride[i]; a.os[i] = out->stride[i];
   }
-  a.cu = cu_seqlens; a.nseq = num_seqs; a.H = (int)H; a.T = T;
+  a.cu = cu_seqlens; a.nseq = num_seqs; a.H = (int)H; a.T = T; a.maxlen = max_seqlen;
   a.window = window < 0 ? -1 : window;
   if (!(softmax_scale > 0.f) || !isfinite(softmax_scale))
     return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: softmax_scale must be > 0");
@@ -552,7 +590,7 @@ extern "C" int vfk_varlen_attn_krot_fwd(const vfk_tensor* q, const vfk_tensor* v
   for (int i = 0; i < 2; ++i) {
     a.qs[i] = q->stride[i]; a.vs[i] = v->stride[i]; a.os[i] = out->stride[i];
   }
-  a.cu = cu_seqlens; a.nseq = num_seqs; a.H = (int)H; a.T = T;
+  a.cu = cu_seqlens; a.nseq = num_seqs; a.H = (int)H; a.T = T; a.maxlen = max_seqlen;
   a.window = window < 0 ? -1 : window;
   a.c2 = softmax_scale * VFK_LOG2E;
   a.key_valid = key_valid;
@@ -563,6 +601,11 @@ extern "C" int vfk_varlen_attn_krot_fwd(const vfk_tensor* q, const vfk_tensor* v
   const int64_t span = (int64_t)max_seqlen * 2;
   if (span * 64 >= (1ll << 31) || span * a.vs[0] >= (1ll << 31))
     return set_error(VFK_ERR_UNSUPPORTED, "%s: max_seqlen x row stride too large", nm);
+  if ((int64_t)num_seqs * H >= (1ll << 31))
+    return set_error(VFK_ERR_UNSUPPORTED, "%s: grid too large", nm);
+  // rows past max_seqlen (no pre-pass runs on this path to clear them)
+  hipLaunchKernelGGL(zero_cut_rows_kernel, dim3((unsigned)(num_seqs * H)), dim3(256), 0,
+                     (hipStream_t)stream, a);
   return launch_varlen(a, dt, true, max_seqlen, (hipStream_t)stream, nm);
 }
 

@@ -683,9 +683,11 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs p) {
   }
 }
 
-template <int DT>
+// Any strides and any even D; cos / sin in the element type or fp32 (CT).
+template <int DT, int CT>
 __global__ __launch_bounds__(256) void rope_scalar_kernel(RopeArgs p) {
   using L = Elt<DT>;
+  using LC = Elt<CT>;
   const int half = p.D / 2;
   const int64_t total = p.B * p.S * p.H * p.D;
   for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total;
@@ -699,9 +701,14 @@ __global__ __launch_bounds__(256) void rope_scalar_kernel(RopeArgs p) {
     const float x = L::ld1(p.x, xo + d * p.xs[3]);
     const int pd = d < half ? d + half : d - half;
     const float xp = L::ld1(p.x, xo + pd * p.xs[3]);
-    const float c = L::ld1(p.c, b * p.cs[0] + s * p.cs[1] + d * p.cs[2]);
-    const float sn = L::ld1(p.s, b * p.ss[0] + s * p.ss[1] + d * p.ss[2]);
-    const float y = d < half ? x * c - xp * sn : x * c + xp * sn;
+    const float c = LC::ld1(p.c, b * p.cs[0] + s * p.cs[1] + d * p.cs[2]);
+    const float sn = LC::ld1(p.s, b * p.ss[0] + s * p.ss[1] + d * p.ss[2]);
+    float y;
+    {
+      // products rounded separately, as in the unfused fp32 formula
+#pragma clang fp contract(off)
+      y = d < half ? x * c - xp * sn : x * c + xp * sn;
+    }
     L::st1(p.y, b * p.ys[0] + s * p.ys[1] + h * p.ys[2] + d * p.ys[3], y);
   }
 }
@@ -914,9 +921,12 @@ extern "C" int vfk_rope_fwd(const vfk_tensor* x, const vfk_tensor* cos,
   for (const vfk_tensor* t : cs) {
     if ((t->size[0] != B && t->size[0] != 1) || t->size[1] != S || t->size[2] != D)
       return set_error(VFK_ERR_INVALID, "vfk_rope_fwd: cos/sin must be [B|1,S,D]");
-    if (t->dtype != x->dtype)
-      return set_error(VFK_ERR_INVALID, "vfk_rope_fwd: cos/sin dtype must match x");
+    if (t->dtype != x->dtype && t->dtype != VFK_F32)
+      return set_error(VFK_ERR_INVALID, "vfk_rope_fwd: cos/sin dtype must be x's or fp32");
   }
+  if (cos->dtype != sin->dtype)
+    return set_error(VFK_ERR_INVALID, "vfk_rope_fwd: cos and sin dtypes differ");
+  const bool f32t = cos->dtype == VFK_F32 && x->dtype != VFK_F32;
   if (out->dtype != x->dtype)
     return set_error(VFK_ERR_INVALID, "vfk_rope_fwd: out dtype must match x");
   RopeArgs p = {};
@@ -929,7 +939,7 @@ extern "C" int vfk_rope_fwd(const vfk_tensor* x, const vfk_tensor* cos,
   const int64_t rows = B * S * H;
   if (rows == 0) return VFK_OK;
   const int VEC = 16 / elem_size(x->dtype);
-  bool vec_ok = (D / 2) % VEC == 0 && x->stride[3] == 1 && out->stride[3] == 1 &&
+  bool vec_ok = !f32t && (D / 2) % VEC == 0 && x->stride[3] == 1 && out->stride[3] == 1 &&
                 cos->stride[2] == 1 && sin->stride[2] == 1 &&
                 aligned16(x->data) && aligned16(out->data) &&
                 aligned16(cos->data) && aligned16(sin->data);
@@ -953,8 +963,10 @@ extern "C" int vfk_rope_fwd(const vfk_tensor* x, const vfk_tensor* cos,
                        gs, (uint32_t)work);                                        \
   else if (vec_ok)                                                                 \
     hipLaunchKernelGGL((rope_vec_kernel<DT>), dim3((unsigned)blocks), dim3(256), 0, st, p); \
+  else if (f32t)                                                                   \
+    hipLaunchKernelGGL((rope_scalar_kernel<DT, VFK_F32>), dim3((unsigned)blocks), dim3(256), 0, st, p); \
   else                                                                             \
-    hipLaunchKernelGGL((rope_scalar_kernel<DT>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((rope_scalar_kernel<DT, DT>), dim3((unsigned)blocks), dim3(256), 0, st, p);
   switch (x->dtype) {
     case VFK_F32: VFK_ROPE(VFK_F32); break;
     case VFK_BF16: VFK_ROPE(VFK_BF16); break;

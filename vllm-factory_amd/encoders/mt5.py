@@ -16,6 +16,7 @@ residual add is fused into the second RMSNorm and the second into the wo GEMM
 """
 from __future__ import annotations
 
+import weakref
 from typing import Optional
 
 import torch
@@ -82,6 +83,28 @@ def mt5_layer_packed(x: torch.Tensor, cu_seqlens: torch.Tensor, max_len: int, wq
     return torch.addmm(x1, g, wff_o)
 
 
+_FUSED: dict = {}
+
+
+def fused_layer_weights(lw):
+    """(wqkv, wi_glu) of one layer tuple (wq, wk, wv, wo, wi0, wi1, ...): the
+    [D, 3D] q|k|v concatenation and stack_glu_weight(wi0, wi1), made once per
+    weight set and kept while the weights live. Keyed by the five source
+    tensors and their version counters, so an in-place update rebuilds;
+    tensors made under inference mode carry no version counter and are keyed
+    by the objects alone."""
+    srcs = (lw[0], lw[1], lw[2], lw[4], lw[5])
+    key = tuple(id(t) for t in srcs)
+    vers = tuple(-1 if t.is_inference() else t._version for t in srcs)
+    hit = _FUSED.get(key)
+    if hit is not None and hit[1] == vers and all(r() is t for r, t in zip(hit[0], srcs)):
+        return hit[2]
+    val = (torch.cat(lw[:3], 1), stack_glu_weight(lw[4], lw[5]))
+    refs = tuple(weakref.ref(t, lambda _r, k=key: _FUSED.pop(k, None)) for t in srcs)
+    _FUSED[key] = (refs, vers, val)
+    return val
+
+
 def stack_glu_weight(wi0: torch.Tensor, wi1: torch.Tensor) -> Optional[torch.Tensor]:
     """[D, d_ff] wi0, wi1 ([in, out]) -> the [2 d_ff, D] weight of glu_linear,
     or None where glu_linear does not take the shapes (D a multiple of 64,
@@ -123,8 +146,9 @@ def mt5_encoder_forward(input_ids: Optional[torch.Tensor], attention_mask: Optio
         T = int(cu[-1])
         xf = unpad_packed(x, cu, T)
         for lw in layers:
+            wqkv, wi_glu = fused_layer_weights(lw)
             xf = mt5_layer_packed(xf, cu, L, *lw, table, None, num_buckets, max_distance, eps,
-                                  wqkv=torch.cat(lw[:3], 1), wi_glu=stack_glu_weight(lw[4], lw[5]))
+                                  wqkv=wqkv, wi_glu=wi_glu)
         x, _ = pad_packed(rms_norm(xf, final_ln, eps), cu, B, L)
         return x.squeeze(0) if squeeze else x
     for lw in layers:
@@ -165,6 +189,7 @@ def mt5_encoder_flat(x: torch.Tensor, positions: torch.Tensor, layers, table: to
     cu, meta = seq_metadata(positions, "zero")
     cu, n, max_len, _ = read_metadata(cu, meta)
     for lw in layers:
+        wqkv, wi_glu = fused_layer_weights(lw)
         x = mt5_layer_packed(x, cu, max_len, *lw, table, None, num_buckets, max_distance, eps,
-                             wqkv=torch.cat(lw[:3], 1), wi_glu=stack_glu_weight(lw[4], lw[5]))
+                             wqkv=wqkv, wi_glu=wi_glu)
     return x

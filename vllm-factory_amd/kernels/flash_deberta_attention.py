@@ -3,7 +3,8 @@
 Drop-in for kernels/flash_deberta_attention.py:455-507: `flash_deberta_attention`
 with the same signature, defaults and output convention (a new [B, H, M, D]
 tensor whose rows >= seq_lengths[b] are zero), plus `clear_config_cache` and
-`HAS_TRITON` for import compatibility. Scores follow
+`HAS_TRITON` (true: the reference's models gate their flash path on it).
+Scores follow
     s(i, j) = (q_i.k_j + pos_key[i, c(i-j)] + pos_query[j, c(i-j)]) * sm_scale,
     c(d) = clamp(bucket(d) + att_span, 0, 2 att_span - 1),
 with the log bucket of models/deberta_v2/deberta_v2_encoder.py:70-89 evaluated
@@ -25,9 +26,13 @@ import torch
 
 from . import _lib
 
-# The reference exports whether its Triton path is usable; this package has no
-# Triton path (the HIP kernels are the only implementation).
-HAS_TRITON = False
+# The reference's DeBERTa models read this flag as "the flash kernel is
+# available" (models/deberta_v2/deberta_v2_encoder.py:39-42, :201, :230;
+# models/deberta/deberta_encoder.py:35-38, :202, :227) and take their eager
+# [B*H, L, L] path when it is false. The flash kernel here is the HIP one, so
+# the flag is true: with this package on the import path those models call
+# flash_deberta_attention. (There is no Triton code in this package.)
+HAS_TRITON = True
 
 
 def clear_config_cache() -> None:

@@ -8,7 +8,10 @@ LayerNorm block, the ColBERT head) read it as [N/32, K/16, 64, 8]: block
 `packed_weight` keeps one packed copy per live weight tensor: the entry is
 keyed by the tensor object (a weak reference) and its version counter, so an
 in-place update of the weight, or a new tensor at the same address,
-re-packs.
+re-packs. Tensors made under torch.inference_mode() (vLLM runs its forward
+there) have no version counter: their entry is keyed by the object alone, so
+an in-place update of such a weight inside inference mode is not seen; call
+`clear_cache()` after one.
 """
 from __future__ import annotations
 
@@ -37,16 +40,27 @@ def pack_weight(weight: torch.Tensor) -> torch.Tensor:
 _CACHE: dict = {}
 
 
+def _version(weight: torch.Tensor) -> int:
+    # inference tensors carry no version counter (reading it raises)
+    return -1 if weight.is_inference() else weight._version
+
+
 def packed_weight(weight: torch.Tensor) -> torch.Tensor:
     """pack_weight(weight), made once per weight tensor and version."""
     key = id(weight)
+    ver = _version(weight)
     hit = _CACHE.get(key)
-    if hit is not None and hit[0]() is weight and hit[1] == weight._version:
+    if hit is not None and hit[0]() is weight and hit[1] == ver:
         return hit[2]
     packed = pack_weight(weight.detach())
-    _CACHE[key] = (weakref.ref(weight, lambda _r, k=key: _CACHE.pop(k, None)), weight._version,
-                   packed)
+    _CACHE[key] = (weakref.ref(weight, lambda _r, k=key: _CACHE.pop(k, None)), ver, packed)
     return packed
 
 
-__all__ = ["pack_weight", "packed_weight"]
+def clear_cache() -> None:
+    """Drops every packed copy (e.g. after an in-place update of a weight
+    made under inference mode, which has no version counter)."""
+    _CACHE.clear()
+
+
+__all__ = ["pack_weight", "packed_weight", "clear_cache"]
