@@ -697,12 +697,28 @@ __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t*
 
 // Rotates the Q operand in registers (non-interleaved RoPE halves): the lane's
 // chunks ds and ds+2 hold d and d+32. cs = table row of this position:
-// cs[2f] = cos(pos * inv_freq[f]), cs[2f+1] = sin(...), f < 32.
+// cs[2f] = cos(pos * inv_freq[f]), cs[2f+1] = sin(...), f < 32. The table
+// values are fetched first (rope_q_fetch: they depend only on the position,
+// so a kernel can issue them before anything else) and applied once q has
+// landed (rope_q_apply).
 // Returns the lane's sum of squares of q before the rotation (the rotation
 // keeps each pair's norm; callers bounding |rotated q| allow for the rounding).
-template <typename E>
-__device__ inline float rope_q_table(u32x4_t (&q)[4], const float* __restrict__ cs) {
+struct RopeQ {
+  f32x4_t v[2][4];  // [dl][i2]: cos, sin of f = 16dl + 8h + 2*i2 (+1)
+};
+
+__device__ inline void rope_q_fetch(RopeQ& r, const float* __restrict__ cs) {
   const int h = (threadIdx.x & 63) >> 5;
+#pragma unroll
+  for (int dl = 0; dl < 2; ++dl) {
+    const f32x4_t* t = reinterpret_cast<const f32x4_t*>(cs + 2 * (16 * dl + 8 * h));
+#pragma unroll
+    for (int i2 = 0; i2 < 4; ++i2) r.v[dl][i2] = t[i2];
+  }
+}
+
+template <typename E>
+__device__ inline float rope_q_apply(u32x4_t (&q)[4], const RopeQ& r) {
   float ss = 0.f;
 #pragma unroll
   for (int dl = 0; dl < 2; ++dl) {
@@ -711,10 +727,9 @@ __device__ inline float rope_q_table(u32x4_t (&q)[4], const float* __restrict__ 
     unpack8<E>(q[dl + 2], b);
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(b[i], b[i], __builtin_fmaf(a[i], a[i], ss));
-    const f32x4_t* t = reinterpret_cast<const f32x4_t*>(cs + 2 * (16 * dl + 8 * h));
 #pragma unroll
     for (int i2 = 0; i2 < 4; ++i2) {
-      const f32x4_t v = t[i2];  // cos, sin of f = 16dl + 8h + 2*i2 (+1)
+      const f32x4_t v = r.v[dl][i2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int i = 2 * i2 + u;

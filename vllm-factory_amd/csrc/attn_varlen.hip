@@ -232,39 +232,48 @@ struct VarlenPolicy {
   }
 };
 
-// Four workgroups per CU (128 VGPRs), except the sliding-window kernels with
-// a key mask: at 128 VGPRs they spill inside the tile loop, and three
-// workgroups per CU without spills run the 22-layer ModernBERT forward
-// (14 such layers at 163 736 tokens) 0.25 ms faster.
-template <typename E, bool ROPE, bool LOCAL, bool KVALID>
-__global__ __launch_bounds__(256, (LOCAL && KVALID) ? 3 : 4) void varlen_fwd_kernel(VarlenArgs a) {
-  __shared__ __align__(16) uint16_t K0[kTileElems];
-  __shared__ __align__(16) uint16_t K1[kTileElems];
-  __shared__ __align__(16) uint16_t V0[kTileElems];
-  __shared__ __align__(16) uint16_t V1[kTileElems];
-  __shared__ float kmask[2 * kBN];
-  __shared__ int kflag[2];
-  __shared__ float pen[LOCAL ? kPenLen : 1];
+// LDS of one workgroup of the 16-bit kernels.
+template <bool LOCAL>
+struct VarlenLds {
+  uint16_t* K0; uint16_t* K1; uint16_t* V0; uint16_t* V1;
+  float* kmask; int* kflag; float* pen;
+};
 
-  const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int qt = work % a.nqt;
-  const int h = (work / a.nqt) % a.H;
-  const int s = work / (a.nqt * a.H);
-  const int tok0 = a.cu[s];
-  const int nfull = a.cu[s + 1] - tok0;
-  const int n = min(nfull, a.maxlen);
+// Loads of an item that need only its (sequence, head, query tile) indices:
+// the table row of the Q rotation and the key norms of the tiles the
+// workgroup may visit. Issued before the sequence offsets (cu_seqlens)
+// arrive, they keep the item's set-up to two memory round trips (kernel
+// arguments and offsets, then Q and the first K/V tiles) instead of three.
+template <bool ROPE, bool LOCAL>
+__device__ inline void varlen_item_prefetch(const VarlenArgs& a, int s, int h, int qt, RopeQ& rq,
+                                            float& kx) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int q0 = qt * kBM;
-  // rows past max_seqlen are written as zeros: without RoPE by the last
-  // query tile, with RoPE by the K pre-pass (or, after the fused projection,
-  // by zero_cut_rows_kernel), which keeps the RoPE kernels' registers free
-  if (q0 >= n) {  // whole workgroup: uniform exit
-    if (!ROPE && qt == a.nqt - 1 && nfull > n)
-      zero_rows_d64(reinterpret_cast<uint16_t*>(a.o) + (int64_t)tok0 * a.os[0] + h * a.os[1],
-                    a.os[0], n, nfull);
-    return;
+  const int qrow = q0 + w * 32 + (lane & 31);
+  const int kt_lo = LOCAL ? max(0, q0 - a.window) / kBN : 0;
+  kx = 0.f;
+  if (ROPE) {
+    // rows past the sequence end rotate zeros: any table row will do
+    rope_q_fetch(rq, a.rope + (int64_t)min(qrow, a.maxlen - 1) * 64);
+    // lanes past the last tile slot load slot nkt - 1 (no branch: a divergent
+    // one here would make the offsets loaded next vector loads)
+    if (!a.kblk32)
+      kx = a.kmax[((int64_t)h * a.nseq + s) * a.nkt + min(kt_lo + lane, a.nkt - 1)];
   }
+}
 
+// One item: query rows q0 .. q0 + 127 (qt = q0 / 128) of head h of sequence
+// s (rows tok0 .. tok0 + n - 1 of the stream), n > q0, against every key of
+// the sequence the layer lets them see; rq / kx as varlen_item_prefetch
+// left them. Leaves the item's output rows written and every LDS buffer free
+// once all waves have passed a barrier.
+template <typename E, bool ROPE, bool LOCAL, bool KVALID>
+__device__ inline void varlen_item(const VarlenArgs& a, const VarlenLds<LOCAL>& L, int s, int h,
+                                   int qt, int tok0, int n, const RopeQ& rq, float kx) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, hl = lane >> 5;
+  const int q0 = qt * kBM;
+  const int wq_lo = q0 + w * 32;
+  const int qrow = wq_lo + (lane & 31);
   const uint16_t* Qp = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)tok0 * a.qs[0] + h * a.qs[1];
 
   // key tiles of the workgroup (sequence-relative)
@@ -274,17 +283,15 @@ __global__ __launch_bounds__(256, (LOCAL && KVALID) ? 3 : 4) void varlen_fwd_ker
     khi = min(n, q0 + kBM + a.window);
     for (int e = t; e < kPenLen; e += 256) {
       const int d = e - kPenOff;
-      pen[e] = (d <= a.window && d >= -a.window) ? 0.f : -INFINITY;
+      L.pen[e] = (d <= a.window && d >= -a.window) ? 0.f : -INFINITY;
     }
   }
   const int kt_begin = klo / kBN;
   const int kt_end = (khi + kBN - 1) / kBN;
   // start of the sequence's partial last key tile (none: -1)
   const int tail0 = (n % kBN) ? (n / kBN) * kBN : -1;
-  if (!KVALID && t < kBN) kmask[t] = (tail0 + t < n) ? 0.f : -INFINITY;
+  if (!KVALID && t < kBN) L.kmask[t] = (tail0 + t < n) ? 0.f : -INFINITY;
 
-  const int wq_lo = q0 + w * 32;
-  const int qrow = wq_lo + (lane & 31);
   const bool qvalid = qrow < n;
 
   VarlenPolicy<E, ROPE, LOCAL, KVALID> pol;
@@ -299,16 +306,15 @@ __global__ __launch_bounds__(256, (LOCAL && KVALID) ? 3 : 4) void varlen_fwd_ker
                 (int)a.vs[0], n);
   pol.tok0 = tok0; pol.n = n; pol.kt0 = kt_begin; pol.t = t; pol.hl = hl; pol.qrow = qrow;
   pol.wq_lo = wq_lo; pol.wq_hi = min(wq_lo + 31, n - 1); pol.window = a.window; pol.tail0 = tail0;
-  pol.kmask = kmask; pol.kflag = kflag; pol.pen = pen;
+  pol.kmask = L.kmask; pol.kflag = L.kflag; pol.pen = L.pen;
 
-  attn_pipe_start(pol, kt_end - kt_begin, K0, K1, V0);
+  attn_pipe_start(pol, kt_end - kt_begin, L.K0, L.K1, L.V0);
 
   u32x4_t qf[4];
   load_q(qf, Qp + (int64_t)qrow * a.qs[0], qvalid);
-  // rows past n rotate zeros with the table row of position n - 1; q2: the
-  // lane's share of |q|^2 before the rotation
+  // q2: the lane's share of |q|^2 before the rotation
   float q2 = 0.f;
-  if (ROPE) q2 = rope_q_table<E>(qf, a.rope + (int64_t)min(qrow, n - 1) * 64);
+  if (ROPE) q2 = rope_q_apply<E>(qf, rq);
 
   float m = -INFINITY;
   // row sums on the matrix core where the 8 extra registers fit (global
@@ -320,15 +326,17 @@ __global__ __launch_bounds__(256, (LOCAL && KVALID) ? 3 : 4) void varlen_fwd_ker
     // |score| <= |q| max|k| over the workgroup's key tiles (scores are in
     // log2 units: K carries c2); the margin covers the fp32 norms and the
     // MFMA's fp32 accumulation
-    float kx = 0.f;
     if (a.kblk32) {
       // stream blocks covering the workgroup's keys (a superset: still a bound)
       const float* km = a.kmax + (int64_t)h * ((a.T + 31) >> 5);
       const int b0 = (tok0 + kt_begin * kBN) >> 5, b1 = (tok0 + min(kt_end * kBN, n) - 1) >> 5;
       for (int j = b0 + lane; j <= b1; j += 64) kx = fmaxf(kx, km[j]);
     } else {
+      // the prefetched norms of tiles kt_begin + lane, kept where inside the
+      // workgroup's range; tiles past the first 64 (sequences > 4096) here
+      if (kt_begin + lane >= kt_end) kx = 0.f;
       const float* km = a.kmax + ((int64_t)h * a.nseq + s) * a.nkt;
-      for (int j = kt_begin + lane; j < kt_end; j += 64) kx = fmaxf(kx, km[j]);
+      for (int j = kt_begin + 64 + lane; j < kt_end; j += 64) kx = fmaxf(kx, km[j]);
     }
     kx = wave_max(kx);
     // the rotation keeps |q|; rounding the rotated q to 16 bits grows each
@@ -336,21 +344,61 @@ __global__ __launch_bounds__(256, (LOCAL && KVALID) ? 3 : 4) void varlen_fwd_ker
     q2 = half_swap_sum(q2);
     const float ub = sqrtf(q2) * 1.00390625f * kx * 1.0078125f + 0.0625f;
     if (__builtin_amdgcn_ballot_w64(ub > E::kLog2PMax) == 0ull)
-      attn_loop_db<E, true>(pol, K0, K1, V0, V1, ntiles, qf, 1.f, m, l, o0, o1);
+      attn_loop_db<E, true>(pol, L.K0, L.K1, L.V0, L.V1, ntiles, qf, 1.f, m, l, o0, o1);
     else
-      attn_loop_db<E, false>(pol, K0, K1, V0, V1, ntiles, qf, 1.f, m, l, o0, o1);
+      attn_loop_db<E, false>(pol, L.K0, L.K1, L.V0, L.V1, ntiles, qf, 1.f, m, l, o0, o1);
   } else {
-    attn_loop_db<E, false>(pol, K0, K1, V0, V1, ntiles, qf, a.c2, m, l, o0, o1);
+    attn_loop_db<E, false>(pol, L.K0, L.K1, L.V0, L.V1, ntiles, qf, a.c2, m, l, o0, o1);
   }
 
   const float l_tot = l.total();
   // whole-row stores through this wave's half of K0 / K1 (free after the
   // loop's last barrier; a workgroup with no key tile never touched them)
   uint16_t* ob = reinterpret_cast<uint16_t*>(a.o) + (int64_t)tok0 * a.os[0] + h * a.os[1];
-  store_out_rows<E>((w < 2 ? K0 : K1) + (w & 1) * 2048, o0, o1, l_tot,
+  store_out_rows<E>((w < 2 ? L.K0 : L.K1) + (w & 1) * 2048, o0, o1, l_tot,
                     [&](int r) { return ob + (int64_t)(wq_lo + r) * a.os[0]; },
                     [&](int r) { return wq_lo + r < n; });
-  if (!ROPE && qt == a.nqt - 1 && nfull > n) zero_rows_d64(ob, a.os[0], n, nfull);
+}
+
+// One workgroup per (sequence, head, query tile) work item. Four workgroups
+// per CU (128 VGPRs), except the sliding-window kernels with a key mask: at
+// 128 VGPRs they spill inside the tile loop, and three workgroups per CU
+// without spills run the 22-layer ModernBERT forward (14 such layers at
+// 163 736 tokens) 0.25 ms faster.
+template <typename E, bool ROPE, bool LOCAL, bool KVALID>
+__global__ __launch_bounds__(256, (LOCAL && KVALID) ? 3 : 4) void varlen_fwd_kernel(VarlenArgs a) {
+  __shared__ __align__(16) uint16_t K0[kTileElems];
+  __shared__ __align__(16) uint16_t K1[kTileElems];
+  __shared__ __align__(16) uint16_t V0[kTileElems];
+  __shared__ __align__(16) uint16_t V1[kTileElems];
+  __shared__ float kmask[2 * kBN];
+  __shared__ int kflag[2];
+  __shared__ float pen[LOCAL ? kPenLen : 1];
+
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = work % a.nqt;
+  const int h = (work / a.nqt) % a.H;
+  const int s = work / (a.nqt * a.H);
+  RopeQ rq;
+  float kx;
+  varlen_item_prefetch<ROPE, LOCAL>(a, s, h, qt, rq, kx);
+  const int tok0 = a.cu[s];
+  const int nfull = a.cu[s + 1] - tok0;
+  const int n = min(nfull, a.maxlen);
+  // rows past max_seqlen are written as zeros: without RoPE by the last
+  // query tile, with RoPE by the K pre-pass (or, after the fused projection,
+  // by zero_cut_rows_kernel), which keeps the RoPE kernels' registers free
+  if (qt * kBM >= n) {  // whole workgroup: uniform exit
+    if (!ROPE && qt == a.nqt - 1 && nfull > n)
+      zero_rows_d64(reinterpret_cast<uint16_t*>(a.o) + (int64_t)tok0 * a.os[0] + h * a.os[1],
+                    a.os[0], n, nfull);
+    return;
+  }
+  const VarlenLds<LOCAL> L = {K0, K1, V0, V1, kmask, kflag, pen};
+  varlen_item<E, ROPE, LOCAL, KVALID>(a, L, s, h, qt, tok0, n, rq, kx);
+  if (!ROPE && qt == a.nqt - 1 && nfull > n)
+    zero_rows_d64(reinterpret_cast<uint16_t*>(a.o) + (int64_t)tok0 * a.os[0] + h * a.os[1],
+                  a.os[0], n, nfull);
 }
 
 // fp32: one thread per query row, exact fp32 arithmetic, accurate sin/cos.
@@ -466,8 +514,10 @@ static int check_thd(const vfk_tensor* t, const char* name, int dtype, int64_t T
 }
 
 static int64_t kr_bytes(int64_t T, int64_t H) { return (T * H * kHD * 2 + 255) / 256 * 256; }
+
 static int launch_varlen(VarlenArgs& a, int dt, bool rope, int max_seqlen, hipStream_t st,
                          const char* nm);
+
 
 extern "C" int64_t vfk_varlen_attn_workspace_bytes(int32_t dtype, int64_t total_tokens,
                                                   int32_t num_heads, int32_t rope,
