@@ -262,6 +262,30 @@ __device__ inline void varlen_item_prefetch(const VarlenArgs& a, int s, int h, i
   }
 }
 
+// The same loads in two steps: the addresses (they need the kernel
+// arguments, not the sequence offsets), then the loads themselves.
+template <bool ROPE, bool LOCAL>
+struct ItemPrefetch {
+  const float* tab;  // the lane's Q-rotation table row
+  const float* km;   // the lane's key-norm slot
+  __device__ ItemPrefetch(const VarlenArgs& a, int s, int h, int qt) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int q0 = qt * kBM;
+    const int qrow = q0 + w * 32 + (lane & 31);
+    const int kt_lo = LOCAL ? max(0, q0 - a.window) / kBN : 0;
+    tab = ROPE ? a.rope + (int64_t)min(qrow, a.maxlen - 1) * 64 : nullptr;
+    km = (ROPE && !a.kblk32) ? a.kmax + ((int64_t)h * a.nseq + s) * a.nkt + min(kt_lo + lane, a.nkt - 1)
+                             : nullptr;
+  }
+  __device__ void issue(RopeQ& rq, float& kx) const {
+    kx = 0.f;
+    if (ROPE) {
+      rope_q_fetch(rq, tab);
+      if (km) kx = *km;
+    }
+  }
+};
+
 // One item: query rows q0 .. q0 + 127 (qt = q0 / 128) of head h of sequence
 // s (rows tok0 .. tok0 + n - 1 of the stream), n > q0, against every key of
 // the sequence the layer lets them see; rq / kx as varlen_item_prefetch
@@ -379,11 +403,30 @@ __global__ __launch_bounds__(256, (LOCAL && KVALID) ? 3 : 4) void varlen_fwd_ker
   const int qt = work % a.nqt;
   const int h = (work / a.nqt) % a.H;
   const int s = work / (a.nqt * a.H);
+  // The loads that need only the item's indices (the Q-rotation table row
+  // and the key norms of the tiles the workgroup may visit) go out with the
+  // sequence offsets, before anything waits on either, so the set-up is two
+  // memory round trips (offsets, then Q and the first K/V tiles) rather than
+  // three. Global layers request the offsets first, with the other addresses
+  // formed beforehand so that no wait for the kernel arguments falls between
+  // the requests (an A/B on config 2: global call 142-144 against 145-146 us
+  // with the offsets requested last); the sliding-window kernels keep the
+  // offsets last, which holds them at 128 VGPRs without a spill.
   RopeQ rq;
   float kx;
-  varlen_item_prefetch<ROPE, LOCAL>(a, s, h, qt, rq, kx);
-  const int tok0 = a.cu[s];
-  const int nfull = a.cu[s + 1] - tok0;
+  int tok0, nfull;
+  if (LOCAL) {
+    varlen_item_prefetch<ROPE, LOCAL>(a, s, h, qt, rq, kx);
+    tok0 = a.cu[s];
+    nfull = a.cu[s + 1] - tok0;
+  } else {
+    const ItemPrefetch<ROPE, LOCAL> pre(a, s, h, qt);
+    __builtin_amdgcn_sched_barrier(0);
+    tok0 = a.cu[s];
+    nfull = a.cu[s + 1] - tok0;
+    __builtin_amdgcn_sched_barrier(0);
+    pre.issue(rq, kx);
+  }
   const int n = min(nfull, a.maxlen);
   // rows past max_seqlen are written as zeros: without RoPE by the last
   // query tile, with RoPE by the K pre-pass (or, after the fused projection,
