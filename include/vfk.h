@@ -417,6 +417,37 @@ int vfk_colbert_head_fwd(const vfk_tensor* x, const vfk_tensor* residual,
                          const vfk_tensor* bias, vfk_tensor* hidden_out,
                          vfk_tensor* out, void* stream);
 
+/* The same head in folded form, for callers that do not need the LayerNorm
+ * output (no counterpart in the reference; it computes what
+ * vfk_colbert_head_fwd does). With u = x + residual rounded to x's dtype (the
+ * encoder's residual sum), mu and rstd its LayerNorm statistics:
+ *   y_n = rstd (sum_k u_k W'_nk - mu G_n) + C_n,  out = y / max(|y|, 1e-8)
+ * so the raw rows go straight into the matrix instructions and each
+ * workgroup (128 tokens) streams the weight through LDS once.
+ * vfk_colbert_fold_weight makes the three constants once per weight:
+ *   weight [N, D] (rows contiguous; N = 32, 64, 96 or 128; D a multiple of
+ *     128 up to 4096), ln_weight gamma, ln_bias beta [D] or NULL (beta needs
+ *     gamma), bias b [N] or NULL, all of weight's 16-bit dtype
+ *   folded [N / 32, D / 16, 64, 8] of weight's dtype: W'_nk = gamma_k W_nk
+ *     rounded (W without gamma), in the operand order of
+ *     vfk_pack_weight_mfma32
+ *   gsum, cvec fp32 [N] (16-byte aligned): G_n = sum_k W'_nk,
+ *     C_n = sum_k beta_k W_nk + b_n
+ * vfk_colbert_head_folded_fwd:
+ *   x [T, D], residual [T, D] or NULL: rows contiguous, 16-byte aligned
+ *   folded, cvec as made above; gsum as made above applies the LayerNorm
+ *     (eps as given), NULL projects the rows as given (fold without gamma)
+ *   out [T, N] (rows 16-byte aligned), x's dtype; the projection is rounded
+ *     to that dtype before its norm is taken, as a 16-bit Linear output is. */
+int vfk_colbert_fold_weight(const vfk_tensor* weight, const vfk_tensor* ln_weight,
+                            const vfk_tensor* ln_bias, const vfk_tensor* bias,
+                            vfk_tensor* folded, vfk_tensor* gsum, vfk_tensor* cvec,
+                            void* stream);
+int vfk_colbert_head_folded_fwd(const vfk_tensor* x, const vfk_tensor* residual,
+                                const vfk_tensor* folded, const vfk_tensor* gsum,
+                                const vfk_tensor* cvec, float eps, vfk_tensor* out,
+                                void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Memory-bound epilogues                                                    */
 /* ------------------------------------------------------------------------ */

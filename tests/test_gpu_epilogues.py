@@ -238,6 +238,65 @@ def test_colbert_head_with_final_layernorm(dev, dtype, T, D, N, pack):
                       f"colbert hidden {dtype}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,D,N,res,ln,lnb,bias", [
+    (1000, 768, 128, True, True, False, False), (1, 768, 128, True, True, False, False),
+    (33, 1024, 96, True, True, True, True), (64, 256, 32, False, True, False, False),
+    (300, 384, 64, False, False, False, True), (129, 2048, 128, True, True, True, False),
+    (257, 640, 128, True, False, False, False)])
+def test_colbert_head_folded(dev, dtype, T, D, N, res, ln, lnb, bias):
+    """The folded form (LayerNorm weight multiplied into the projection, the
+    raw rows projected; taken whenever the LayerNorm output is not returned):
+    with and without residual, LayerNorm weight and bias, projection bias;
+    token counts around the 128-token workgroup; hidden sizes up to 2048."""
+    from kernels.colbert_head import colbert_head
+    x = _rand((T, D), dtype, 141)
+    r = _rand((T, D), dtype, 142) if res else None
+    lw = (1 + 0.1 * _rand((D,), torch.float32, 143)).to(dtype) if ln else None
+    lb = (0.1 * _rand((D,), torch.float32, 144)).to(dtype) if lnb else None
+    w = _rand((N, D), dtype, 145, 0.05)
+    b = _rand((N,), dtype, 146, 0.1) if bias else None
+    want = oe.colbert_head(x, [(w, b, None, False)], lw, lb, 1e-5, residual=r,
+                           layer_norm=ln)
+    d = lambda t: None if t is None else t.to(dev)
+    got = colbert_head(x.to(dev), w.to(dev), d(b), d(lw), d(lb), 1e-5, residual=d(r))
+    _colbert_rows_close(got, want, f"folded {dtype} {T}x{D}->{N} res={res} ln={ln}")
+
+
+def test_colbert_head_folded_rows_far_from_zero_mean(dev):
+    """Rows whose mean is 30 standard deviations from zero: the folded form
+    subtracts mu G from the raw projection, which its shifted statistics keep
+    exact enough. The LayerNorm input is the residual sum rounded to bf16 (as
+    the encoder's is; its spacing near 30 is 1/8), so the oracle takes that
+    rounded sum."""
+    from kernels.colbert_head import colbert_head
+    T, D, N = 500, 768, 128
+    x = (_rand((T, D), torch.float32, 151) + 30.0).bfloat16()
+    r = (0.5 * _rand((T, D), torch.float32, 152)).bfloat16()
+    lw = (1 + 0.1 * _rand((D,), torch.float32, 153)).bfloat16()
+    w = _rand((N, D), torch.bfloat16, 154, 0.05)
+    u = (x.float() + r.float()).bfloat16()
+    want = oe.colbert_head(u, [(w, None, None, False)], lw, None, 1e-5)
+    got = colbert_head(x.to(dev), w.to(dev), None, lw.to(dev), None, 1e-5, residual=r.to(dev))
+    _colbert_rows_close(got, want, "folded, mean 30")
+
+
+def test_colbert_head_refolds_an_updated_norm_weight(dev):
+    """The folded weight follows the LayerNorm weight it was made from: an
+    in-place update of it is seen by the next call."""
+    from kernels.colbert_head import colbert_head
+    x = _rand((200, 768), torch.bfloat16, 161)
+    w = _rand((128, 768), torch.bfloat16, 162, 0.05)
+    lw = (1 + 0.1 * _rand((768,), torch.float32, 163)).bfloat16()
+    wd, lwd = w.to(dev), lw.to(dev)
+    got1 = colbert_head(x.to(dev), wd, None, lwd)
+    _colbert_rows_close(got1, oe.colbert_head(x, [(w, None, None, False)], lw, None, 1e-5), "before")
+    lwd.mul_(torch.linspace(0.5, 1.5, 768, device=dev).bfloat16())
+    got2 = colbert_head(x.to(dev), wd, None, lwd)
+    _colbert_rows_close(got2, oe.colbert_head(x, [(w, None, None, False)], lwd.cpu(), None, 1e-5),
+                        "after")
+
+
 def test_colbert_head_repacks_an_updated_weight(dev):
     """The packed copy is cached per weight tensor and version: an in-place
     update of the weight is seen by the next call."""

@@ -86,6 +86,8 @@ _SIGNATURES = {
     "vfk_act_fwd": [_i32, _P, _P, _vp],
     "vfk_residual_add": [_P, _P, _P, _vp],
     "vfk_colbert_head_fwd": [_P, _P, _P, _P, _f32, _P, _P, _P, _P, _vp],
+    "vfk_colbert_fold_weight": [_P, _P, _P, _P, _P, _P, _P, _vp],
+    "vfk_colbert_head_folded_fwd": [_P, _P, _P, _P, _P, _f32, _P, _vp],
 }
 
 _RESTYPES = {"vfk_varlen_attn_workspace_bytes": ctypes.c_int64,

@@ -6,7 +6,9 @@ the encoder's final LayerNorm (models/modernbert/modernbert_encoder.py:412-415,
 :478), then its projection stack and
 `projected / projected.norm(dim=-1, keepdim=True).clamp(min=1e-8)`
 (plugins/moderncolbert/model.py:260-267, _ResidualDense :68-95) as separate
-torch ops. Here the LayerNorm output is projected while it is still in LDS.
+torch ops. Here the LayerNorm output is projected while it is still in LDS,
+or, when it is not wanted back, the LayerNorm is folded into the projection:
+y = rstd (u (gamma W)^T - mu G) + C.
 """
 from __future__ import annotations
 
@@ -16,7 +18,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .weight_pack import packed_weight
+from .weight_pack import folded_colbert_weight, packed_weight
 
 
 def colbert_head(hidden: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
@@ -26,18 +28,31 @@ def colbert_head(hidden: torch.Tensor, weight: torch.Tensor, bias: Optional[torc
                  return_hidden: bool = False, pack: bool = True):
     """hidden [T, D] (+ residual) -> LayerNorm (if norm_weight) -> @ weight^T
     (+ bias) -> rows scaled to unit L2 norm (norm clamped at 1e-8).
-    weight [N, D] with N in {32, 64, 96, 128}, D a multiple of 256 up to 1024.
-    pack: the kernel reads the weight in MFMA operand order, packed once per
-    weight tensor (weight_pack.packed_weight); False reads the [N, D] rows.
+    weight [N, D] with N in {32, 64, 96, 128}; D a multiple of 128 up to 4096
+    in the folded form, of 256 up to 1024 in the staged one.
+    pack: the kernel reads the weight in MFMA operand order, made once per
+    weight tensor (weight_pack); False reads the [N, D] rows. With pack, no
+    return_hidden and D a multiple of 128, the LayerNorm weight is folded into
+    the projection (vfk_colbert_head_folded_fwd: the raw rows go straight
+    into the matrix instructions, 128 tokens per workgroup); otherwise the
+    normalised rows are staged in LDS (vfk_colbert_head_fwd).
     Returns the [T, N] embeddings, and the LayerNorm output if return_hidden."""
     dev = _lib.require_gpu(hidden, weight, bias, norm_weight, norm_bias, residual)
     if hidden.dim() != 2 or weight.dim() != 2 or weight.shape[1] != hidden.shape[1]:
         raise ValueError("hidden must be [T, D] and weight [N, D]")
     x = _lib.rows_aligned(hidden)
     r = _lib.rows_aligned(residual) if residual is not None else None
-    wt = packed_weight(weight) if pack else _lib.rows_aligned(weight)
     T, N = x.shape[0], weight.shape[0]
     out = torch.empty(T, N, dtype=x.dtype, device=dev)
+    if pack and not return_hidden and x.shape[1] % 128 == 0:
+        # folded form: gamma multiplied into the weight, the raw rows projected
+        folded, g, c = folded_colbert_weight(weight, norm_weight, norm_bias, bias)
+        _lib.on_device(
+            "vfk_colbert_head_folded_fwd", dev, _lib.ref(_lib.desc(x)), _lib.ref(_lib.desc(r)),
+            _lib.ref(_lib.desc(folded)), _lib.ref(_lib.desc(g if norm_weight is not None else None)),
+            _lib.ref(_lib.desc(c)), float(eps), _lib.ref(_lib.desc(out)))
+        return out
+    wt = packed_weight(weight) if pack else _lib.rows_aligned(weight)
     h = torch.empty_like(x) if return_hidden else None
     vec = lambda t: None if t is None else t.contiguous()
     _lib.on_device(

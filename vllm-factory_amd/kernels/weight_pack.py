@@ -12,6 +12,10 @@ re-packs. Tensors made under torch.inference_mode() (vLLM runs its forward
 there) have no version counter: their entry is keyed by the object alone, so
 an in-place update of such a weight inside inference mode is not seen; call
 `clear_cache()` after one.
+
+The ColBERT head's folded weight (`folded_colbert_weight`) is cached the same
+way, per projection weight, and also follows the LayerNorm weight and bias
+and the projection bias it was made from.
 """
 from __future__ import annotations
 
@@ -57,10 +61,54 @@ def packed_weight(weight: torch.Tensor) -> torch.Tensor:
     return packed
 
 
+_FOLDED: dict = {}
+
+
+def fold_colbert_weight(weight: torch.Tensor, norm_weight=None, norm_bias=None, bias=None):
+    """The ColBERT head's folded constants (vfk_colbert_fold_weight): the
+    LayerNorm weight gamma multiplied into the projection weight, packed in
+    operand order, plus fp32 G = row sums of that product and
+    C = W beta + b. Returns (folded, G, C)."""
+    dev = _lib.require_gpu(weight, norm_weight, norm_bias, bias)
+    if weight.dim() != 2:
+        raise ValueError(f"weight must be [N, D], got {tuple(weight.shape)}")
+    N, D = weight.shape
+    w2 = _lib.rows_aligned(weight.detach())
+    folded = torch.empty(max(N // 32, 1), max(D // 16, 1), 64, 8, dtype=weight.dtype, device=dev)
+    g = torch.empty(N, dtype=torch.float32, device=dev)
+    c = torch.empty(N, dtype=torch.float32, device=dev)
+    vec = lambda t: None if t is None else t.detach().contiguous()
+    _lib.on_device("vfk_colbert_fold_weight", dev, _lib.ref(_lib.desc(w2)),
+                   _lib.ref(_lib.desc(vec(norm_weight))), _lib.ref(_lib.desc(vec(norm_bias))),
+                   _lib.ref(_lib.desc(vec(bias))), _lib.ref(_lib.desc(folded)),
+                   _lib.ref(_lib.desc(g)), _lib.ref(_lib.desc(c)))
+    return folded, g, c
+
+
+def folded_colbert_weight(weight: torch.Tensor, norm_weight=None, norm_bias=None, bias=None):
+    """fold_colbert_weight(...), made once per weight tensor: the entry is
+    keyed by the projection weight (one entry each) and remembers the
+    LayerNorm weight, LayerNorm bias and bias objects and the versions of
+    all four; any change re-folds."""
+    parts = (weight, norm_weight, norm_bias, bias)
+    sig = tuple((None, 0) if t is None else (id(t), _version(t)) for t in parts)
+    key = id(weight)
+    hit = _FOLDED.get(key)
+    if (hit is not None and hit[0]() is weight and hit[1] == sig
+            and all(t is None or r() is t for t, r in zip(parts[1:], hit[2]))):
+        return hit[3]
+    val = fold_colbert_weight(weight, norm_weight, norm_bias, bias)
+    refs = tuple(None if t is None else weakref.ref(t) for t in parts[1:])
+    _FOLDED[key] = (weakref.ref(weight, lambda _r, k=key: _FOLDED.pop(k, None)), sig, refs, val)
+    return val
+
+
 def clear_cache() -> None:
-    """Drops every packed copy (e.g. after an in-place update of a weight
-    made under inference mode, which has no version counter)."""
+    """Drops every packed and folded copy (e.g. after an in-place update of a
+    weight made under inference mode, which has no version counter)."""
     _CACHE.clear()
+    _FOLDED.clear()
 
 
-__all__ = ["pack_weight", "packed_weight", "clear_cache"]
+__all__ = ["pack_weight", "packed_weight", "fold_colbert_weight", "folded_colbert_weight",
+           "clear_cache"]
