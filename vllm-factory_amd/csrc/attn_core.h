@@ -406,7 +406,8 @@ __device__ inline void store_out_rows(uint16_t* __restrict__ stage, f32x16_t o0,
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int r = (lane >> 3) + 8 * k;
-    if (valid(r)) *reinterpret_cast<u32x4_t*>(rowp(r) + 8 * q) = v[k];
+    // non-temporal: the output is not read again by the attention
+    if (valid(r)) __builtin_nontemporal_store(v[k], reinterpret_cast<u32x4_t*>(rowp(r) + 8 * q));
   }
 }
 

@@ -126,8 +126,9 @@ __global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int nkt)
 #pragma unroll
   for (int u = 0; u < kPackHeads; ++u) {
     const uint16_t* p = src + (int64_t)min(h0 + u, a.H - 1) * a.ks[1];
-    k0[u] = *reinterpret_cast<const u32x4_t*>(p);
-    k1[u] = *reinterpret_cast<const u32x4_t*>(p + 32);
+    // non-temporal: K is read once here (the attention reads the rotated copy)
+    k0[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    k1[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p + 32));
   }
 #pragma unroll
   for (int u = 0; u < kPackHeads; ++u) {
