@@ -513,7 +513,9 @@ __global__ __launch_bounds__(256) void span_rows_kernel(const uint8_t* __restric
 #pragma unroll
       for (int k = 0; k < kSpanPass; ++k) {
         const int c = c0 + lane + 64 * k;
-        if (c < total) dst[c] = v[u][k];
+        // non-temporal: the pair rows stream out without displacing the
+        // source rows that neighbouring spans read again from L2
+        if (c < total) __builtin_nontemporal_store(v[u][k], dst + c);
       }
     }
   }
