@@ -33,6 +33,7 @@ sys.path.insert(0, os.path.join(ROOT, "vllm-factory_amd"))
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+SETTLE_S = 0.5              # busy time before the headline's warmup steps (clock ramp)
 
 
 def _events(torch):
@@ -125,6 +126,24 @@ def measured_traffic(name):
     return None
 
 
+def settle(torch, fn, seconds):
+    """Runs fn back to back for about `seconds` of GPU time. The
+    MI355X raises its clock over tens of milliseconds of load: measured on one
+    box, the headline read 345-356 TFLOP/s after 5 warmup steps, 396-397 after
+    50 and 405-407 after 200. Timing starts from that steady state; the
+    warmup steps asked for still run after it."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(4):
+        fn()
+    torch.cuda.synchronize()
+    per = max((time.perf_counter() - t0) / 4, 1e-5)
+    # the calls are queued without a sync in between, so the GPU never idles
+    for _ in range(int(seconds / per) + 1):
+        fn()
+    torch.cuda.synchronize()
+
+
 def device_ms(torch, fn, n):
     """Average device time of fn over n back-to-back calls: a spin kernel first
     holds the stream so that all n launches are queued before the start event
@@ -161,6 +180,7 @@ def headline(torch, args):
         timer.run("local", lambda: varlen_rope_attention(q, k, v, c.cu_seqlens, c.max_seqlen, 64,
                                                           10000.0, 0.125, out=out_l))
 
+    settle(torch, step, SETTLE_S)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -804,7 +824,8 @@ def main():
         "config": {"workload": "ModernBERT-base attention, 64 varlen-packed sequences U{512..768} "
                                "(T=%d), 12 heads x 64, global (RoPE 160000) + local +-64 (RoPE 10000)"
                                % head["tokens"],
-                   "global_batch": 64, "seq_len": "512-768", "parallelism": "none (1 GPU)"},
+                   "global_batch": 64, "seq_len": "512-768", "parallelism": "none (1 GPU)",
+                   "settle_s": SETTLE_S},
         "roofline": head["roofline"],
         "kernels": head["kernels"],
         "extra": extra,
