@@ -83,8 +83,8 @@ def test_modernbert_colbert_head_matches_unfused():
 
 # ---------------------------------------------------------------- config 5
 DEPTHS = (1, 4, 11, 22)
-# 1.25x the max-abs measured on MI355X at each depth (see the test below)
-MAX_ABS_BOUND = {1: 5.3e-2, 4: 9.8e-2, 11: 1.49e-1, 22: 1.69e-1}
+# about 1.2x the largest max-abs measured on MI355X at each depth (see the test below)
+MAX_ABS_BOUND = {1: 5.3e-2, 4: 9.8e-2, 11: 1.49e-1, 22: 2.0e-1}
 
 
 def _config5_subset(nseq=4):
@@ -118,10 +118,11 @@ def test_modernbert_config5_22_layers_match_oracle():
     two masked keys), bf16 on the GPU against the fp32 oracle. The bf16 path
     rounds every activation; its error grows with depth roughly like the
     square root of the number of layers. Measured on MI355X at depths 1 / 4 /
-    11 / 22: max-abs 4.2e-2 / 7.8e-2 / 1.19e-1 / 1.35e-1, cosine 0.999996 /
-    0.999987 / 0.999964 / 0.999925. Bound: 1.25x the measured max-abs at each
-    depth (5.3e-2 / 9.8e-2 / 1.49e-1 / 1.69e-1), so a change that adds a
-    fifth to the error fails, and cosine 0.9998 at every depth."""
+    11 / 22: max-abs 4.2e-2 / 7.8e-2 / 1.19e-1 / 1.35e-1 and, in a later run,
+    1.64e-1 at depth 22 (the others the same to three digits); cosine
+    0.999996 / 0.999987 / 0.999964 / 0.999925. Bound: about 1.2x the largest
+    measured max-abs at each depth (5.3e-2 / 9.8e-2 / 1.49e-1 / 2.0e-1), and
+    cosine 0.9998 at every depth."""
     import encoders.modernbert as em
     ids, cu, mx, _ = _config5_subset()
     w = em.random_weights()
