@@ -126,7 +126,7 @@ def measured_traffic(name):
     return None
 
 
-def settle(torch, fn, seconds):
+def settle(torch, fn, seconds, max_calls=1 << 30):
     """Runs fn back to back for about `seconds` of GPU time. The
     MI355X raises its clock over tens of milliseconds of load: measured on one
     box, the headline read 345-356 TFLOP/s after 5 warmup steps, 396-397 after
@@ -139,7 +139,7 @@ def settle(torch, fn, seconds):
     torch.cuda.synchronize()
     per = max((time.perf_counter() - t0) / 4, 1e-5)
     # the calls are queued without a sync in between, so the GPU never idles
-    for _ in range(int(seconds / per) + 1):
+    for _ in range(min(int(seconds / per) + 1, max_calls)):
         fn()
     torch.cuda.synchronize()
 
@@ -147,7 +147,9 @@ def settle(torch, fn, seconds):
 def device_ms(torch, fn, n):
     """Average device time of fn over n back-to-back calls: a spin kernel first
     holds the stream so that all n launches are queued before the start event
-    fires, which keeps host launch overhead out of short kernels' figures."""
+    fires, which keeps host launch overhead out of short kernels' figures.
+    The clock is settled first (about 0.1 s of queued calls, at most 2000)."""
+    settle(torch, fn, 0.1, 2000)
     torch.cuda.synchronize()
     torch.cuda._sleep(20_000_000)  # ~10 ms of spinning at MI355X clocks
     s, e = _events(torch)
