@@ -281,6 +281,29 @@ def test_colbert_head_folded_rows_far_from_zero_mean(dev):
     _colbert_rows_close(got, want, "folded, mean 30")
 
 
+def test_colbert_head_folded_multi_chunk(dev):
+    """Token counts past 128 x the workgroups the device holds at once: each
+    workgroup then runs several 128-token chunks through one pipeline (the
+    next chunk's first slices load during a chunk's outputs), the last one
+    partial. Every 97th row against the oracle; every row equal, bit for bit,
+    to the same rows run in a call of their own (a row's result does not
+    depend on how the rows are split among workgroups)."""
+    from kernels.colbert_head import colbert_head
+    T, D, N = 131149, 768, 128
+    x = _rand((T, D), torch.bfloat16, 171)
+    r = _rand((T, D), torch.bfloat16, 172)
+    lw = (1 + 0.1 * _rand((D,), torch.float32, 173)).bfloat16()
+    w = _rand((N, D), torch.bfloat16, 174, 0.05)
+    xd, rd, lwd, wd = x.to(dev), r.to(dev), lw.to(dev), w.to(dev)
+    got = colbert_head(xd, wd, None, lwd, None, 1e-5, residual=rd)
+    idx = torch.arange(0, T, 97)
+    want = oe.colbert_head(x[idx], [(w, None, None, False)], lw, None, 1e-5, residual=r[idx])
+    _colbert_rows_close(got[idx.to(dev)], want, "folded, several chunks per workgroup")
+    for a, b in ((0, 1000), (T - 777, T), (65536, 65536 + 300)):
+        part = colbert_head(xd[a:b], wd, None, lwd, None, 1e-5, residual=rd[a:b])
+        assert torch.equal(part, got[a:b]), (a, b)
+
+
 def test_colbert_head_refolds_an_updated_norm_weight(dev):
     """The folded weight follows the LayerNorm weight it was made from: an
     in-place update of it is seen by the next call."""
