@@ -123,10 +123,10 @@ def test_product_rejects_cpu_tensors():
 def test_varlen_workspace_bytes():
     from kernels import _lib
     lib = _lib.load()
-    # rotated K rounded up to 256 bytes, then one fp32 norm per (head, sequence, key tile)
+    # rotated K rounded up to 256 bytes, then four fp32 norms per (head, sequence, key tile)
     kr = (40265 * 12 * 64 * 2 + 255) // 256 * 256
-    assert lib.vfk_varlen_attn_workspace_bytes(_lib.BF16, 40265, 12, 1, 64, 768) == kr + 12 * 64 * 12 * 4
-    assert lib.vfk_varlen_attn_workspace_bytes(_lib.F16, 7, 3, 1, 2, 5) == 7 * 3 * 128 + 256 - 7 * 3 * 128 % 256 + 3 * 2 * 1 * 4
+    assert lib.vfk_varlen_attn_workspace_bytes(_lib.BF16, 40265, 12, 1, 64, 768) == kr + 12 * 64 * 12 * 16
+    assert lib.vfk_varlen_attn_workspace_bytes(_lib.F16, 7, 3, 1, 2, 5) == 7 * 3 * 128 + 256 - 7 * 3 * 128 % 256 + 3 * 2 * 1 * 16
     assert lib.vfk_varlen_attn_workspace_bytes(_lib.BF16, 40265, 12, 0, 64, 768) == 0
     assert lib.vfk_varlen_attn_workspace_bytes(_lib.F32, 40265, 12, 1, 64, 768) == 0
 

@@ -746,36 +746,34 @@ __device__ inline float rope_q_apply(u32x4_t (&q)[4], const RopeQ& r) {
   return ss;
 }
 
-// Rotates a staged K tile row (thread t holds key t>>2, d chunks cp and cp+4
-// with cp = t&3); cs8 = the 8 (cos, sin) pairs of f = 8*cp .. 8*cp+7 for the
-// row's position, as loaded by rope_k_fetch.
+// cos/sin of one K row for one group of 8 rotary frequencies: the 8 (cos,
+// sin) pairs of f = 8 grp .. 8 grp + 7 at the row's position.
 struct RopeK {
   f32x4_t v[4];
 };
 
-__device__ inline void rope_k_fetch(RopeK& r, const float* __restrict__ table, int pos, bool valid) {
-  const int cp = threadIdx.x & 3;
-  const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-  const f32x4_t* t = reinterpret_cast<const f32x4_t*>(table + (int64_t)pos * 64 + 16 * cp);
+__device__ inline void rope_k_fetch(RopeK& r, const float* __restrict__ table, int pos, int grp) {
+  const f32x4_t* t = reinterpret_cast<const f32x4_t*>(table + (int64_t)pos * 64 + 16 * grp);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) r.v[i] = valid ? t[i] : z;
+  for (int i = 0; i < 4; ++i) r.v[i] = t[i];
 }
 
-// Rotates and multiplies by `scale` before the one rounding to 16 bits.
+// One 16-byte half of a rotate-half pair, rotated and multiplied by `scale`
+// before the one rounding to 16 bits: own holds dims d .. d + 7 of the row,
+// partner the dims 32 away, with the partner negated for the first half
+// (pneg = -1: x1 cos - x2 sin) and not for the second (+1: x2 cos + x1 sin).
 template <typename E>
-__device__ inline void rope_k_apply(u32x4_t& k0, u32x4_t& k1, const RopeK& r, float scale = 1.f) {
-  float a[8], b[8];
-  unpack8<E>(k0, a);
-  unpack8<E>(k1, b);
+__device__ inline u32x4_t rope_k_half(u32x4_t own, u32x4_t partner, const RopeK& r, float pneg,
+                                      float scale) {
+  float x[8], p[8];
+  unpack8<E>(own, x);
+  unpack8<E>(partner, p);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float cs_ = r.v[i >> 1][2 * (i & 1)], sn = r.v[i >> 1][2 * (i & 1) + 1];
-    const float x1 = a[i], x2 = b[i];
-    a[i] = (x1 * cs_ - x2 * sn) * scale;
-    b[i] = (x2 * cs_ + x1 * sn) * scale;
+    x[i] = (x[i] * cs_ + (pneg * p[i]) * sn) * scale;
   }
-  k0 = pack8<E>(a);
-  k1 = pack8<E>(b);
+  return pack8<E>(x);
 }
 
 }  // namespace vfk

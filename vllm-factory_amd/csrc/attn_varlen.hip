@@ -13,7 +13,8 @@
 //
 // With RoPE the pre-pass also folds c = softmax_scale * log2(e) into K before
 // its one rounding to 16 bits, so the QK^T MFMA yields scores in log2 units,
-// and records the largest row norm of every 64-key tile. From |q| and those
+// and records the largest row norm of each 16 rows of every 64-key tile (four
+// partial maxima per tile). From |q| and those
 // norms each wave bounds |score| <= |q| max|k| before its loop; where the
 // bound stays within log2(kPMax) for all its rows, p = exp2(score) is taken
 // directly (no running max, no rescale: it can neither overflow the fp32
@@ -37,7 +38,8 @@ struct VarlenArgs {
   const float* rope;        // optional [positions][32][2] (cos, sin) table
   const uint8_t* key_valid; // optional, [T]
   const void* kr;           // RoPE: rotated, scaled K, head-major [H][T][64]
-  float* kmax;              // RoPE: max row norm of each key tile [H][nseq][nkt], or
+  float* kmax;              // RoPE: max row norm of each 16 rows of each key tile
+                            // [H][nseq][nkt][4], or
                             // (kblk32) of each 32-token block of the stream [H][ceil(T / 32)]
   int nkt;                  // key tiles per sequence slot: ceil(max_seqlen / 64)
   int kblk32;               // kmax holds 32-token stream blocks (K from the fused projection)
@@ -71,18 +73,36 @@ __global__ __launch_bounds__(256) void rope_table_kernel(RopeTableArgs a) {
 constexpr int kPenOff = 192;
 constexpr int kPenLen = 2 * kPenOff;
 
-// K rotation pre-pass: block (s, kt, g) rotates rows [64 kt, 64 kt + 64) of
-// sequence s for heads [kPackHeads g, kPackHeads g + kPackHeads); thread t
-// handles row t >> 2 and d chunks cp = t & 3 and cp + 4 (the rotate-half
-// partners d and d + 32), loading the row's cos/sin once for its heads. All
-// of a thread's loads are issued before any store, with head and row indices
-// clamped so that the loads are unconditional; one pass per block, no head
-// loop. The rows are stored multiplied by c2 = softmax_scale * log2(e), and
-// the largest Euclidean norm of the tile's stored rows per head goes to
-// kmax[h][s][kt].
-constexpr int kPackHeads = 6;
+// K rotation pre-pass: block (s, g, hg) rotates rows [16 g, 16 g + 16) of
+// sequence s for heads [2 NPAIR hg, 2 NPAIR hg + 2 NPAIR). Each 16-lane group
+// owns one row and covers two heads per load: lane i of a head's 8 holds 16
+// bytes of its 128-byte row, chunk i (i < 4) or 11 - i (i >= 4), so that every
+// load and store instruction moves whole 128-byte lines (half-line pieces
+// held the pass ~30 % below the copy rate), and the rotate-half partners
+// (dims d and d + 32) sit in lanes i and 7 - i, swapped by a DPP
+// row_half_mirror. All loads are issued before any store, with head indices
+// clamped so that the loads are unconditional. The rows are stored multiplied
+// by c2 = softmax_scale * log2(e); the largest Euclidean norm of the block's
+// stored rows per head goes to kmax[h][s][kt][g & 3] (kt = g / 4, four
+// partial maxima per 64-key tile), and the slots of a live tile that lie past
+// the sequence end get 0.
+constexpr int kPackRows = 16;
+
+// DPP row_half_mirror: the value of lane 7 - i of the lane's group of 8.
+__device__ inline uint32_t mirror8(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false);
+}
+
+// max over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the 4 rows of a wave)
+__device__ inline float rows_max4(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+  v = fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
 
 __device__ inline float wave_max(float v) { return group_max<64>(v); }
+__device__ inline float max4(f32x4_t v) { return fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])); }
 
 template <typename E>
 __device__ inline float sumsq8(u32x4_t v) {
@@ -94,63 +114,73 @@ __device__ inline float sumsq8(u32x4_t v) {
   return r;
 }
 
-template <typename E>
-__global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int nkt) {
-  __shared__ float part[4][kPackHeads];
-  const int kt = blockIdx.x % nkt;
-  const int s = blockIdx.x / nkt;
+template <typename E, int NPAIR>
+__global__ __launch_bounds__(256) void rope_k_pack_kernel(VarlenArgs a, int ngrp, int nhg) {
+  __shared__ float part[4][2 * NPAIR];
+  // blocks (s, g, head group) in that order, each XCD a contiguous share:
+  // sequence s is rotated on the XCD whose attention workgroups read it
+  // (the attention's items are dealt the same way), so those find its rows
+  // in their L2
+  const int pb = xcd_remap(blockIdx.x, gridDim.x);
+  const int hg = pb % nhg;
+  const int g = (pb / nhg) % ngrp;
+  const int s = pb / (nhg * ngrp);
   const int tok0 = a.cu[s];
   const int nfull = a.cu[s + 1] - tok0;
   const int n = min(nfull, a.maxlen);
-  const int h0 = blockIdx.y * kPackHeads;
-  if (kt == nkt - 1 && nfull > n) {
+  const int h0 = hg * 2 * NPAIR;
+  const int t = threadIdx.x;
+  if (g == ngrp - 1 && nfull > n) {
     // a sequence longer than max_seqlen: the attention computes its first
     // max_seqlen rows; the rest of its output rows become zeros here
-    for (int u = 0; u < kPackHeads && h0 + u < a.H; ++u)
+    for (int u = 0; u < 2 * NPAIR && h0 + u < a.H; ++u)
       zero_rows_d64(reinterpret_cast<uint16_t*>(a.o) + (int64_t)tok0 * a.os[0] + (h0 + u) * a.os[1],
                     a.os[0], n, nfull);
   }
-  if (kt * 64 >= n) return;  // uniform: no row of the sequence in this tile
-  const int row = kt * 64 + (threadIdx.x >> 2);
-  const bool valid = row < n;
-  const int rr = valid ? row : kt * 64;  // tail threads load a valid row, store nothing
-  const int cp = threadIdx.x & 3;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  RopeK rk;
-  rope_k_fetch(rk, a.rope, rr, true);
-  const uint16_t* src = reinterpret_cast<const uint16_t*>(a.k) + (int64_t)(tok0 + rr) * a.ks[0] + 8 * cp;
-  uint16_t* dst = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(a.kr)) +
-                  (int64_t)(tok0 + row) * 64 + 8 * cp;
-  const int64_t hs = (int64_t)a.T * 64;
-  u32x4_t k0[kPackHeads], k1[kPackHeads];
-#pragma unroll
-  for (int u = 0; u < kPackHeads; ++u) {
-    const uint16_t* p = src + (int64_t)min(h0 + u, a.H - 1) * a.ks[1];
-    // non-temporal: K is read once here (the attention reads the rotated copy)
-    k0[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-    k1[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p + 32));
+  if (g * kPackRows >= n) {  // uniform: no row of the sequence in this block
+    if ((g >> 2) * 64 < n && t < 2 * NPAIR && h0 + t < a.H)
+      a.kmax[(((int64_t)(h0 + t) * a.nseq + s) * a.nkt + (g >> 2)) * 4 + (g & 3)] = 0.f;
+    return;
   }
+  const int row = g * kPackRows + (t >> 4);
+  const bool valid = row < n;
+  const int rr = valid ? row : g * kPackRows;  // tail rows load a valid row, store nothing
+  const int l = t & 15, i8 = l & 7, lw = t & 63, w = t >> 6;
+  const int ch = i8 < 4 ? i8 : 11 - i8;  // the lane's 16-byte chunk of the head row
+  RopeK rk;
+  rope_k_fetch(rk, a.rope, rr, ch & 3);
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(a.k) + (int64_t)(tok0 + rr) * a.ks[0] + 8 * ch;
+  u32x4_t kv[NPAIR];
 #pragma unroll
-  for (int u = 0; u < kPackHeads; ++u) {
+  for (int j = 0; j < NPAIR; ++j) {
+    const int h = min(h0 + 2 * j + (l >> 3), a.H - 1);
+    // non-temporal: K is read once here (the attention reads the rotated copy)
+    kv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + (int64_t)h * a.ks[1]));
+  }
+  uint16_t* dst = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(a.kr)) +
+                  (int64_t)(tok0 + row) * 64 + 8 * ch;
+  const int64_t hs = (int64_t)a.T * 64;
+  const float pneg = i8 < 4 ? -1.f : 1.f;
+#pragma unroll
+  for (int j = 0; j < NPAIR; ++j) {
+    const int h = h0 + 2 * j + (l >> 3);
+    u32x4_t pv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pv[e] = mirror8(kv[j][e]);
+    const u32x4_t r = rope_k_half<E>(kv[j], pv, rk, pneg, a.c2);
     float nrm = 0.f;
-    if (h0 + u < a.H) {
-      rope_k_apply<E>(k0[u], k1[u], rk, a.c2);
-      if (valid) {
-        uint16_t* q = dst + (h0 + u) * hs;
-        *reinterpret_cast<u32x4_t*>(q) = k0[u];
-        *reinterpret_cast<u32x4_t*>(q + 32) = k1[u];
-        nrm = sumsq8<E>(k0[u]) + sumsq8<E>(k1[u]);
-      }
+    if (valid && h < a.H) {
+      *reinterpret_cast<u32x4_t*>(dst + h * hs) = r;
+      nrm = sumsq8<E>(r);
     }
-    // squared row norm (the row's 4 threads form a quad), then the wave's max
-    nrm = wave_max(group_sum<4>(nrm));
-    if (lane == 0) part[w][u] = nrm;
+    // squared row norm (the head row's 8 lanes), then the max over the wave's rows
+    nrm = rows_max4(group_sum<8>(nrm));
+    if ((lw & ~8) == 0) part[w][2 * j + (lw >> 3)] = nrm;
   }
   __syncthreads();
-  const int t = threadIdx.x;
-  if (t < kPackHeads && h0 + t < a.H) {
+  if (t < 2 * NPAIR && h0 + t < a.H) {
     const float m = fmaxf(fmaxf(part[0][t], part[1][t]), fmaxf(part[2][t], part[3][t]));
-    a.kmax[((int64_t)(h0 + t) * a.nseq + s) * a.nkt + kt] = sqrtf(m);
+    a.kmax[(((int64_t)(h0 + t) * a.nseq + s) * a.nkt + (g >> 2)) * 4 + (g & 3)] = sqrtf(m);
   }
 }
 
@@ -247,19 +277,20 @@ struct VarlenLds {
 // arguments and offsets, then Q and the first K/V tiles) instead of three.
 template <bool ROPE, bool LOCAL>
 __device__ inline void varlen_item_prefetch(const VarlenArgs& a, int s, int h, int qt, RopeQ& rq,
-                                            float& kx) {
+                                            f32x4_t& kx) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int q0 = qt * kBM;
   const int qrow = q0 + w * 32 + (lane & 31);
   const int kt_lo = LOCAL ? max(0, q0 - a.window) / kBN : 0;
-  kx = 0.f;
+  kx = f32x4_t{0.f, 0.f, 0.f, 0.f};
   if (ROPE) {
     // rows past the sequence end rotate zeros: any table row will do
     rope_q_fetch(rq, a.rope + (int64_t)min(qrow, a.maxlen - 1) * 64);
     // lanes past the last tile slot load slot nkt - 1 (no branch: a divergent
     // one here would make the offsets loaded next vector loads)
     if (!a.kblk32)
-      kx = a.kmax[((int64_t)h * a.nseq + s) * a.nkt + min(kt_lo + lane, a.nkt - 1)];
+      kx = *reinterpret_cast<const f32x4_t*>(
+          a.kmax + (((int64_t)h * a.nseq + s) * a.nkt + min(kt_lo + lane, a.nkt - 1)) * 4);
   }
 }
 
@@ -268,33 +299,34 @@ __device__ inline void varlen_item_prefetch(const VarlenArgs& a, int s, int h, i
 template <bool ROPE, bool LOCAL>
 struct ItemPrefetch {
   const float* tab;  // the lane's Q-rotation table row
-  const float* km;   // the lane's key-norm slot
+  const float* km;   // the lane's key-norm slot (the tile's 4 partial maxima)
   __device__ ItemPrefetch(const VarlenArgs& a, int s, int h, int qt) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int q0 = qt * kBM;
     const int qrow = q0 + w * 32 + (lane & 31);
     const int kt_lo = LOCAL ? max(0, q0 - a.window) / kBN : 0;
     tab = ROPE ? a.rope + (int64_t)min(qrow, a.maxlen - 1) * 64 : nullptr;
-    km = (ROPE && !a.kblk32) ? a.kmax + ((int64_t)h * a.nseq + s) * a.nkt + min(kt_lo + lane, a.nkt - 1)
-                             : nullptr;
+    km = (ROPE && !a.kblk32)
+             ? a.kmax + (((int64_t)h * a.nseq + s) * a.nkt + min(kt_lo + lane, a.nkt - 1)) * 4
+             : nullptr;
   }
-  __device__ void issue(RopeQ& rq, float& kx) const {
-    kx = 0.f;
+  __device__ void issue(RopeQ& rq, f32x4_t& kx) const {
+    kx = f32x4_t{0.f, 0.f, 0.f, 0.f};
     if (ROPE) {
       rope_q_fetch(rq, tab);
-      if (km) kx = *km;
+      if (km) kx = *reinterpret_cast<const f32x4_t*>(km);
     }
   }
 };
 
 // One item: query rows q0 .. q0 + 127 (qt = q0 / 128) of head h of sequence
 // s (rows tok0 .. tok0 + n - 1 of the stream), n > q0, against every key of
-// the sequence the layer lets them see; rq / kx as varlen_item_prefetch
+// the sequence the layer lets them see; rq / kx4 as varlen_item_prefetch
 // left them. Leaves the item's output rows written and every LDS buffer free
 // once all waves have passed a barrier.
 template <typename E, bool ROPE, bool LOCAL, bool KVALID>
 __device__ inline void varlen_item(const VarlenArgs& a, const VarlenLds<LOCAL>& L, int s, int h,
-                                   int qt, int tok0, int n, const RopeQ& rq, float kx) {
+                                   int qt, int tok0, int n, const RopeQ& rq, f32x4_t kx4) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, hl = lane >> 5;
   const int q0 = qt * kBM;
   const int wq_lo = q0 + w * 32;
@@ -351,8 +383,11 @@ __device__ inline void varlen_item(const VarlenArgs& a, const VarlenLds<LOCAL>& 
     // |score| <= |q| max|k| over the workgroup's key tiles (scores are in
     // log2 units: K carries c2); the margin covers the fp32 norms and the
     // MFMA's fp32 accumulation
+    // the 4 partial maxima of the lane's tile, reduced only here so that the
+    // prologue never waits for their load
+    float kx = max4(kx4);
     if (a.kblk32) {
-      // stream blocks covering the workgroup's keys (a superset: still a bound)
+      // (kx is 0 here: no norms were prefetched) stream blocks covering the workgroup's keys (a superset: still a bound)
       const float* km = a.kmax + (int64_t)h * ((a.T + 31) >> 5);
       const int b0 = (tok0 + kt_begin * kBN) >> 5, b1 = (tok0 + min(kt_end * kBN, n) - 1) >> 5;
       for (int j = b0 + lane; j <= b1; j += 64) kx = fmaxf(kx, km[j]);
@@ -360,8 +395,8 @@ __device__ inline void varlen_item(const VarlenArgs& a, const VarlenLds<LOCAL>& 
       // the prefetched norms of tiles kt_begin + lane, kept where inside the
       // workgroup's range; tiles past the first 64 (sequences > 4096) here
       if (kt_begin + lane >= kt_end) kx = 0.f;
-      const float* km = a.kmax + ((int64_t)h * a.nseq + s) * a.nkt;
-      for (int j = kt_begin + 64 + lane; j < kt_end; j += 64) kx = fmaxf(kx, km[j]);
+      const f32x4_t* km = reinterpret_cast<const f32x4_t*>(a.kmax) + ((int64_t)h * a.nseq + s) * a.nkt;
+      for (int j = kt_begin + 64 + lane; j < kt_end; j += 64) kx = fmaxf(kx, max4(km[j]));
     }
     kx = wave_max(kx);
     // the rotation keeps |q|; rounding the rotated q to 16 bits grows each
@@ -414,7 +449,7 @@ __global__ __launch_bounds__(256, (LOCAL && KVALID) ? 3 : 4) void varlen_fwd_ker
   // with the offsets requested last); the sliding-window kernels keep the
   // offsets last, which holds them at 128 VGPRs without a spill.
   RopeQ rq;
-  float kx;
+  f32x4_t kx;
   int tok0, nfull;
   if (LOCAL) {
     varlen_item_prefetch<ROPE, LOCAL>(a, s, h, qt, rq, kx);
@@ -569,8 +604,9 @@ extern "C" int64_t vfk_varlen_attn_workspace_bytes(int32_t dtype, int64_t total_
   if (!rope || dtype == VFK_F32 || total_tokens <= 0 || num_heads <= 0 || num_seqs <= 0 ||
       max_seqlen <= 0)
     return 0;
+  // four partial key-norm maxima (one per 16 rows) per 64-key tile
   const int64_t nkt = (max_seqlen + 63) / 64;
-  return kr_bytes(total_tokens, num_heads) + (int64_t)num_heads * num_seqs * nkt * 4;
+  return kr_bytes(total_tokens, num_heads) + (int64_t)num_heads * num_seqs * nkt * 16;
 }
 
 extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
@@ -636,14 +672,23 @@ extern "C" int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
     const int nkt = ceil_div(max_seqlen, 64);
     a.nkt = nkt;
     a.kmax = reinterpret_cast<float*>(static_cast<char*>(workspace) + kr_bytes(T, H));
-    const int64_t pblocks = (int64_t)num_seqs * nkt;
+    const int ngrp = nkt * (64 / kPackRows);
+    // 4 head pairs per block where H is a multiple of 8 but not of 12, else 6
+    const int npair = (H % 8 == 0 && H % 12 != 0) ? 4 : 6;
+    const int nhg = (int)ceil_div(H, 2 * npair);
+    const int64_t pblocks = (int64_t)num_seqs * ngrp * nhg;
     if (pblocks >= (1ll << 31))
       return set_error(VFK_ERR_UNSUPPORTED, "vfk_varlen_attn_fwd: grid too large");
-    const dim3 pgrid((unsigned)pblocks, (unsigned)ceil_div(H, kPackHeads));
-    if (dt == VFK_BF16)
-      hipLaunchKernelGGL(rope_k_pack_kernel<BF16>, pgrid, dim3(256), 0, st, a, nkt);
-    else
-      hipLaunchKernelGGL(rope_k_pack_kernel<F16>, pgrid, dim3(256), 0, st, a, nkt);
+#define VFK_PACK(E, NP) \
+  hipLaunchKernelGGL((rope_k_pack_kernel<E, NP>), dim3((unsigned)pblocks), dim3(256), 0, st, a, ngrp, nhg)
+    if (dt == VFK_BF16) {
+      if (npair == 4) VFK_PACK(BF16, 4);
+      else VFK_PACK(BF16, 6);
+    } else {
+      if (npair == 4) VFK_PACK(F16, 4);
+      else VFK_PACK(F16, 6);
+    }
+#undef VFK_PACK
   }
   return launch_varlen(a, dt, rope, max_seqlen, st, "vfk_varlen_attn_fwd");
 }
