@@ -214,9 +214,9 @@ int vfk_varlen_attn_fwd(const vfk_tensor* q, const vfk_tensor* k,
 /* Workspace size of vfk_varlen_attn_fwd for total_tokens rows (q->size[0]),
  * num_heads heads, num_seqs sequences and max_seqlen: for 16-bit dtypes with
  * RoPE, the rotated and scaled K (head-major, total_tokens * num_heads * 64 * 2
- * bytes rounded up to 256) plus one fp32 row-norm maximum per (head,
- * sequence, 64-key tile) (num_heads * num_seqs * ceil(max_seqlen / 64) * 4
- * bytes); else 0. */
+ * bytes rounded up to 256) plus four fp32 row-norm maxima per (head,
+ * sequence, 64-key tile), one per 16 rows (num_heads * num_seqs *
+ * ceil(max_seqlen / 64) * 16 bytes); else 0. */
 int64_t vfk_varlen_attn_workspace_bytes(int32_t dtype, int64_t total_tokens,
                                         int32_t num_heads, int32_t rope,
                                         int32_t num_seqs, int32_t max_seqlen);

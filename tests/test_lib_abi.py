@@ -32,7 +32,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     from kernels import _lib
-    assert _lib.load().vfk_abi_version() == 18
+    assert _lib.load().vfk_abi_version() == 19
 
 
 def _host_t5(rel, bidirectional, nb, md):

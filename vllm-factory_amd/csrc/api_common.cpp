@@ -21,6 +21,6 @@ void clear_error() { g_last_error[0] = 0; }
 
 }  // namespace vfk
 
-extern "C" int vfk_abi_version(void) { return 18; }
+extern "C" int vfk_abi_version(void) { return 19; }
 
 extern "C" const char* vfk_last_error(void) { return vfk::g_last_error; }
