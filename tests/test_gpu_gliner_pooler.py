@@ -198,6 +198,44 @@ def test_gliner_span_hidden_matches_gathered_sum(dtype, N):
     assert torch.equal(nob, torch.relu(a.float()[src[:, 0]] + b.float()[src[:, 1]]).to(dtype))
 
 
+@pytest.mark.parametrize("dtype, N", [(torch.bfloat16, 3072), (torch.float32, 1000),
+                                      (torch.float16, 24)])
+@pytest.mark.parametrize("lead", [0, 5])
+def test_gliner_span_hidden_default_span_lists(dtype, N, lead):
+    """Default span lists only (every wave of 12 spans then shares one start
+    row, the kernel's one-load-per-start form), and the same lists after a
+    caller-given request of `lead` spans, so that the waves straddle two
+    starts; bit for bit against the fp32 sum over the oracle's rows, with and
+    without bias."""
+    from kernels.gliner_pooler import gliner_span_hidden
+    g = torch.Generator().manual_seed(31 + N + lead)
+    lens = [int(x) for x in torch.randint(1, 40, (9,), generator=g)]
+    idxs, masks = [], []
+    if lead:
+        lens = [6] + lens
+        idxs.append(torch.randint(0, 6, (lead, 2), generator=g))
+        masks.append(torch.ones(lead, dtype=torch.int64))
+    for L in lens[1 if lead else 0:]:
+        i, m = op.gliner_default_spans(L, L, 12)
+        idxs.append(i)
+        masks.append(m)
+    cu = lambda c: torch.tensor([0] + torch.tensor(c).cumsum(0).tolist(), dtype=torch.int32)
+    row_cu, span_cu = cu(lens), cu([i.shape[0] for i in idxs])
+    W = sum(lens)
+    a = torch.randn(W, N, generator=g).to(dtype)
+    b = torch.randn(W, N, generator=g).to(dtype)
+    bias = torch.randn(N, generator=g).to(dtype)
+    print(f"gliner span hidden default lists {dtype} N={N} lead={lead} spans={int(span_cu[-1])}",
+          flush=True)
+    src = _span_sources(lens, idxs, masks)
+    args = (row_cu.cuda(), torch.cat(idxs).cuda(), torch.cat(masks).cuda(), span_cu.cuda())
+    got = gliner_span_hidden(a.cuda(), b.cuda(), bias.cuda(), *args).cpu()
+    want = torch.relu((a.float()[src[:, 0]] + b.float()[src[:, 1]]) + bias.float()).to(dtype)
+    assert torch.equal(got, want)
+    nob = gliner_span_hidden(a.cuda(), b.cuda(), None, *args).cpu()
+    assert torch.equal(nob, torch.relu(a.float()[src[:, 0]] + b.float()[src[:, 1]]).to(dtype))
+
+
 def test_gliner_span_hidden_request_without_rows():
     """A request with no rows gives relu(bias) for each of its spans."""
     from kernels.gliner_pooler import gliner_span_hidden

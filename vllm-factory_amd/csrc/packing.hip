@@ -572,12 +572,45 @@ __device__ inline void st16_nt(uint8_t* p, const float* f) {
 // cat(start[i], end[j]) distributes over the halves, and W1 splits with
 // them). out[s] = relu(a[ra] + b[rb] + bias), summed in fp32 in that order and
 // rounded once; ra, rb as for the pair rows (a request without rows adds
-// nothing: relu(bias)). Each wave writes kSpansPerWave consecutive spans;
-// every lane loads the bias chunk once for all of them.
-constexpr int kHidPass = 2;  // 16-byte chunks per lane and span in one pass
+// nothing: relu(bias)).
+//
+// Each wave writes kHidSpans consecutive spans. The row loads, served from
+// L2, bound this kernel (its output stream alone runs near the HBM write
+// rate). Where the wave's spans are kHidStarts consecutive starts of the
+// default span list with all kHidWidths widths valid (span u = (i + u / 12,
+// i + u / 12 + u % 12)), the wave loads each of its 4 start rows and 15 end
+// rows once per chunk for all 48 spans: 20 row loads for 48 outputs where
+// span-by-span loading takes 96. Other span lists, and the starts whose
+// widths run past the text, run the wave's spans in groups of
+// kSpansPerWave, every span loading both of its rows.
+constexpr int kHidWidths = 12;
+constexpr int kHidStarts = 4;
+constexpr int kHidSpans = kHidStarts * kHidWidths;
+constexpr int kHidPass = 2;  // 16-byte chunks per lane and span in one pass of the group form
+
+__device__ inline int64_t readlane64(int64_t v, int l) {
+  const int lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const int hi = __builtin_amdgcn_readlane((int)(v >> 32), l);
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
 
 template <int EB>
-__global__ __launch_bounds__(256) void span_hidden_kernel(const uint8_t* __restrict__ a,
+__device__ inline void unpack16(u32x4_t v, float* f) {
+  if constexpr (EB == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(v[i]);
+  } else if constexpr (EB == 2) {
+    unpack8<BF16>(v, f);
+  } else {
+    unpack8<F16>(v, f);
+  }
+}
+
+// Three waves per SIMD (<= 168 VGPRs): the 48-span form holds 20 packed row
+// chunks and 4 unpacked start rows per lane; the compiler's own choice, 177
+// VGPRs and two waves, ran ~1 % slower.
+template <int EB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void span_hidden_kernel(const uint8_t* __restrict__ a,
                                                           const uint8_t* __restrict__ b,
                                                           const uint8_t* __restrict__ bias,
                                                           int64_t row_bytes, int64_t W,
@@ -588,21 +621,15 @@ __global__ __launch_bounds__(256) void span_hidden_kernel(const uint8_t* __restr
                                                           int64_t S, uint8_t* __restrict__ out) {
   constexpr int V = EB == 4 ? 4 : 8;  // values per 16 bytes (EB: 2 bf16, 3 fp16, 4 fp32)
   // each XCD takes a contiguous run of spans, so the rows that neighbouring
-  // spans share (a start row for max_width spans, an end row for the spans
-  // of nearby starts) are reused from that XCD's L2
+  // spans share are reused from that XCD's L2
   const int64_t blk = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t s0 = (blk * 4 + (threadIdx.x >> 6)) * kSpansPerWave;
+  const int64_t s0 = (blk * 4 + (threadIdx.x >> 6)) * kHidSpans;
   const int lane = threadIdx.x & 63;
   if (s0 >= S) return;
   const int chunks = (int)(row_bytes / 16);
+  const int ns = (int)min((int64_t)kHidSpans, S - s0);
   int64_t ra = -1, rb = -1;  // source rows of span s0 + lane
-  if (lane < kSpansPerWave && s0 + lane < S && W > 0) span_rows_of(row_cu, idx, mask, span_cu, n, s0 + lane, ra, rb);
-  int64_t sa[kSpansPerWave], sb[kSpansPerWave];
-#pragma unroll
-  for (int u = 0; u < kSpansPerWave; ++u) {
-    sa[u] = __shfl(ra, u, 64);
-    sb[u] = __shfl(rb, u, 64);
-  }
+  if (lane < ns && W > 0) span_rows_of(row_cu, idx, mask, span_cu, n, s0 + lane, ra, rb);
   // every load is unconditional: sources that do not exist (no bias, no
   // rows at all) are read from a valid row and their values replaced by 0
   const bool hb = bias != nullptr, hr = W > 0;
@@ -610,34 +637,88 @@ __global__ __launch_bounds__(256) void span_hidden_kernel(const uint8_t* __restr
   const uint8_t* src_b = hr ? b : (hb ? bias : out);
   const uint8_t* src_c = hb ? bias : src_a;
   const int64_t rs = hr ? row_bytes : 0, wmax = hr ? W - 1 : 0;
-  for (int c0 = 0; c0 < chunks; c0 += 64 * kHidPass) {
-    float bv[kHidPass][V], av[kSpansPerWave][kHidPass][V], cv[kSpansPerWave][kHidPass][V];
+  const int64_t a0 = readlane64(ra, 0);
+  const bool grid = hr && a0 >= 0 && ns == kHidSpans &&
+                    __builtin_amdgcn_ballot_w64(lane < kHidSpans &&
+                                                (ra != a0 + lane / kHidWidths ||
+                                                 rb != ra + lane % kHidWidths)) == 0ull;
+  if (grid) {
+    // start rows a0 .. a0 + 3 and end rows a0 .. a0 + 14, all valid rows
+    const uint8_t* arow = src_a + a0 * rs;
+    const uint8_t* brow = src_b + a0 * rs;
+    for (int c0 = 0; c0 < chunks; c0 += 64) {
+      const int c = c0 + lane;
+      const uint32_t off = (uint32_t)min(c, chunks - 1) * 16u;
+      const u32x4_t cq = *reinterpret_cast<const u32x4_t*>(src_c + off);
+      u32x4_t aq[kHidStarts], bq[kHidStarts + kHidWidths - 1];
 #pragma unroll
-    for (int k = 0; k < kHidPass; ++k) {
-      const int64_t c16 = (int64_t)min(c0 + lane + 64 * k, chunks - 1) * 16;
-      ld16<EB>(src_c + c16, bv[k]);
+      for (int i = 0; i < kHidStarts; ++i) aq[i] = *reinterpret_cast<const u32x4_t*>(arow + i * rs + off);
 #pragma unroll
-      for (int u = 0; u < kSpansPerWave; ++u) {
-        ld16<EB>(src_a + min(max(sa[u], (int64_t)0), wmax) * rs + c16, av[u][k]);
-        ld16<EB>(src_b + min(max(sb[u], (int64_t)0), wmax) * rs + c16, cv[u][k]);
+      for (int j = 0; j < kHidStarts + kHidWidths - 1; ++j)
+        bq[j] = *reinterpret_cast<const u32x4_t*>(brow + j * rs + off);
+      float cv[V], av[kHidStarts][V];
+      unpack16<EB>(cq, cv);
+#pragma unroll
+      for (int i = 0; i < kHidStarts; ++i) unpack16<EB>(aq[i], av[i]);
+      // end row j serves start i at width j - i; each end row is unpacked once
+      // and its outputs written before the next (predicated, not branched
+      // out of: the loops must unroll fully so that bq stays in registers)
+#pragma unroll
+      for (int j = 0; j < kHidStarts + kHidWidths - 1; ++j) {
+        float bv[V];
+        unpack16<EB>(bq[j], bv);
+#pragma unroll
+        for (int i = 0; i < kHidStarts; ++i) {
+          const int w = j - i;
+          if (w < 0 || w >= kHidWidths) continue;  // compile-time: fully unrolled
+          float y[V];
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            const float v = (av[i][e] + bv[e]) + (hb ? cv[e] : 0.f);
+            y[e] = v < 0.f ? 0.f : v;
+          }
+          if (c < chunks) st16_nt<EB>(out + (s0 + i * kHidWidths + w) * row_bytes + (int64_t)c * 16, y);
+        }
       }
     }
+    return;
+  }
+  for (int g0 = 0; g0 < ns; g0 += kSpansPerWave) {
+    int64_t sa[kSpansPerWave], sb[kSpansPerWave];
 #pragma unroll
     for (int u = 0; u < kSpansPerWave; ++u) {
-      if (s0 + u >= S) break;
-      const bool has = hr && sa[u] >= 0;
+      sa[u] = readlane64(ra, min(g0 + u, kHidSpans - 1));
+      sb[u] = readlane64(rb, min(g0 + u, kHidSpans - 1));
+    }
+    for (int c0 = 0; c0 < chunks; c0 += 64 * kHidPass) {
+      float bv[kHidPass][V], av[kSpansPerWave][kHidPass][V], cv[kSpansPerWave][kHidPass][V];
 #pragma unroll
       for (int k = 0; k < kHidPass; ++k) {
-        const int c = c0 + lane + 64 * k;
-        if (c >= chunks) continue;
-        float y[V];
+        const int64_t c16 = (int64_t)min(c0 + lane + 64 * k, chunks - 1) * 16;
+        ld16<EB>(src_c + c16, bv[k]);
 #pragma unroll
-        for (int e = 0; e < V; ++e) {
-          const float bb = hb ? bv[k][e] : 0.f;
-          const float v = has ? (av[u][k][e] + cv[u][k][e]) + bb : bb;
-          y[e] = v < 0.f ? 0.f : v;
+        for (int u = 0; u < kSpansPerWave; ++u) {
+          ld16<EB>(src_a + min(max(sa[u], (int64_t)0), wmax) * rs + c16, av[u][k]);
+          ld16<EB>(src_b + min(max(sb[u], (int64_t)0), wmax) * rs + c16, cv[u][k]);
         }
-        st16_nt<EB>(out + (s0 + u) * row_bytes + (int64_t)c * 16, y);
+      }
+#pragma unroll
+      for (int u = 0; u < kSpansPerWave; ++u) {
+        if (g0 + u >= ns) break;
+        const bool has = hr && sa[u] >= 0;
+#pragma unroll
+        for (int k = 0; k < kHidPass; ++k) {
+          const int c = c0 + lane + 64 * k;
+          if (c >= chunks) continue;
+          float y[V];
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            const float bb = hb ? bv[k][e] : 0.f;
+            const float v = has ? (av[u][k][e] + cv[u][k][e]) + bb : bb;
+            y[e] = v < 0.f ? 0.f : v;
+          }
+          st16_nt<EB>(out + (s0 + g0 + u) * row_bytes + (int64_t)c * 16, y);
+        }
       }
     }
   }
@@ -960,7 +1041,7 @@ extern "C" int vfk_gliner_span_hidden(const void* a, const void* b, const void* 
   if (num_requests <= 0 || num_rows < 0 || num_spans < 0 || num_spans >= (1ll << 31) - 1)
     return set_error(VFK_ERR_INVALID, "%s: bad sizes", name);
   if (num_spans == 0) return VFK_OK;
-  const dim3 grid((unsigned)ceil_div(num_spans, 4 * kSpansPerWave));
+  const dim3 grid((unsigned)ceil_div(num_spans, 4 * kHidSpans));
   hipStream_t st = (hipStream_t)stream;
   const uint8_t* ap = static_cast<const uint8_t*>(a);
   const uint8_t* bp = static_cast<const uint8_t*>(b);
