@@ -143,6 +143,40 @@ def test_gliner_span_rows(dtype, D):
         assert torch.equal(got[int(span_cu[r]):int(span_cu[r + 1])], want), f"request {r}"
 
 
+@pytest.mark.parametrize("dtype, D", [(torch.bfloat16, 768), (torch.float32, 1000),
+                                      (torch.float16, 24)])
+@pytest.mark.parametrize("lead", [0, 5])
+def test_gliner_span_rows_default_span_lists(dtype, D, lead):
+    """Default span lists only (waves of 48 spans then cover 4 starts x 12
+    widths, the kernel's one-load-per-row form), and the same after a
+    caller-given request of `lead` spans (waves straddle starts): bit for bit
+    against the oracle's pair rows."""
+    from kernels.gliner_pooler import gliner_span_rows
+    g = torch.Generator().manual_seed(61 + D + lead)
+    lens = [int(x) for x in torch.randint(1, 45, (9,), generator=g)]
+    idxs, masks = [], []
+    if lead:
+        lens = [6] + lens
+        idxs.append(torch.randint(0, 6, (lead, 2), generator=g))
+        masks.append(torch.ones(lead, dtype=torch.int64))
+    for L in lens[1 if lead else 0:]:
+        i, m = op.gliner_default_spans(L, L, 12)
+        idxs.append(i)
+        masks.append(m)
+    cu = lambda c: torch.tensor([0] + torch.tensor(c).cumsum(0).tolist(), dtype=torch.int32)
+    row_cu, span_cu = cu(lens), cu([i.shape[0] for i in idxs])
+    W = sum(lens)
+    start = torch.randn(W, D, generator=g).to(dtype)
+    end = torch.randn(W, D, generator=g).to(dtype)
+    print(f"gliner span rows default lists {dtype} D={D} lead={lead} spans={int(span_cu[-1])}",
+          flush=True)
+    got = gliner_span_rows(start.cuda(), end.cuda(), row_cu.cuda(), torch.cat(idxs).cuda(),
+                           torch.cat(masks).cuda(), span_cu.cuda()).cpu()
+    want = torch.cat([op.gliner_span_rows(start[a:b], end[a:b], i, m)
+                      for a, b, i, m in zip(row_cu[:-1].tolist(), row_cu[1:].tolist(), idxs, masks)])
+    assert torch.equal(got, want)
+
+
 def test_gliner_span_rows_special_values():
     """ReLU on the bits: negatives (-0 and -inf included) become +0, NaN and
     +inf pass; an empty request gives zero rows."""
