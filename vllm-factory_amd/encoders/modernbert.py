@@ -121,8 +121,8 @@ def _encode(ids: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int, w: Mod
     """Embeddings and layers; returns (pending MLP output or None, residual
     stream) before the final LayerNorm. fuse_qkv_rope: Wqkv and the k rotation
     as one kernel (qkv_rope_projection) where the weights allow it; off by
-    default, since hipBLASLt plus the k pass measures 2-3 % faster per layer
-    at 163 736 tokens. fuse_dense_ln: the attention output's Wo, residual add
+    default, since hipBLASLt plus the k pass measures about 5 % faster per
+    layer at 163 736 tokens. fuse_dense_ln: the attention output's Wo, residual add
     and mlp_norm as one kernel (dense_add_layernorm, which also writes the
     new residual stream) where _dense_ln_fusable allows it; off by default:
     the 22-layer forward at 163 736 tokens takes 52.21 ms with it and
