@@ -69,6 +69,26 @@ def test_modernbert_varlen_cut_at_max_seqlen(dev, window, theta, dtype):
     _check(got, want, cu, cut_cu, f"varlen w={window} theta={theta} {dtype}")
 
 
+@pytest.mark.parametrize("H", [1, 3, 16, 20, 24])
+@pytest.mark.parametrize("window,theta", [(-1, 160000.0), (64, 10000.0)])
+def test_modernbert_varlen_head_counts(dev, H, window, theta):
+    """Head counts other than 12 through the K pre-pass's head groups: 4 head
+    pairs per block for 16, 6 for the others, two groups for 16, 20 (the
+    second clamped at the last head) and 24, one partly filled group for 1 and
+    3; the cut rows of every head are zeroed by its group's blocks."""
+    from kernels.varlen_attention import varlen_rope_attention
+    qkv, cu = _pack(H, 60 + H)
+    out = torch.full(qkv[:, 0].shape, float("nan"), dtype=qkv.dtype, device=dev)
+    qd = qkv.to(dev)
+    print(f"head counts H={H} window={window}", flush=True)
+    got = varlen_rope_attention(qd[:, 0], qd[:, 1], qd[:, 2], cu.to(dev), MAXLEN, window=window,
+                                rope_theta=theta, softmax_scale=0.125, out=out)
+    cut, cut_cu = _cut(qkv, cu)
+    want = oa.varlen_attention(cut[:, 0], cut[:, 1], cut[:, 2], cut_cu, window=window,
+                               rope_theta=theta, softmax_scale=0.125)
+    _check(got, want, cu, cut_cu, f"varlen H={H} w={window}")
+
+
 def test_rpb_varlen_cut_at_max_seqlen(dev):
     from kernels.flash_attention_rpb import flash_attention_rpb_varlen
     H = 8
