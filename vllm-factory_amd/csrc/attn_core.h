@@ -628,11 +628,14 @@ __device__ inline void pv_tile_sw(const uint16_t* __restrict__ Vt, const VOff& v
 //                                       masks; returns "exact" for softmax_exp
 // ---------------------------------------------------------------------------
 
-// Issues the loads and metadata of tiles 0 and 1; call before the Q set-up so
-// that their latency overlaps it, then attn_loop_db.
+// Issues the loads and metadata of tiles 0 and 1 (K and V of both); call
+// before the Q set-up so that their latency overlaps it, then attn_loop_db.
+// With tile 1's V issued here rather than in the first step, the first
+// step's barrier waits for no load issued just before it.
 template <typename P>
 __device__ inline void attn_pipe_start(P& pol, int n, uint16_t* __restrict__ K0,
-                                       uint16_t* __restrict__ K1, uint16_t* __restrict__ V0) {
+                                       uint16_t* __restrict__ K1, uint16_t* __restrict__ V0,
+                                       uint16_t* __restrict__ V1) {
   if (n <= 0) return;
   const auto m0 = pol.meta_ld(0);
   pol.loadK(0, K0);
@@ -641,6 +644,7 @@ __device__ inline void attn_pipe_start(P& pol, int n, uint16_t* __restrict__ K0,
   if (n > 1) {
     const auto m1 = pol.meta_ld(1);
     pol.loadK(1, K1);
+    pol.loadV(1, V1);
     pol.meta_st(m1, 1);
   }
 }
@@ -663,12 +667,13 @@ __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t*
                   uint16_t* __restrict__ Kn, uint16_t* __restrict__ Vn, int b) {
     ko.refresh();
     vo.refresh();
-    // tile 1's K and meta were issued with tile 0; the next tile's metadata is
-    // loaded before its DMA and written to LDS after this tile's compute
+    // tile 1's K, V and meta were issued with tile 0; the next tile's
+    // metadata is loaded before its DMA and written to LDS after this tile's
+    // compute
     const bool meta_next = i + 1 < n && i > 0;
     const auto mn = pol.meta_ld(meta_next ? i + 1 : i);
-    if (i + 1 < n) {
-      if (i > 0) pol.loadK(i + 1, Kn);
+    if (meta_next) {
+      pol.loadK(i + 1, Kn);
       pol.loadV(i + 1, Vn);
     }
     if (wave_on && (P::kAllActive || __builtin_amdgcn_readfirstlane((int)pol.active(i)) != 0)) {

@@ -286,7 +286,7 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   pol.wq_hi = min(pol.wq_lo + 31, Lq - 1);
   // lut index of element e in the tile at key0: key0 + x_key(e, 0) + lut_base
   pol.lut_base = 4 * hl - w * 32 - (lane & 31) + (kBM - 1);
-  attn_pipe_start(pol, n, K0, K1, V0);
+  attn_pipe_start(pol, n, K0, K1, V0, V1);
 
   const bool qvalid = pol.qrow < Lq;
   u32x4_t qf[4];

@@ -365,7 +365,7 @@ __device__ inline void varlen_item(const VarlenArgs& a, const VarlenLds<LOCAL>& 
   pol.wq_lo = wq_lo; pol.wq_hi = min(wq_lo + 31, n - 1); pol.window = a.window; pol.tail0 = tail0;
   pol.kmask = L.kmask; pol.kflag = L.kflag; pol.pen = L.pen;
 
-  attn_pipe_start(pol, kt_end - kt_begin, L.K0, L.K1, L.V0);
+  attn_pipe_start(pol, kt_end - kt_begin, L.K0, L.K1, L.V0, L.V1);
 
   u32x4_t qf[4];
   load_q(qf, Qp + (int64_t)qrow * a.qs[0], qvalid);
