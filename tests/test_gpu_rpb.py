@@ -117,6 +117,41 @@ def test_strided_inputs(dev):
     assert_attn_close(got, want, "strided")
 
 
+@pytest.mark.parametrize("case", ["overflow", "underflow", "mixed"])
+@pytest.mark.parametrize("masked", [False, True])
+def test_fixed_pass_fallback(dev, case, masked):
+    """The bf16 kernel first takes p = exp2(c s) without a running max, and
+    runs a workgroup again with it where a row sum or output is not finite or
+    below 2^-64. Cases that need the second run: scores that overflow 2^127
+    (q = k, |q|^2 ~ 1000), scores all far below 0 (a table of -300), and a
+    batch where only the second row's items overflow; with and without a key
+    mask (the two kernels that take the first pass)."""
+    g = torch.Generator().manual_seed(11)
+    B, H, L = 2, 3, 200
+    q = torch.randn(B, H, L, 64, generator=g) * 0.5
+    k = torch.randn(B, H, L, 64, generator=g) * 0.5
+    v = torch.randn(B, H, L, 64, generator=g)
+    table = torch.randn(32, H, generator=g) * 0.1
+    if case == "overflow":
+        q = torch.randn(B, H, L, 64, generator=g) * 4.0
+        k = q.clone()
+    elif case == "underflow":
+        table = torch.full((32, H), -300.0)
+    else:
+        q[1] = torch.randn(H, L, 64, generator=g) * 4.0
+        k[1] = q[1]
+    q, k, v = (t.bfloat16() for t in (q, k, v))
+    mask = None
+    if masked:
+        mask = torch.zeros(B, 1, 1, L)
+        mask[:, :, :, 170:] = torch.finfo(torch.float32).min
+    want = oa.rpb_attention(q, k, v, table, 32, 128, False, mask, 1.0)
+    got = _rpb()(q.to(dev), k.to(dev), v.to(dev), table.to(dev), 32, 128, False,
+                 padding_mask=None if mask is None else mask.to(dev))
+    assert torch.isfinite(got.float()).all(), f"{case}: non-finite output"
+    assert_attn_close(got, want, f"fallback {case} masked={masked}")
+
+
 def test_all_keys_masked_row_is_uniform(dev):
     """A batch row whose keys are all masked averages V uniformly, as the
     reference's finite additive mask does."""

@@ -177,6 +177,31 @@ struct RowSumAdd {
   __device__ float total() const { return half_swap_sum(l); }
 };
 
+// RowSumDot: the 16-bit probabilities P summed by packed dot products with
+// (1, 1): 16 v_dot2 per tile instead of 31 adds, and, as with RowSumMfma,
+// the denominator sums exactly the rounded weights of the numerator (with
+// the fp32 sums a row dominated by one key whose weight rounds would be off
+// by that rounding). One register, like RowSumAdd.
+template <typename E>
+struct RowSumDot {
+  float l = 0.f;
+  static constexpr bool kF32 = false;
+  __device__ void scale(float a) { l *= a; }
+  __device__ void add_f32(const f32x16_t&, const f32x16_t&) {}
+  __device__ void add_p(const u32x4_t (&p)[4]) {
+    float la = 0.f, lb = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      la = E::dot2_ones(p[0][j], la);
+      lb = E::dot2_ones(p[1][j], lb);
+      la = E::dot2_ones(p[2][j], la);
+      lb = E::dot2_ones(p[3][j], lb);
+    }
+    l += la + lb;
+  }
+  __device__ float total() const { return half_swap_sum(l); }
+};
+
 template <typename E>
 struct RowSumMfma {
   f32x4_t acc = {};
@@ -268,16 +293,20 @@ __device__ inline void softmax_exp(f32x16_t& s0, f32x16_t& s1, float c, float m,
   l.add_p(p);
 }
 
-// Probabilities without a reference: p = exp2(s) for scores already in log2
-// units and known to satisfy |s| <= log2(E::kPMax) (a bound computed from
-// |q| and max |k| before the loop), so p can neither overflow the fp32
-// accumulators nor underflow the 16-bit P operand; no row max, no rescale.
+// Probabilities without a reference: p = exp2(c s), no row max, no rescale.
+// Callers either know that |c s| <= log2(E::kPMax) (the varlen kernels: a
+// bound from |q| and max |k| before the loop, scores already in log2 units,
+// c = 1), so p can neither overflow the fp32 accumulators nor underflow the
+// 16-bit P operand, or check the row sums and outputs afterwards and run the
+// item again with the running max where they are not finite or too small
+// (the bf16 RPB kernel).
 template <typename E, typename RS>
-__device__ inline void softmax_fixed(f32x16_t& s0, f32x16_t& s1, u32x4_t (&p)[4], RS& l) {
+__device__ inline void softmax_fixed(f32x16_t& s0, f32x16_t& s1, u32x4_t (&p)[4], RS& l,
+                                     float c) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    s0[i] = fast_exp2(s0[i]);
-    s1[i] = fast_exp2(s1[i]);
+    s0[i] = fast_exp2(s0[i] * c);
+    s1[i] = fast_exp2(s1[i] * c);
   }
   l.add_f32(s0, s1);
   pack_p<E>(s0, s1, p);
@@ -649,8 +678,9 @@ __device__ inline void attn_pipe_start(P& pol, int n, uint16_t* __restrict__ K0,
   }
 }
 
-// FIXED: scores arrive in log2 units within +-log2(E::kPMax) (softmax_fixed);
-// otherwise the online softmax with running max m and scale c.
+// FIXED: p = exp2(c s) with no running max (softmax_fixed: the caller bounds
+// the scores or checks the result); otherwise the online softmax with running
+// max m and scale c.
 template <typename E, bool FIXED = false, typename P, typename RS>
 __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t* __restrict__ K1,
                                     uint16_t* __restrict__ V0, uint16_t* __restrict__ V1, int n,
@@ -685,7 +715,7 @@ __device__ inline void attn_loop_db(P& pol, uint16_t* __restrict__ K0, uint16_t*
       const bool exact = pol.modify(s0, s1, i, b);
       u32x4_t p[4];
       if (FIXED)
-        softmax_fixed<E>(s0, s1, p, l);
+        softmax_fixed<E>(s0, s1, p, l, c);
       else
         softmax_tile<E>(s0, s1, c, m, l, o0, o1, p, exact);
       pv_tile_sw<E>(Vc, vo, p, o0, o1);

@@ -9,6 +9,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "attn_core.h"
 #include "launch_util.h"
@@ -158,6 +159,7 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   __shared__ float tailm[kBN];
   __shared__ int ntl;
   __shared__ int nolive_s;
+  __shared__ int spec_bad;  // some row of the fixed-softmax pass failed its check
   extern __shared__ __align__(16) unsigned char smem[];
   const int nqt = (a.Lq + kBM - 1) / kBM;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
@@ -192,6 +194,7 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
 
   // keys past Lk in the partial last tile (read before the first barrier)
   if (t < kBN) tailm[t] = ((Lk - 1) / kBN) * kBN + t < Lk ? 0.f : -INFINITY;
+  if (t == 0) spec_bad = 0;
 
   // ---- bias table over rel = key - query, rel in [-(q0+127), Lk-1-q0] ----
   // the step thresholds and the head's table column go to LDS first, so each
@@ -293,11 +296,43 @@ __global__ __launch_bounds__(256, 4) void rpb_fwd_kernel(RpbArgs a) {
   load_q(qf, reinterpret_cast<const uint16_t*>(a.q) + qo + h * a.qs[1] + (int64_t)pol.qrow * a.qs[2],
          qvalid);
 
-  float m = -INFINITY;
-  RowSumAdd l;
+  // bf16: first p = exp2(c2 s) with no running max. T5 does not scale its
+  // scores, so no bound known before the loop keeps them small, but bf16 and
+  // the fp32 sums hold p up to 2^127: the pass fails only for rows whose sum
+  // or outputs overflow, or whose sum is below 2^-64 (every score far below
+  // 0, where low probabilities would flush to zero). Such a workgroup runs
+  // the item again with the running max. fp16 (p at most 65504) and the full
+  // [L, L] mask (whose second loop would not fit the registers) always take
+  // the running max.
+  constexpr bool kSpec = std::is_same<E, BF16>::value && MASK != MASK_FULL;
+  float m = -INFINITY, l_tot = 0.f;
+  RowSumDot<E> l;
   f32x16_t o0 = {}, o1 = {};
-  attn_loop_db<E>(pol, K0, K1, V0, V1, n, qf, a.c2, m, l, o0, o1);
-  const float l_tot = l.total();
+  bool rerun = !kSpec;
+  if (kSpec) {
+    attn_loop_db<E, true>(pol, K0, K1, V0, V1, n, qf, a.c2, m, l, o0, o1);
+    l_tot = l.total();
+    float fin = l_tot * 0.f;  // NaN when anything below is not finite
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      fin = __builtin_fmaf(o0[i], 0.f, fin);
+      fin = __builtin_fmaf(o1[i], 0.f, fin);
+    }
+    const bool bad = qvalid && n > 0 && (fin != 0.f || !(l_tot >= 0x1p-64f));
+    if (__builtin_amdgcn_ballot_w64(bad) != 0ull && lane == 0) spec_bad = 1;
+    __syncthreads();
+    rerun = spec_bad != 0;
+    if (rerun) {
+      l = RowSumDot<E>{};
+      o0 = f32x16_t{};
+      o1 = f32x16_t{};
+      attn_pipe_start(pol, n, K0, K1, V0, V1);  // the first tiles again
+    }
+  }
+  if (rerun) {
+    attn_loop_db<E>(pol, K0, K1, V0, V1, n, qf, a.c2, m, l, o0, o1);
+    l_tot = l.total();
+  }
   // whole-row stores through this wave's half of K0 / K1 (free after the loop)
   uint16_t* ob = reinterpret_cast<uint16_t*>(a.o) + oo + h * a.os[1];
   const int wq_lo = pol.wq_lo;
