@@ -1,14 +1,14 @@
 """Register budget of the gfx950 kernels (CPU: hipcc cross-compiles).
 
-The attention kernels run four waves per SIMD at <= 128 VGPRs (the
-sliding-window kernels with a key mask three, at <= 168); a change that
+The attention kernels run four waves per SIMD at <= 128 VGPRs; a change that
 pushes one past its budget makes the compiler spill to scratch memory, which
 costs far more than the change saves and shows up in no parity test. This
 test compiles each kernel source to AMD assembly and compares every kernel's
 .vgpr_spill_count with the committed maximum: 0 for every kernel but the two
 bf16 RPB kernels with a key mask, which hold their second, running-max pass
-next to the first: 2 registers stored before a tile loop and reloaded
-after it, never inside one.
+next to the first, and the sliding-window varlen kernels with a key mask:
+1 or 2 registers stored before a tile loop and reloaded after it, never
+inside one.
 
 It also checks .private_segment_fixed_size, the per-lane scratch a kernel
 reserves: a private array that the compiler cannot keep in registers (one
@@ -16,7 +16,7 @@ indexed by a loop that did not unroll) lands there without counting as a
 spill, and its scratch loads and stores can halve a memory-bound kernel's
 rate. Only the LayerNorm / RMSNorm kernels for 16-bit rows wider than 4096
 values (12 and 16 chunks per lane, no configured model's width) use any,
-besides those two RPB kernels' spill slots."""
+besides those kernels' spill slots."""
 import concurrent.futures as cf
 import os
 import re
@@ -32,6 +32,10 @@ HIPCC = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "bin", "hipcc")
 KNOWN_SPILLS: dict = {
     "_ZN3vfk14rpb_fwd_kernelINS_4BF16ELi1ELb0EEEvNS_7RpbArgsE": 2,
     "_ZN3vfk14rpb_fwd_kernelINS_4BF16ELi1ELb1EEEvNS_7RpbArgsE": 2,
+    "_ZN3vfk17varlen_fwd_kernelINS_4BF16ELb1ELb1ELb1EEEvNS_10VarlenArgsE": 1,
+    "_ZN3vfk17varlen_fwd_kernelINS_4BF16ELb0ELb1ELb1EEEvNS_10VarlenArgsE": 2,
+    "_ZN3vfk17varlen_fwd_kernelINS_3F16ELb1ELb1ELb1EEEvNS_10VarlenArgsE": 1,
+    "_ZN3vfk17varlen_fwd_kernelINS_3F16ELb0ELb1ELb1EEEvNS_10VarlenArgsE": 2,
 }
 # kernels allowed a private segment: norm_vec_kernel<16-bit dtype, lanes, 12 or 16 chunks, rms>
 KNOWN_PRIVATE = re.compile(r"_ZN3vfk15norm_vec_kernelILi[12]ELi(32|64)ELi(12|16)ELb[01]EEEvNS_8NormArgsE")

@@ -375,8 +375,9 @@ __device__ inline void varlen_item(const VarlenArgs& a, const VarlenLds<LOCAL>& 
 
   float m = -INFINITY;
   // row sums on the matrix core where the 8 extra registers fit (global
-  // layers); the sliding-window variants would spill
-  typename std::conditional<LOCAL, RowSumAdd, RowSumMfma<E>>::type l;
+  // layers); the sliding-window variants would spill and sum the same
+  // rounded weights by packed dots
+  typename std::conditional<LOCAL, RowSumDot<E>, RowSumMfma<E>>::type l;
   f32x16_t o0 = {}, o1 = {};
   const int ntiles = kt_end - kt_begin;
   if (ROPE) {
@@ -420,13 +421,13 @@ __device__ inline void varlen_item(const VarlenArgs& a, const VarlenLds<LOCAL>& 
                     [&](int r) { return wq_lo + r < n; });
 }
 
-// One workgroup per (sequence, head, query tile) work item. Four workgroups
-// per CU (128 VGPRs), except the sliding-window kernels with a key mask: at
-// 128 VGPRs they spill inside the tile loop, and three workgroups per CU
-// without spills run the 22-layer ModernBERT forward (14 such layers at
-// 163 736 tokens) 0.25 ms faster.
+// One workgroup per (sequence, head, query tile) work item, four workgroups
+// per CU (128 VGPRs). The sliding-window kernels with a key mask fit that
+// with their row sums as packed dots: 1 (RoPE) or 2 registers are spilled
+// outside the tile loops, and the 22-layer ModernBERT forward at 163 736
+// tokens runs 0.15 ms faster than at three workgroups per CU.
 template <typename E, bool ROPE, bool LOCAL, bool KVALID>
-__global__ __launch_bounds__(256, (LOCAL && KVALID) ? 3 : 4) void varlen_fwd_kernel(VarlenArgs a) {
+__global__ __launch_bounds__(256, 4) void varlen_fwd_kernel(VarlenArgs a) {
   __shared__ __align__(16) uint16_t K0[kTileElems];
   __shared__ __align__(16) uint16_t K1[kTileElems];
   __shared__ __align__(16) uint16_t V0[kTileElems];
