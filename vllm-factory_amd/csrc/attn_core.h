@@ -148,9 +148,10 @@ __device__ inline int x_key(int i, int h) {
   return kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
 }
 
-// Row sums of the softmax probabilities, two forms:
-//  * RowSumAdd: fp32 adds of the fp32 probabilities; each lane sums its 32
-//    keys and total() adds the partner lane's (l ^ 32) share.
+// Row sums of the softmax probabilities, two forms; both sum the 16-bit
+// probabilities P (the PV operand), so that the denominator is the sum of
+// exactly the rounded weights the numerator uses (fp32 sums of the unrounded
+// values would be off by the rounding of a row's dominant weight):
 //  * RowSumMfma: the 16-bit probabilities P (the PV operand) summed on the
 //    matrix core, which takes 31 adds per tile off the vector ALU and makes
 //    the denominator the sum of exactly the weights the numerator uses. The
@@ -160,34 +161,14 @@ __device__ inline int x_key(int i, int h) {
 //    A[m][k] = 1 when (k / 8) % 2 == m % 2, so row m of the product is the
 //    16-key sum of query n + 16 (m % 2). Lane l holds rows 4 (l / 16) .. +3:
 //    acc[0] = sum of query l % 16, acc[1] = sum of query l % 16 + 16.
-struct RowSumAdd {
-  float l = 0.f;
-  static constexpr bool kF32 = true;
-  __device__ void scale(float a) { l *= a; }
-  __device__ void add_f32(const f32x16_t& s0, const f32x16_t& s1) {
-    float la = s0[0] + s0[1], lb = s1[0] + s1[1];
-#pragma unroll
-    for (int i = 2; i < 16; ++i) {
-      la += s0[i];
-      lb += s1[i];
-    }
-    l += la + lb;
-  }
-  __device__ void add_p(const u32x4_t (&)[4]) {}
-  __device__ float total() const { return half_swap_sum(l); }
-};
-
-// RowSumDot: the 16-bit probabilities P summed by packed dot products with
-// (1, 1): 16 v_dot2 per tile instead of 31 adds, and, as with RowSumMfma,
-// the denominator sums exactly the rounded weights of the numerator (with
-// the fp32 sums a row dominated by one key whose weight rounds would be off
-// by that rounding). One register, like RowSumAdd.
+//  * RowSumDot: P summed by packed dot products with (1, 1), 16 v_dot2 per
+//    tile in one register, for kernels without the 8 registers RowSumMfma
+//    needs; each lane sums its 32 keys and total() adds the partner lane's
+//    (l ^ 32) share.
 template <typename E>
 struct RowSumDot {
   float l = 0.f;
-  static constexpr bool kF32 = false;
   __device__ void scale(float a) { l *= a; }
-  __device__ void add_f32(const f32x16_t&, const f32x16_t&) {}
   __device__ void add_p(const u32x4_t (&p)[4]) {
     float la = 0.f, lb = 0.f;
 #pragma unroll
@@ -205,9 +186,7 @@ struct RowSumDot {
 template <typename E>
 struct RowSumMfma {
   f32x4_t acc = {};
-  static constexpr bool kF32 = false;
   __device__ void scale(float a) { acc *= a; }
-  __device__ void add_f32(const f32x16_t&, const f32x16_t&) {}
   __device__ void add_p(const u32x4_t (&p)[4]) {
     const int l = threadIdx.x & 63;
     const uint32_t s = (((l >> 4) ^ l) & 1) ? 0u : E::kOnePair;
@@ -223,7 +202,7 @@ struct RowSumMfma {
 // masked), held in the two S^T accumulators s0 (keys 0..31) and s1 (32..63).
 // c = softmax scale * log2(e), so p = exp2(c * (x - m)) is one FMA and one
 // exp2 per score. m: running reference max in raw units; l: the row sum
-// (RowSumAdd / RowSumMfma). The step is split in two so that a pipelined loop
+// (RowSumDot / RowSumMfma). The step is split in two so that a pipelined loop
 // can place the parts apart: softmax_ref (row max, O rescale) and softmax_exp
 // (probabilities, row sum, 16-bit packing).
 
@@ -288,7 +267,6 @@ __device__ inline void softmax_exp(f32x16_t& s0, f32x16_t& s1, float c, float m,
       s1[i] = fast_exp2(__builtin_fmaf(s1[i], c, nmc));
     }
   }
-  l.add_f32(s0, s1);
   pack_p<E>(s0, s1, p);
   l.add_p(p);
 }
@@ -308,7 +286,6 @@ __device__ inline void softmax_fixed(f32x16_t& s0, f32x16_t& s1, u32x4_t (&p)[4]
     s0[i] = fast_exp2(s0[i] * c);
     s1[i] = fast_exp2(s1[i] * c);
   }
-  l.add_f32(s0, s1);
   pack_p<E>(s0, s1, p);
   l.add_p(p);
 }
